@@ -1,0 +1,208 @@
+/*
+ * spock_hip.h -- C ABI of the MI355X (gfx950) DeltaNet hot path.
+ *
+ * Drop-in replacement for the Vulkan dispatches of Alexintosh/spock's
+ * DecodeSession on three sub-paths: gated-DeltaNet chunk prefill, the fused
+ * DeltaNet recurrent decode step, and the fp16 decode GEMV / lm_head + argmax.
+ *
+ * Conventions (every entry point):
+ *   - returns SPK_OK (0) or a negative SPK_ERR_* code; no exception crosses the
+ *     ABI; spk_last_error() gives a message for the calling thread;
+ *   - all tensor pointers are caller-owned DEVICE memory (hipMalloc'd), plain
+ *     pointers plus sizes; fp16 tensors are passed as uint16_t bit patterns;
+ *   - calls are stream-ordered and asynchronous on `stream` (NULL = default
+ *     stream); nothing is allocated inside a call except where stated;
+ *   - re-entrant per stream: concurrent calls on different streams must not
+ *     share output or workspace buffers.
+ * Layouts and numerics follow the reference shaders cited per entry point
+ * (paths relative to the Alexintosh/spock checkout).
+ */
+#ifndef SPOCK_HIP_H
+#define SPOCK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* spk_stream_t; /* == hipStream_t */
+
+enum {
+  SPK_OK = 0,
+  SPK_ERR_NULL = -1,      /* a required pointer is NULL */
+  SPK_ERR_SHAPE = -2,     /* unsupported or inconsistent shape */
+  SPK_ERR_HIP = -3,       /* the HIP runtime reported an error */
+  SPK_ERR_ALIGN = -4,     /* a pointer or stride breaks the alignment contract */
+  SPK_ERR_ARG = -5        /* any other invalid argument */
+};
+
+enum { SPK_F32 = 0, SPK_F16 = 1 };
+
+/* Message for the last non-zero status returned on this thread. */
+const char* spk_last_error(void);
+/* ABI version: (major << 16) | minor. */
+uint32_t spk_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Gated-DeltaNet chunk prefill (WY/UT chunk rule).
+ *
+ * Replaces: run_deltanet_chunk_rule (src/runtime/deltanet_chunk.hpp:39-40,
+ * deltanet_chunk.cpp:53-284) and the tiled dispatch of
+ * shaders/deltanet_chunk_prefill_tiled.comp:53-273 issued by
+ * DecodeSession::gpu_chunk_prefill_from_gpu_collect (vk_session.cpp:4466-4828,
+ * dispatch at :4573) and gpu_chunk_prefill (:4192-4465).
+ *
+ * Inputs are head-major as the reference collects them
+ * (deltanet_prefill_collect.comp): q,k [H][N][dk], v [H][N][dv] (fp32 or fp16
+ * per `input_dtype`), g and beta fp32 [H][N].  With cu_seqlens == NULL there is
+ * one sequence of N tokens; otherwise sequence s owns tokens
+ * [cu_seqlens[s], cu_seqlens[s+1]) (device int32, num_seqs+1 entries, host
+ * copy in cu_seqlens_host) and is chunked from its own start and zero padded
+ * independently.  initial_state (nullable = zeros, which is what the tiled
+ * shader assumes, :66-71) and out_state are [num_seqs][H][dk][dv] fp32.
+ * out_core row (h, t) starts at out_core + (h*core_head_stride + t)*dv, so the
+ * reference's single output buffer [H*total_seq*dv | H*dk*dv] is addressed by
+ * core_head_stride = total_seq and out_state = out_core + H*total_seq*dv.
+ * Supported shape: dk == dv == 128, chunk_size == 64.
+ * workspace: device buffer of spk_chunk_prefill_workspace_size() bytes,
+ * 256-byte aligned, contents ignored.
+ * ---------------------------------------------------------------------- */
+typedef struct SpkChunkArgs {
+  int32_t num_heads;
+  int32_t total_tokens;      /* N: tokens of all sequences (sequence_length) */
+  int32_t key_dim;           /* 128 */
+  int32_t value_dim;         /* 128 */
+  int32_t chunk_size;        /* 64 */
+  int32_t use_qk_l2norm;     /* deltanet_chunk.cpp:78-85 */
+  float q_scale;             /* 0 => 1/sqrt(key_dim) (deltanet_chunk.cpp:87) */
+  int32_t input_dtype;       /* SPK_F32 or SPK_F16, for q/k/v */
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* g;
+  const float* beta;
+  const float* initial_state;
+  float* out_core;
+  int64_t core_head_stride;  /* tokens per head row block; 0 => total_tokens */
+  float* out_state;
+  const int32_t* cu_seqlens;       /* device, nullable */
+  const int32_t* cu_seqlens_host;  /* host, required when cu_seqlens != NULL */
+  int32_t num_seqs;                /* 1 when cu_seqlens == NULL */
+  void* workspace;
+  size_t workspace_bytes;
+} SpkChunkArgs;
+
+size_t spk_chunk_prefill_workspace_size(int32_t num_heads, int32_t total_tokens,
+                                        int32_t num_seqs, int32_t chunk_size);
+int spk_chunk_prefill(const SpkChunkArgs* args, spk_stream_t stream);
+
+/* Prefill collect for one token: shaders/deltanet_prefill_collect.comp:75-108
+ * (dispatch vk_session.cpp:1632-1670).  dn_qkv fp16 [Q H*dk | K H*dk | V H*dv],
+ * g_beta fp32 [g H | beta H]; outputs head-major fp32 with row stride seq_len. */
+int spk_prefill_collect(const uint16_t* dn_qkv, const float* g_beta, float* q_out,
+                        float* k_out, float* v_out, float* g_out, float* beta_out,
+                        int32_t num_heads, int32_t seq_len, int32_t token_idx,
+                        int32_t key_dim, int32_t value_dim, spk_stream_t stream);
+
+/* Last-token core_attn_out -> fp16 with the reference's truncating, flushing
+ * conversion: shaders/deltanet_chunk_last_to_fp16.comp:37-77 (dispatch
+ * vk_session.cpp:4628).  dst[h*dv+d] = trunc16(src[(h*total_seq+seq_len-1)*dv+d]). */
+int spk_chunk_last_to_fp16(const float* src, uint16_t* dst, int32_t num_heads,
+                           int32_t value_dim, int32_t seq_len, int32_t total_seq,
+                           spk_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * DeltaNet recurrent decode step, batched over B independent sequences.
+ *
+ * Per sequence the buffers are the reference's per-layer buffers
+ * (vk_session.cpp:350-371): qkv fp16 [Q H*128 | K H*128 | V H*128]
+ * (conv output written back; the gated output overwrites V), conv_state fp16
+ * channel-major [conv_dim][4], state fp32 [H][128][128] (+ optional g/beta
+ * tail, see spk_deltanet_recurrent), z fp16 [H*128], a and b fp16 [H].
+ * Shared: conv_weight fp16 [conv_dim][4], a_log_bias fp32 [layers][H][2] =
+ * (A_log, dt_bias) (vk_session.cpp:486-495), norm_weight fp32 [128].
+ * Strides are in elements between consecutive sequences.  H == 16 heads of
+ * key_dim == value_dim == 128 (conv_dim = 6144).  state must be 16-byte
+ * aligned with state_stride % 4 == 0.
+ * ---------------------------------------------------------------------- */
+typedef struct SpkDecodeArgs {
+  int32_t batch;
+  int32_t num_heads;        /* 16 */
+  int32_t layer_idx;        /* row of a_log_bias */
+  float q_scale;            /* 0 => 1/sqrt(128) */
+  float rms_eps;            /* 0 => 1e-6 */
+  uint16_t* qkv;            int64_t qkv_stride;
+  uint16_t* conv_state;     int64_t conv_state_stride;
+  const uint16_t* conv_weight;
+  const uint16_t* a;
+  const uint16_t* b;        int64_t ab_stride;
+  const float* a_log_bias;
+  float* state;             int64_t state_stride;
+  const uint16_t* z;        int64_t z_stride;
+  const float* norm_weight;
+} SpkDecodeArgs;
+
+/* Fused: deltanet_conv_l2_qk.comp:41-111 followed by
+ * deltanet_recurrent_gbeta_norm_gate.comp:91-225 (dispatches
+ * vk_session.cpp:2876-2884 and :3212-3219), one kernel, state read once. */
+int spk_deltanet_decode_step(const SpkDecodeArgs* args, spk_stream_t stream);
+/* deltanet_conv_l2_qk.comp alone (uses qkv, conv_state, conv_weight). */
+int spk_deltanet_conv_l2_qk(const SpkDecodeArgs* args, spk_stream_t stream);
+/* deltanet_recurrent_gbeta_norm_gate.comp alone (qkv already convolved). */
+int spk_deltanet_recurrent_gbeta_norm_gate(const SpkDecodeArgs* args, spk_stream_t stream);
+/* Unfused deltanet_recurrent.comp (prefill path vk_session.cpp:1717-1742):
+ * g and beta are read from the state tail state[H*128*128 + h] and
+ * state[H*128*128 + H + h]; the raw output is rounded to fp16 into V.
+ * Uses qkv, state (stride must include the tail) and q_scale. */
+int spk_deltanet_recurrent(const SpkDecodeArgs* args, spk_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * fp16 decode GEMV, lm_head and argmax.
+ * ---------------------------------------------------------------------- */
+
+/* y[r] = fp16(sum_j W[r][j] x[j]), fp32 accumulation.  Replaces matvec.comp:28-41
+ * and matvec_tiled.comp:41-84 (bind/dispatch vk_session.cpp:2247-2256); the
+ * summation order is lm_head_tiled.comp's (64 lanes x contiguous spans, then a
+ * 32..1 tree).  W row-major [out_dim][in_dim]; in_dim % 64 == 0. */
+int spk_matvec_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, int32_t out_dim,
+                   int32_t in_dim, spk_stream_t stream);
+
+/* Several independent GEMVs in one launch (the decode projections). */
+typedef struct SpkMatvecDesc {
+  const uint16_t* W;
+  const uint16_t* x;
+  uint16_t* y;
+  int32_t out_dim;
+  int32_t in_dim;
+} SpkMatvecDesc;
+int spk_matvec_f16_batched(const SpkMatvecDesc* descs, int32_t count, spk_stream_t stream);
+
+/* argmax over fp16 values with argmax.comp:27-63's exact tie rule (256 lanes
+ * over contiguous blocks, first strict maximum per lane, strictly-greater tree;
+ * NaN and -inf never win; all-invalid gives 0).  Dispatch vk_session.cpp:3558-3563. */
+int spk_argmax_f16(const uint16_t* vals, int32_t n, uint32_t* out_index, spk_stream_t stream);
+
+/* Tied lm_head (lm_head_tiled.comp:40-87, dispatch vk_session.cpp:3533-3547)
+ * fused with argmax (same tie rule as spk_argmax_f16 over the fp16 logits).
+ * logits (nullable) receives the fp16 logits.  workspace: device buffer of
+ * spk_lm_head_workspace_size(vocab) bytes, contents ignored. */
+size_t spk_lm_head_workspace_size(int32_t vocab);
+int spk_lm_head_argmax(const uint16_t* W, const uint16_t* x, int32_t vocab, int32_t hidden,
+                       uint16_t* logits, uint32_t* out_index, void* workspace,
+                       size_t workspace_bytes, spk_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Diagnostics (no reference counterpart).
+ * ---------------------------------------------------------------------- */
+
+/* Evaluates the device scalar numerics used by the bit-exact kernels on x[n]
+ * and writes six planes of n floats to out: exp, log, 1/sqrt, SiLU,
+ * float(half_rne(x)), and the bits of the truncating half in the low 16 bits. */
+int spk_selftest_numerics(const float* x, int32_t n, float* out, spk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

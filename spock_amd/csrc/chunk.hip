@@ -1,0 +1,642 @@
+// chunk.hip -- gated-DeltaNet chunk prefill (WY/UT chunk rule) on fp32 MFMA.
+//
+// Math (deltanet_chunk.cpp:134-268, deltanet_chunk_prefill_tiled.comp:116-262):
+// per (sequence, head) and chunk of C=64 tokens with cumulative log-decay
+// gcum and Gamma_ij = exp(gcum_i - gcum_j):
+//   L  = strict_lower(beta_i (k_i . k_j) Gamma_ij),   T = (I + L)^{-1}
+//   U  = T (V * beta),   W = T (K * beta * e^gcum)
+//   A  = lower(q_i . k_j * scale * Gamma_ij)
+//   v_new = U - W S,  o = (Q scale e^gcum) S + A v_new,
+//   S <- e^{gcum_last} S + (K e^{gcum_last - gcum})^T v_new.
+//
+// Two launches:
+//  1. chunk_intra_kernel -- one workgroup per (chunk, head), all chunks of all
+//     sequences in parallel.  K/Q/V of the chunk are staged in LDS; K K^T and
+//     Q K^T are 16x16x4 fp32 MFMA tiles; T is inverted blockwise (4 diagonal
+//     16x16 blocks by per-lane forward substitution in registers, off-diagonal
+//     blocks T_IJ = -T_II sum_M L_IM T_MJ as MFMA products); U and W are MFMA
+//     products skipping the zero upper blocks of T.  U, W, A and per-token
+//     scales go to the workspace.
+//  2. chunk_state_kernel -- one workgroup per (sequence, head, 32-column tile
+//     of the value dim): columns of S evolve independently, so the sequential
+//     chunk scan runs on 4*H*num_seqs workgroups.  The 128x32 state tile lives
+//     in LDS; each wavefront owns 32 rows of [W; Q e^g] S, of the output and of
+//     the state update, all 16x16x4 MFMA.
+// MFMA operand trick: the contraction index of a 16x16x4 step is a free
+// permutation, so lane (m = l%16, g = l/16) reads a float4 at k = 16u + 4g and
+// feeds its elements to 4 consecutive steps; the B operand uses the same map.
+#include "capi_common.hpp"
+#include "numerics.hpp"
+
+namespace {
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kC = 64;
+constexpr int kD = 128;
+constexpr int kLDK = 132;  // LDS row stride (floats) of [64][128] tiles
+constexpr int kLDT = 68;   // LDS row stride of [64][64] tiles
+constexpr int kLDS2 = 33;  // LDS row stride of the 32-column state / v_new tiles
+// workspace record per (chunk, head), in floats
+constexpr int kWsU = 0;
+constexpr int kWsW = 8192;
+constexpr int kWsA = 16384;
+constexpr int kWsQs = 20480;
+constexpr int kWsKs = 20544;
+constexpr int kWsMisc = 20608;
+constexpr int kWsStride = 20672;  // 82688 bytes, a multiple of 256
+
+__device__ __forceinline__ f4v mfma4(float a, float b, f4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+struct ChunkParams {
+  int H;
+  int N;
+  int S;
+  int l2;
+  float q_scale;
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* g;
+  const float* beta;
+  const float* init;
+  float* core;
+  long long core_hs;
+  float* state;
+  const int* cu;
+  float* ws;
+};
+
+__device__ __forceinline__ float4 load4(const float* p, size_t i) {
+  return *reinterpret_cast<const float4*>(p + i);
+}
+__device__ __forceinline__ float4 load4(const uint16_t* p, size_t i) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p + i);
+  return make_float4(spk::h2f((uint16_t)(u.x & 0xffffu)), spk::h2f((uint16_t)(u.x >> 16)),
+                     spk::h2f((uint16_t)(u.y & 0xffffu)), spk::h2f((uint16_t)(u.y >> 16)));
+}
+__device__ __forceinline__ float load1(const float* p, size_t i) { return p[i]; }
+__device__ __forceinline__ float load1(const uint16_t* p, size_t i) { return spk::h2f(p[i]); }
+
+__device__ __forceinline__ float elem(const float4& v, int e) {
+  return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+
+// Global chunk id -> (sequence, chunk within it, first token, valid tokens).
+__device__ __forceinline__ void locate_chunk(const ChunkParams& p, int gchunk, int& seq,
+                                             int& t0, int& len) {
+  if (p.cu == nullptr) {
+    seq = 0;
+    t0 = gchunk * kC;
+    len = min(kC, p.N - t0);
+    return;
+  }
+  int acc = 0;
+  for (int s = 0; s < p.S; ++s) {
+    const int L = p.cu[s + 1] - p.cu[s];
+    const int n = (L + kC - 1) / kC;
+    if (gchunk < acc + n) {
+      const int c = gchunk - acc;
+      seq = s;
+      t0 = p.cu[s] + c * kC;
+      len = min(kC, L - c * kC);
+      return;
+    }
+    acc += n;
+  }
+  seq = -1;
+  t0 = 0;
+  len = 0;
+}
+
+constexpr int kIntraSmemFloats = 3 * 64 * kLDK + 2 * 64 * kLDT + 4 * 16 * 17 + 4 * 64;
+
+template <typename TIn>
+__global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
+  __shared__ float smem[kIntraSmemFloats];
+  float* sK = smem;              // [64][kLDK] K (L2-normalised if requested)
+  float* sQ = sK + 64 * kLDK;    // [64][kLDK] Q, later K * beta * e^gcum
+  float* sV = sQ + 64 * kLDK;    // [64][kLDK] V, later V * beta
+  float* sL = sV + 64 * kLDK;    // [64][kLDT] L
+  float* sT = sL + 64 * kLDT;    // [64][kLDT] T = (I + L)^-1
+  float* sX = sT + 64 * kLDT;    // [4][16][17] per-wave product scratch
+  float* sG = sX + 4 * 16 * 17;  // [64] gcum
+  float* sB = sG + 64;           // [64] beta
+  float* sIQ = sB + 64;          // [64] 1/|q| (or 1), later beta*e^gcum
+  float* sIK = sIQ + 64;         // [64] 1/|k| (or 1)
+
+  const int gchunk = blockIdx.x;
+  const int h = blockIdx.y;
+  int seq, t0, len;
+  locate_chunk(p, gchunk, seq, t0, len);
+  if (seq < 0) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const TIn* q = static_cast<const TIn*>(p.q);
+  const TIn* k = static_cast<const TIn*>(p.k);
+  const TIn* v = static_cast<const TIn*>(p.v);
+  float* ws = p.ws + ((size_t)gchunk * p.H + h) * kWsStride;
+
+  // ---- stage chunk rows; padding rows (t >= len) are zero, g = beta = 0
+  for (int i = tid; i < 64 * 32; i += 256) {
+    const int r = i >> 5;
+    const int c = (i & 31) * 4;
+    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), kv = qv, vv = qv;
+    if (r < len) {
+      const size_t off = ((size_t)h * p.N + t0 + r) * kD + c;
+      qv = load4(q, off);
+      kv = load4(k, off);
+      vv = load4(v, off);
+    }
+    *reinterpret_cast<float4*>(&sQ[r * kLDK + c]) = qv;
+    *reinterpret_cast<float4*>(&sK[r * kLDK + c]) = kv;
+    *reinterpret_cast<float4*>(&sV[r * kLDK + c]) = vv;
+  }
+  if (tid < 64) {
+    const bool valid = tid < len;
+    sG[tid] = valid ? p.g[(size_t)h * p.N + t0 + tid] : 0.0f;
+    sB[tid] = valid ? p.beta[(size_t)h * p.N + t0 + tid] : 0.0f;
+  }
+  for (int i = tid; i < 64 * kLDT; i += 256) {
+    sL[i] = 0.0f;
+    sT[i] = 0.0f;
+  }
+  __syncthreads();
+  if (tid == 0) {  // running cumulative sum (deltanet_chunk.cpp:137-142)
+    float run = 0.0f;
+    for (int r = 0; r < 64; ++r) {
+      run = run + sG[r];
+      sG[r] = run;
+    }
+  }
+  if (p.l2) {  // deltanet_chunk.cpp:27-39, eps inside the sqrt
+    if (tid < 128) {
+      const int r = tid & 63;
+      const float* row = (tid < 64 ? sQ : sK) + r * kLDK;
+      float ss = 0.0f;
+      for (int d = 0; d < kD; ++d) ss = ss + row[d] * row[d];
+      (tid < 64 ? sIQ : sIK)[r] = 1.0f / sqrtf(ss + 1e-6f);
+    }
+  } else if (tid < 64) {
+    sIQ[tid] = 1.0f;
+    sIK[tid] = 1.0f;
+  }
+  __syncthreads();
+  if (p.l2) {
+    for (int i = tid; i < 64 * kD; i += 256) {
+      const int r = i >> 7;
+      const int c = i & 127;
+      sQ[r * kLDK + c] *= sIQ[r];
+      sK[r * kLDK + c] *= sIK[r];
+    }
+  }
+  const float gL = sG[63];
+  if (tid < 64) {
+    ws[kWsQs + tid] = (sIQ[tid] * p.q_scale) * expf(sG[tid]);
+    ws[kWsKs + tid] = sIK[tid] * expf(gL - sG[tid]);
+  }
+  if (tid == 0) ws[kWsMisc] = expf(gL);
+  __syncthreads();
+
+  // ---- K K^T -> L (into LDS) and Q K^T -> A (into the workspace); 20 tiles
+  for (int tt = wave; tt < 20; tt += 4) {
+    const bool isq = tt >= 10;
+    const int t = isq ? tt - 10 : tt;
+    const int I = t >= 6 ? 3 : t >= 3 ? 2 : t >= 1 ? 1 : 0;
+    const int J = t - I * (I + 1) / 2;
+    const float* A = isq ? sQ : sK;
+    f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float4 a4 = *reinterpret_cast<const float4*>(&A[(16 * I + li) * kLDK + 16 * u + 4 * lg]);
+      const float4 b4 = *reinterpret_cast<const float4*>(&sK[(16 * J + li) * kLDK + 16 * u + 4 * lg]);
+      acc = mfma4(a4.x, b4.x, acc);
+      acc = mfma4(a4.y, b4.y, acc);
+      acc = mfma4(a4.z, b4.z, acc);
+      acc = mfma4(a4.w, b4.w, acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * I + 4 * lg + r;
+      const int j = 16 * J + li;
+      if (!isq) {
+        if (j < i) sL[i * kLDT + j] = sB[i] * acc[r] * expf(sG[i] - sG[j]);
+      } else {
+        ws[kWsA + i * 64 + j] = (j <= i) ? acc[r] * p.q_scale * expf(sG[i] - sG[j]) : 0.0f;
+      }
+    }
+  }
+  for (int e = tid; e < 64 * 64; e += 256) {  // strictly-upper blocks of A are zero
+    const int i = e >> 6;
+    const int j = e & 63;
+    if ((j >> 4) > (i >> 4)) ws[kWsA + e] = 0.0f;
+  }
+  __syncthreads();
+
+  // ---- B operands of U and W: V*beta in place, Q slot <- K*beta*e^gcum
+  if (tid < 64) sIQ[tid] = sB[tid] * expf(sG[tid]);
+  __syncthreads();
+  for (int i = tid; i < 64 * kD; i += 256) {
+    const int r = i >> 7;
+    const int c = i & 127;
+    sV[r * kLDK + c] = sV[r * kLDK + c] * sB[r];
+    sQ[r * kLDK + c] = sK[r * kLDK + c] * sIQ[r];
+  }
+
+  // ---- diagonal 16x16 blocks of T: lane j < 16 of wave w solves column j of
+  // block w in registers, T_ij = -sum_{m<i} L_im T_mj (T_mj = 0 for m < j).
+  if (li == lane) {
+    const int b0 = 16 * wave;
+    const int j = lane;
+    float tc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s = 0.0f;
+#pragma unroll
+      for (int m = 0; m < i; ++m) s = __builtin_fmaf(sL[(b0 + i) * kLDT + b0 + m], tc[m], s);
+      tc[i] = (i == j) ? 1.0f : (i < j ? 0.0f : -s);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sT[(b0 + i) * kLDT + b0 + j] = tc[i];
+  }
+  __syncthreads();
+
+  // ---- off-diagonal blocks, by distance d = I - J
+  for (int d = 1; d < 4; ++d) {
+    const bool active = wave < 4 - d;
+    const int J = wave;
+    const int I = J + d;
+    if (active) {
+      f4v acc = {0.f, 0.f, 0.f, 0.f};
+      for (int M = J; M < I; ++M) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const float a = sL[(16 * I + li) * kLDT + 16 * M + 4 * s + lg];
+          const float b = sT[(16 * M + 4 * s + lg) * kLDT + 16 * J + li];
+          acc = mfma4(a, b, acc);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sX[wave * 272 + (4 * lg + r) * 17 + li] = acc[r];
+    }
+    __syncthreads();
+    if (active) {
+      f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float a = sT[(16 * I + li) * kLDT + 16 * I + 4 * s + lg];
+        const float b = sX[wave * 272 + (4 * s + lg) * 17 + li];
+        acc = mfma4(a, b, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sT[(16 * I + 4 * lg + r) * kLDT + 16 * J + li] = -acc[r];
+    }
+    __syncthreads();
+  }
+
+  // ---- U = T (V*beta), W = T (K*beta*e^g); wave w owns column tiles 2w, 2w+1
+  for (int mat = 0; mat < 2; ++mat) {
+    const float* Bm = mat == 0 ? sV : sQ;
+    float* out = ws + (mat == 0 ? kWsU : kWsW);
+    for (int jj = 0; jj < 2; ++jj) {
+      const int J = 2 * wave + jj;
+      for (int I = 0; I < 4; ++I) {
+        f4v acc = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < 4 * (I + 1); ++s) {
+          const float a = sT[(16 * I + li) * kLDT + 4 * s + lg];
+          const float b = Bm[(4 * s + lg) * kLDK + 16 * J + li];
+          acc = mfma4(a, b, acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) out[(16 * I + 4 * lg + r) * kD + 16 * J + li] = acc[r];
+      }
+    }
+  }
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(256) void chunk_state_kernel(ChunkParams p) {
+  __shared__ float sS[128 * kLDS2];
+  __shared__ float sVn[64 * kLDS2];
+
+  // Workgroup -> (column tile, head, sequence).  Consecutive logical ids share
+  // (sequence, head) and are placed on one XCD (workgroups are dealt to the 8
+  // XCDs round-robin) so the four tiles reading the same W/Q/K/A hit one L2.
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  const int tile = bid & 3;
+  const int h = (bid >> 2) % p.H;
+  const int seq = (bid >> 2) / p.H;
+  const int n0 = tile * 32;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const TIn* q = static_cast<const TIn*>(p.q);
+  const TIn* k = static_cast<const TIn*>(p.k);
+
+  int t_begin = 0, L = p.N, co = 0;
+  if (p.cu) {
+    t_begin = p.cu[seq];
+    L = p.cu[seq + 1] - t_begin;
+    for (int s = 0; s < seq; ++s) co += (p.cu[s + 1] - p.cu[s] + kC - 1) / kC;
+  }
+  const int nchunks = (L + kC - 1) / kC;
+
+  const float* init = p.init ? p.init + ((size_t)seq * p.H + h) * kD * kD : nullptr;
+  for (int i = tid; i < 128 * 32; i += 256) {
+    const int r = i >> 5;
+    const int c = i & 31;
+    sS[r * kLDS2 + c] = init ? init[r * kD + n0 + c] : 0.0f;
+  }
+  __syncthreads();
+
+  for (int c = 0; c < nchunks; ++c) {
+    const int gchunk = co + c;
+    const int tok0 = t_begin + c * kC;
+    const int len = min(kC, L - c * kC);
+    const float* ws = p.ws + ((size_t)gchunk * p.H + h) * kWsStride;
+
+    // ---- stage A: P = [W ; Q*qs] S, wave w rows 32w..32w+31
+    f4v acc[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
+    const bool wrows = wave < 2;
+#pragma unroll 2
+    for (int u = 0; u < 8; ++u) {
+      float4 a4[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int row = 32 * wave + 16 * mt + li;
+        if (wrows) {
+          a4[mt] = load4(ws + kWsW, (size_t)row * kD + 16 * u + 4 * lg);
+        } else {
+          const int tok = row - 64;
+          if (tok < len) {
+            const float sc = ws[kWsQs + tok];
+            float4 x = load4(q, ((size_t)h * p.N + tok0 + tok) * kD + 16 * u + 4 * lg);
+            a4[mt] = make_float4(x.x * sc, x.y * sc, x.z * sc, x.w * sc);
+          } else {
+            a4[mt] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kr = 16 * u + 4 * lg + e;
+        const float b0 = sS[kr * kLDS2 + li];
+        const float b1 = sS[kr * kLDS2 + 16 + li];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const float a = elem(a4[mt], e);
+          acc[mt][0] = mfma4(a, b0, acc[mt][0]);
+          acc[mt][1] = mfma4(a, b1, acc[mt][1]);
+        }
+      }
+    }
+
+    // ---- stage B: v_new = U - W S (waves 0, 1)
+    if (wrows) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = 32 * wave + 16 * mt + 4 * lg + r;
+            const int n = 16 * nt + li;
+            sVn[tok * kLDS2 + n] = ws[kWsU + tok * kD + n0 + n] - acc[mt][nt][r];
+          }
+    }
+    __syncthreads();
+
+    // ---- stage C: o = Q*qs S + A v_new (waves 2, 3: tokens 32(w-2)..+31)
+    if (!wrows) {
+      const int tb = 32 * (wave - 2);
+      const int nu = (wave == 2) ? 2 : 4;
+      for (int u = 0; u < nu; ++u) {
+        float4 a4[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          a4[mt] = load4(ws + kWsA, (size_t)(tb + 16 * mt + li) * 64 + 16 * u + 4 * lg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int kt = 16 * u + 4 * lg + e;
+          const float b0 = sVn[kt * kLDS2 + li];
+          const float b1 = sVn[kt * kLDS2 + 16 + li];
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) {
+            const float a = elem(a4[mt], e);
+            acc[mt][0] = mfma4(a, b0, acc[mt][0]);
+            acc[mt][1] = mfma4(a, b1, acc[mt][1]);
+          }
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = tb + 16 * mt + 4 * lg + r;
+            if (tok < len)
+              p.core[((size_t)h * p.core_hs + tok0 + tok) * kD + n0 + 16 * nt + li] = acc[mt][nt][r];
+          }
+    }
+
+    // ---- stage D: S <- e^{gL} S + (K*ks)^T v_new, wave w rows 32w..32w+31
+    const float gle = ws[kWsMisc];
+    f4v sacc[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sacc[mt][nt][r] = sS[(32 * wave + 16 * mt + 4 * lg + r) * kLDS2 + 16 * nt + li] * gle;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float a[2][4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 16 * u + 4 * lg + e;
+        const float ks = t < len ? ws[kWsKs + t] : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          a[mt][e] = t < len ? load1(k, ((size_t)h * p.N + tok0 + t) * kD + 32 * wave + 16 * mt + li) * ks
+                             : 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 16 * u + 4 * lg + e;
+        const float b0 = sVn[t * kLDS2 + li];
+        const float b1 = sVn[t * kLDS2 + 16 + li];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          sacc[mt][0] = mfma4(a[mt][e], b0, sacc[mt][0]);
+          sacc[mt][1] = mfma4(a[mt][e], b1, sacc[mt][1]);
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sS[(32 * wave + 16 * mt + 4 * lg + r) * kLDS2 + 16 * nt + li] = sacc[mt][nt][r];
+    __syncthreads();
+  }
+
+  float* out = p.state + ((size_t)seq * p.H + h) * kD * kD;
+  for (int i = tid; i < 128 * 32; i += 256) {
+    const int r = i >> 5;
+    const int c = i & 31;
+    out[r * kD + n0 + c] = sS[r * kLDS2 + c];
+  }
+}
+
+__global__ void prefill_collect_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ gb,
+                                       float* qo, float* ko, float* vo, float* go, float* bo, int H,
+                                       int T, int tok, int dk, int dv) {
+  const int h = blockIdx.x;
+  const int lid = threadIdx.x;
+  if (lid < dk) {
+    qo[((size_t)h * T + tok) * dk + lid] = spk::h2f(qkv[h * dk + lid]);
+    ko[((size_t)h * T + tok) * dk + lid] = spk::h2f(qkv[H * dk + h * dk + lid]);
+  }
+  if (lid < dv) vo[((size_t)h * T + tok) * dv + lid] = spk::h2f(qkv[2 * H * dk + h * dv + lid]);
+  if (lid == 0) {
+    go[(size_t)h * T + tok] = gb[h];
+    bo[(size_t)h * T + tok] = gb[H + h];
+  }
+}
+
+__global__ void last_to_fp16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst, int H,
+                                    int dv, int T, int total) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= H * dv) return;
+  const int h = idx / dv;
+  const int d = idx - h * dv;
+  dst[idx] = spk::f2h_trunc(src[((size_t)h * total + (T - 1)) * dv + d]);
+}
+
+size_t ws_bytes_for(int H, long long chunks) { return (size_t)chunks * H * kWsStride * sizeof(float); }
+
+}  // namespace
+
+extern "C" size_t spk_chunk_prefill_workspace_size(int32_t num_heads, int32_t total_tokens,
+                                                   int32_t num_seqs, int32_t chunk_size) {
+  if (num_heads <= 0 || total_tokens < 0 || num_seqs <= 0 || chunk_size != kC) return 0;
+  const long long bound = (total_tokens + kC - 1) / kC + num_seqs;
+  return ws_bytes_for(num_heads, bound);
+}
+
+extern "C" int spk_chunk_prefill(const SpkChunkArgs* a, spk_stream_t stream) {
+  if (!a) return spk::fail(SPK_ERR_NULL, "spk_chunk_prefill: args is NULL");
+  if (a->key_dim != kD || a->value_dim != kD || a->chunk_size != kC)
+    return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill: need key_dim == value_dim == 128 and chunk_size == 64 (got %d, %d, %d)",
+                     a->key_dim, a->value_dim, a->chunk_size);
+  if (a->num_heads <= 0 || a->total_tokens < 0)
+    return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill: num_heads %d total_tokens %d", a->num_heads, a->total_tokens);
+  if (a->input_dtype != SPK_F32 && a->input_dtype != SPK_F16)
+    return spk::fail(SPK_ERR_ARG, "spk_chunk_prefill: input_dtype %d", a->input_dtype);
+  const int S = a->cu_seqlens ? a->num_seqs : 1;
+  if (S <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill: num_seqs %d", a->num_seqs);
+  if (!a->out_state || !a->workspace) return spk::fail(SPK_ERR_NULL, "spk_chunk_prefill: out_state/workspace NULL");
+  if (a->total_tokens > 0 && (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->out_core))
+    return spk::fail(SPK_ERR_NULL, "spk_chunk_prefill: q/k/v/g/beta/out_core NULL");
+  long long chunks = 0;
+  if (a->cu_seqlens) {
+    if (!a->cu_seqlens_host) return spk::fail(SPK_ERR_NULL, "spk_chunk_prefill: cu_seqlens_host is required with cu_seqlens");
+    const int32_t* cu = a->cu_seqlens_host;
+    if (cu[0] != 0 || cu[S] != a->total_tokens)
+      return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill: cu_seqlens must start at 0 and end at total_tokens");
+    for (int s = 0; s < S; ++s) {
+      if (cu[s + 1] < cu[s]) return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill: cu_seqlens not monotonic at %d", s);
+      chunks += (cu[s + 1] - cu[s] + kC - 1) / kC;
+    }
+  } else {
+    chunks = (a->total_tokens + kC - 1) / kC;
+  }
+  const size_t need = ws_bytes_for(a->num_heads, chunks);
+  if (a->workspace_bytes < need)
+    return spk::fail(SPK_ERR_ARG, "spk_chunk_prefill: workspace %zu < %zu bytes", a->workspace_bytes, need);
+  const size_t vec = a->input_dtype == SPK_F32 ? 16 : 8;
+  if (!spk::aligned(a->q, vec) || !spk::aligned(a->k, vec) || !spk::aligned(a->v, vec) ||
+      !spk::aligned(a->workspace, 16) || !spk::aligned(a->out_state, 4) || !spk::aligned(a->out_core, 4))
+    return spk::fail(SPK_ERR_ALIGN, "spk_chunk_prefill: q/k/v must be %zu-byte aligned, workspace 16-byte", vec);
+  const long long hs = a->core_head_stride ? a->core_head_stride : a->total_tokens;
+  if (hs < a->total_tokens) return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill: core_head_stride < total_tokens");
+
+  ChunkParams p;
+  p.H = a->num_heads;
+  p.N = a->total_tokens;
+  p.S = S;
+  p.l2 = a->use_qk_l2norm ? 1 : 0;
+  p.q_scale = a->q_scale != 0.0f ? a->q_scale : 1.0f / sqrtf((float)kD);
+  p.q = a->q;
+  p.k = a->k;
+  p.v = a->v;
+  p.g = a->g;
+  p.beta = a->beta;
+  p.init = a->initial_state;
+  p.core = a->out_core;
+  p.core_hs = hs;
+  p.state = a->out_state;
+  p.cu = a->cu_seqlens;
+  p.ws = static_cast<float*>(a->workspace);
+  hipStream_t s = spk::to_hip(stream);
+  if (chunks > 0) {
+    dim3 g1((unsigned)chunks, (unsigned)p.H);
+    if (a->input_dtype == SPK_F32)
+      hipLaunchKernelGGL(chunk_intra_kernel<float>, g1, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(chunk_intra_kernel<uint16_t>, g1, dim3(256), 0, s, p);
+    const int rc = spk::check_launch("spk_chunk_prefill (intra)");
+    if (rc) return rc;
+  }
+  dim3 g2((unsigned)(4 * p.H * S));
+  if (a->input_dtype == SPK_F32)
+    hipLaunchKernelGGL(chunk_state_kernel<float>, g2, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(chunk_state_kernel<uint16_t>, g2, dim3(256), 0, s, p);
+  return spk::check_launch("spk_chunk_prefill (state)");
+}
+
+extern "C" int spk_prefill_collect(const uint16_t* dn_qkv, const float* g_beta, float* q_out,
+                                   float* k_out, float* v_out, float* g_out, float* beta_out,
+                                   int32_t num_heads, int32_t seq_len, int32_t token_idx,
+                                   int32_t key_dim, int32_t value_dim, spk_stream_t stream) {
+  if (!dn_qkv || !g_beta || !q_out || !k_out || !v_out || !g_out || !beta_out)
+    return spk::fail(SPK_ERR_NULL, "spk_prefill_collect: NULL pointer");
+  if (num_heads <= 0 || seq_len <= 0 || token_idx < 0 || token_idx >= seq_len || key_dim <= 0 ||
+      value_dim <= 0 || key_dim > 1024 || value_dim > 1024)
+    return spk::fail(SPK_ERR_SHAPE, "spk_prefill_collect: bad shape");
+  const int threads = ((key_dim > value_dim ? key_dim : value_dim) + 63) / 64 * 64;
+  hipLaunchKernelGGL(prefill_collect_kernel, dim3(num_heads), dim3(threads), 0, spk::to_hip(stream), dn_qkv,
+                     g_beta, q_out, k_out, v_out, g_out, beta_out, num_heads, seq_len, token_idx,
+                     key_dim, value_dim);
+  return spk::check_launch("spk_prefill_collect");
+}
+
+extern "C" int spk_chunk_last_to_fp16(const float* src, uint16_t* dst, int32_t num_heads,
+                                      int32_t value_dim, int32_t seq_len, int32_t total_seq,
+                                      spk_stream_t stream) {
+  if (!src || !dst) return spk::fail(SPK_ERR_NULL, "spk_chunk_last_to_fp16: NULL pointer");
+  if (num_heads <= 0 || value_dim <= 0 || seq_len <= 0 || total_seq < seq_len)
+    return spk::fail(SPK_ERR_SHAPE, "spk_chunk_last_to_fp16: bad shape");
+  const int n = num_heads * value_dim;
+  hipLaunchKernelGGL(last_to_fp16_kernel, dim3((n + 63) / 64), dim3(64), 0, spk::to_hip(stream), src, dst,
+                     num_heads, value_dim, seq_len, total_seq);
+  return spk::check_launch("spk_chunk_last_to_fp16");
+}

@@ -1,0 +1,313 @@
+// decode.hip -- DeltaNet recurrent decode step for B independent sequences.
+//
+// One workgroup (256 lanes, 4 wavefronts) per (head, sequence).  The fused
+// variant performs, in one launch and with one read and one write of the
+// head's 64 KiB fp32 state:
+//   deltanet_conv_l2_qk.comp:41-111              conv-state shift, depthwise
+//       conv (k=4) + SiLU, fp16 store, L2 of the Q and K head blocks;
+//   deltanet_recurrent_gbeta_norm_gate.comp:91-225  g/beta, decay, kv=S^T k,
+//       delta, rank-1 update, o=S^T q, RMSNorm, fp16(w*n)*SiLU(z).
+// The state stream is the cost (2 x 64 KiB per head): each lane owns a 16-row
+// x 4-column slice loaded as 16 float4 (global_load_dwordx4, row segments of
+// 512 B per 32 lanes), issued before the conv work so the HBM latency overlaps.
+//
+// Reduction orders (fixed, and restated by the CPU oracle):
+//   conv taps summed i = 0..3; L2 / RMS sums use the shaders' 128-wide tree
+//   (s[l] += s[l+64], then 32..1: lane-local add, then wave shuffles);
+//   S^T x per column: 8 row groups of 16 rows, fma-accumulated from 0 in row
+//   order, combined ((p0+p1)+(p2+p3))+((p4+p5)+(p6+p7)).
+#include "capi_common.hpp"
+#include "numerics.hpp"
+
+namespace {
+
+struct DecodeParams {
+  int nh;
+  int layer;
+  float q_scale;
+  float eps;
+  uint16_t* qkv;
+  long long qkv_stride;
+  uint16_t* conv_state;
+  long long conv_stride;
+  const uint16_t* conv_w;
+  const uint16_t* a;
+  const uint16_t* b;
+  long long ab_stride;
+  const float* alb;
+  float* state;
+  long long state_stride;
+  const uint16_t* z;
+  long long z_stride;
+  const float* norm_w;
+};
+
+__device__ __forceinline__ float tree8(const float* p) {
+  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
+
+// CONV: run the conv/L2 phase.  REC: run the recurrence.  GB_TAIL: g/beta from
+// the state tail (deltanet_recurrent.comp) instead of a/b/A_log/dt_bias.
+// NORM_GATE: RMSNorm-gate the output (else fp16 of the raw output).
+template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE>
+__global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
+  const int h = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nh = p.nh;
+  uint16_t* qkv = p.qkv + (long long)seq * p.qkv_stride;
+
+  __shared__ float s_q[128], s_k[128], s_v[128], s_delta[128];
+  __shared__ float s_part[8][128];
+
+  const int c4 = tid & 31;  // owns columns 4*c4 .. 4*c4+3
+  const int rg = tid >> 5;  // owns rows 16*rg .. 16*rg+15
+  float4 S[16];
+  float* st_head = nullptr;
+  if (REC) {
+    float* st_seq = p.state + (long long)seq * p.state_stride;
+    st_head = st_seq + (long long)h * 128 * 128;
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+      S[m] = *reinterpret_cast<const float4*>(st_head + (rg * 16 + m) * 128 + c4 * 4);
+  }
+
+  if (CONV) {
+    if (wave < 3) {
+      // wave 0: Q block of head h, wave 1: K block, wave 2: V block.
+      const int ch0 = wave * nh * 128 + h * 128;
+      uint16_t* cs_seq = p.conv_state + (long long)seq * p.conv_stride;
+      uint16_t y[2];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int ch = ch0 + lane + 64 * half;
+        uint2* csp = reinterpret_cast<uint2*>(cs_seq + ch * 4);
+        const uint2 old = *csp;
+        const uint2 wv = *reinterpret_cast<const uint2*>(p.conv_w + ch * 4);
+        const uint16_t x = qkv[ch];
+        // shifted window (conv_l2_qk.comp:48-58): [old1, old2, old3, x]
+        const uint16_t s0 = (uint16_t)(old.x >> 16);
+        const uint16_t s1 = (uint16_t)(old.y & 0xffffu);
+        const uint16_t s2 = (uint16_t)(old.y >> 16);
+        const uint16_t s3 = x;
+        *csp = make_uint2((uint32_t)s0 | ((uint32_t)s1 << 16), (uint32_t)s2 | ((uint32_t)s3 << 16));
+        float sum = 0.0f;
+        sum = sum + spk::h2f(s0) * spk::h2f((uint16_t)(wv.x & 0xffffu));
+        sum = sum + spk::h2f(s1) * spk::h2f((uint16_t)(wv.x >> 16));
+        sum = sum + spk::h2f(s2) * spk::h2f((uint16_t)(wv.y & 0xffffu));
+        sum = sum + spk::h2f(s3) * spk::h2f((uint16_t)(wv.y >> 16));
+        y[half] = spk::f2h(spk::silu_det(sum));
+      }
+      if (wave < 2) {
+        const float ya = spk::h2f(y[0]);
+        const float yb = spk::h2f(y[1]);
+        float v = ya * ya + yb * yb;          // tree step stride 64
+        v = spk::tree64_to_lane0(v);          // strides 32..1
+        const float tot = __shfl(v, 0, 64);
+        const float inv = spk::rsqrt_det(tot + 1e-6f);
+        y[0] = spk::f2h(ya * inv);
+        y[1] = spk::f2h(yb * inv);
+      }
+      qkv[ch0 + lane] = y[0];
+      qkv[ch0 + lane + 64] = y[1];
+      if (REC) {
+        if (wave == 0) {
+          s_q[lane] = spk::h2f(y[0]) * p.q_scale;
+          s_q[lane + 64] = spk::h2f(y[1]) * p.q_scale;
+        } else if (wave == 1) {
+          s_k[lane] = spk::h2f(y[0]);
+          s_k[lane + 64] = spk::h2f(y[1]);
+        } else {
+          s_v[lane] = spk::h2f(y[0]);
+          s_v[lane + 64] = spk::h2f(y[1]);
+        }
+      }
+    }
+  } else if (REC) {
+    if (tid < 128) {
+      s_q[tid] = spk::h2f(qkv[h * 128 + tid]) * p.q_scale;
+      s_k[tid] = spk::h2f(qkv[nh * 128 + h * 128 + tid]);
+      s_v[tid] = spk::h2f(qkv[2 * nh * 128 + h * 128 + tid]);
+    }
+  }
+  if (!REC) return;
+
+  float g, beta;
+  if (GB_TAIL) {
+    const float* tail = p.state + (long long)seq * p.state_stride + (long long)nh * 128 * 128;
+    g = tail[h];
+    beta = tail[nh + h];
+  } else {
+    const float av = spk::h2f(p.a[(long long)seq * p.ab_stride + h]);
+    const float bv = spk::h2f(p.b[(long long)seq * p.ab_stride + h]);
+    const float a_log = p.alb[(p.layer * nh + h) * 2];
+    const float dt_bias = p.alb[(p.layer * nh + h) * 2 + 1];
+    const float sp = spk::logf_det(1.0f + spk::expf_det(av + dt_bias));
+    g = -spk::expf_det(a_log) * sp;
+    beta = 1.0f / (1.0f + spk::expf_det(-bv));
+  }
+  __syncthreads();
+
+  // decay + kv partials
+  const float eg = spk::expf_det(g);
+  float kp0 = 0.f, kp1 = 0.f, kp2 = 0.f, kp3 = 0.f;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const float ki = s_k[rg * 16 + m];
+    S[m].x = S[m].x * eg;
+    S[m].y = S[m].y * eg;
+    S[m].z = S[m].z * eg;
+    S[m].w = S[m].w * eg;
+    kp0 = __builtin_fmaf(S[m].x, ki, kp0);
+    kp1 = __builtin_fmaf(S[m].y, ki, kp1);
+    kp2 = __builtin_fmaf(S[m].z, ki, kp2);
+    kp3 = __builtin_fmaf(S[m].w, ki, kp3);
+  }
+  *reinterpret_cast<float4*>(&s_part[rg][c4 * 4]) = make_float4(kp0, kp1, kp2, kp3);
+  __syncthreads();
+  if (tid < 128) {
+    float pp[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) pp[r] = s_part[r][tid];
+    const float kv = tree8(pp);
+    s_delta[tid] = (s_v[tid] - kv) * beta;
+  }
+  __syncthreads();
+
+  // rank-1 update, state write-back, output partials
+  const float4 d4 = *reinterpret_cast<const float4*>(&s_delta[c4 * 4]);
+  float op0 = 0.f, op1 = 0.f, op2 = 0.f, op3 = 0.f;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const float ki = s_k[rg * 16 + m];
+    const float qi = s_q[rg * 16 + m];
+    S[m].x = __builtin_fmaf(ki, d4.x, S[m].x);
+    S[m].y = __builtin_fmaf(ki, d4.y, S[m].y);
+    S[m].z = __builtin_fmaf(ki, d4.z, S[m].z);
+    S[m].w = __builtin_fmaf(ki, d4.w, S[m].w);
+    *reinterpret_cast<float4*>(st_head + (rg * 16 + m) * 128 + c4 * 4) = S[m];
+    op0 = __builtin_fmaf(S[m].x, qi, op0);
+    op1 = __builtin_fmaf(S[m].y, qi, op1);
+    op2 = __builtin_fmaf(S[m].z, qi, op2);
+    op3 = __builtin_fmaf(S[m].w, qi, op3);
+  }
+  *reinterpret_cast<float4*>(&s_part[rg][c4 * 4]) = make_float4(op0, op1, op2, op3);
+  __syncthreads();
+
+  if (wave == 0) {
+    float pa[8], pb[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      pa[r] = s_part[r][lane];
+      pb[r] = s_part[r][lane + 64];
+    }
+    const float oa = tree8(pa);
+    const float ob = tree8(pb);
+    uint16_t* out = qkv + 2 * nh * 128 + h * 128;
+    if (NORM_GATE) {
+      float v = oa * oa + ob * ob;
+      v = spk::tree64_to_lane0(v);
+      const float tot = __shfl(v, 0, 64);
+      const float r = spk::rsqrt_det(tot / 128.0f + p.eps);
+      const uint16_t* zr = p.z + (long long)seq * p.z_stride + h * 128;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int j = lane + 64 * half;
+        const float o = half ? ob : oa;
+        const float normed = o * r;
+        const float weighted = spk::h2f(spk::f2h(p.norm_w[j] * normed));
+        out[j] = spk::f2h(weighted * spk::silu_det(spk::h2f(zr[j])));
+      }
+    } else {
+      out[lane] = spk::f2h(oa);
+      out[lane + 64] = spk::f2h(ob);
+    }
+  }
+}
+
+int validate(const SpkDecodeArgs* a, bool conv, bool rec, bool gb_inline, bool norm_gate) {
+  if (!a) return spk::fail(SPK_ERR_NULL, "decode: args is NULL");
+  if (a->batch < 0) return spk::fail(SPK_ERR_SHAPE, "decode: batch %d < 0", a->batch);
+  if (a->num_heads <= 0 || a->num_heads > 64)
+    return spk::fail(SPK_ERR_SHAPE, "decode: num_heads %d unsupported", a->num_heads);
+  const long long conv_dim = 3LL * a->num_heads * 128;
+  if (!a->qkv) return spk::fail(SPK_ERR_NULL, "decode: qkv is NULL");
+  if (a->batch > 1 && a->qkv_stride < conv_dim)
+    return spk::fail(SPK_ERR_SHAPE, "decode: qkv_stride %lld < conv_dim %lld", (long long)a->qkv_stride, conv_dim);
+  if (conv) {
+    if (!a->conv_state || !a->conv_weight) return spk::fail(SPK_ERR_NULL, "decode: conv_state/conv_weight NULL");
+    if (!spk::aligned(a->conv_state, 8) || !spk::aligned(a->conv_weight, 8) || (a->conv_state_stride % 4) != 0)
+      return spk::fail(SPK_ERR_ALIGN, "decode: conv_state/conv_weight must be 8-byte aligned, stride %% 4 == 0");
+    if (a->batch > 1 && a->conv_state_stride < conv_dim * 4)
+      return spk::fail(SPK_ERR_SHAPE, "decode: conv_state_stride too small");
+  }
+  if (rec) {
+    if (!a->state) return spk::fail(SPK_ERR_NULL, "decode: state is NULL");
+    if (!spk::aligned(a->state, 16) || (a->state_stride % 4) != 0)
+      return spk::fail(SPK_ERR_ALIGN, "decode: state must be 16-byte aligned with state_stride %% 4 == 0");
+    const long long need = (long long)a->num_heads * 128 * 128 + (gb_inline ? 0 : 2LL * a->num_heads);
+    if (a->batch > 1 && a->state_stride < need)
+      return spk::fail(SPK_ERR_SHAPE, "decode: state_stride %lld < %lld", (long long)a->state_stride, need);
+    if (gb_inline) {
+      if (!a->a || !a->b || !a->a_log_bias) return spk::fail(SPK_ERR_NULL, "decode: a/b/a_log_bias NULL");
+      if (a->layer_idx < 0) return spk::fail(SPK_ERR_ARG, "decode: layer_idx < 0");
+      if (a->batch > 1 && a->ab_stride < a->num_heads) return spk::fail(SPK_ERR_SHAPE, "decode: ab_stride too small");
+    }
+    if (norm_gate) {
+      if (!a->z || !a->norm_weight) return spk::fail(SPK_ERR_NULL, "decode: z/norm_weight NULL");
+      if (a->batch > 1 && a->z_stride < a->num_heads * 128) return spk::fail(SPK_ERR_SHAPE, "decode: z_stride too small");
+    }
+  }
+  return SPK_OK;
+}
+
+DecodeParams make_params(const SpkDecodeArgs* a) {
+  DecodeParams p;
+  p.nh = a->num_heads;
+  p.layer = a->layer_idx;
+  p.q_scale = a->q_scale != 0.0f ? a->q_scale : 1.0f / sqrtf(128.0f);
+  p.eps = a->rms_eps != 0.0f ? a->rms_eps : 1e-6f;
+  p.qkv = a->qkv;
+  p.qkv_stride = a->qkv_stride;
+  p.conv_state = a->conv_state;
+  p.conv_stride = a->conv_state_stride;
+  p.conv_w = a->conv_weight;
+  p.a = a->a;
+  p.b = a->b;
+  p.ab_stride = a->ab_stride;
+  p.alb = a->a_log_bias;
+  p.state = a->state;
+  p.state_stride = a->state_stride;
+  p.z = a->z;
+  p.z_stride = a->z_stride;
+  p.norm_w = a->norm_weight;
+  return p;
+}
+
+template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE>
+int launch(const SpkDecodeArgs* a, spk_stream_t stream, const char* name) {
+  const int rc = validate(a, CONV, REC, REC && !GB_TAIL, REC && NORM_GATE);
+  if (rc) return rc;
+  if (a->batch == 0) return SPK_OK;
+  dim3 grid(a->num_heads, a->batch);
+  hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE>), grid, dim3(256), 0,
+                     spk::to_hip(stream), make_params(a));
+  return spk::check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int spk_deltanet_decode_step(const SpkDecodeArgs* a, spk_stream_t stream) {
+  return launch<true, true, false, true>(a, stream, "spk_deltanet_decode_step");
+}
+extern "C" int spk_deltanet_conv_l2_qk(const SpkDecodeArgs* a, spk_stream_t stream) {
+  return launch<true, false, false, false>(a, stream, "spk_deltanet_conv_l2_qk");
+}
+extern "C" int spk_deltanet_recurrent_gbeta_norm_gate(const SpkDecodeArgs* a, spk_stream_t stream) {
+  return launch<false, true, false, true>(a, stream, "spk_deltanet_recurrent_gbeta_norm_gate");
+}
+extern "C" int spk_deltanet_recurrent(const SpkDecodeArgs* a, spk_stream_t stream) {
+  return launch<false, true, true, false>(a, stream, "spk_deltanet_recurrent");
+}

@@ -1,0 +1,340 @@
+// gemv.hip -- batch-1 fp16 decode GEMV, tied lm_head fused with argmax, and a
+// standalone argmax.  All are HBM streams (weights read once); no MFMA.
+//
+// One wavefront per output row at a time, R rows in flight per wavefront.
+// Lane l reads the contiguous span [l*in/64, (l+1)*in/64) of the row with
+// 16-byte loads (in=1024: 2 x dwordx4 per lane, the wave covers the 2 KiB row),
+// accumulates fp16*fp16 products (exact in fp32) in span order, then the
+// 64-lane tree s[l] += s[l+stride] for stride 32..1 -- lm_head_tiled.comp:
+// 59-73's order -- and rounds once to fp16 (RNE).
+//
+// Argmax keeps argmax.comp:27-63's exact result, including its tie rule: with
+// E = ceil(N/256) and element i in "lane" i/E, the shader keeps the first
+// strict maximum inside each lane and a strictly-greater tree across lanes, so
+// among equal maxima the winner is the lane with the smallest 8-bit-reversed
+// lane id, then the smallest offset.  That is a total order, encoded as a
+// 64-bit key (value, rank) whose maximum is the winner; any reduction order
+// (waves, workgroups) gives the same index.
+#include "capi_common.hpp"
+#include "numerics.hpp"
+
+#include <float.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t ordered_f32(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) == 0u) u = 0u;  // +0 and -0 tie in argmax.comp
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Key of element idx with value v; 0 = never wins (NaN, -inf: fails v > -FLT_MAX).
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx, uint32_t E) {
+  if (!(v > -FLT_MAX)) return 0ull;
+  const uint32_t lane = idx / E;
+  const uint32_t off = idx - lane * E;
+  const uint32_t rev = __builtin_bitreverse32(lane) >> 24;
+  const uint32_t rank = ((255u - rev) << 24) | (0xffffffu - off);
+  return ((unsigned long long)ordered_f32(v) << 32) | rank;
+}
+
+__device__ __forceinline__ uint32_t key_to_index(unsigned long long key, uint32_t E) {
+  if (key == 0ull) return 0u;
+  const uint32_t rank = (uint32_t)key;
+  const uint32_t rev = 255u - (rank >> 24);
+  const uint32_t lane = __builtin_bitreverse32(rev) >> 24;
+  const uint32_t off = 0xffffffu - (rank & 0xffffffu);
+  return lane * E + off;
+}
+
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, d, 64);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), d, 64);
+    v = umax64(v, ((unsigned long long)hi << 32) | lo);
+  }
+  return v;
+}
+
+template <int NT>
+__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v) {
+  __shared__ unsigned long long s_red[NT / 64];
+  v = wave_max_u64(v);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) s_red[wave] = v;
+  __syncthreads();
+  unsigned long long r = 0ull;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) r = umax64(r, s_red[w]);
+  return r;
+}
+
+__device__ __forceinline__ void unpack8(const uint4& u, float* f) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = spk::h2f((uint16_t)(w[i] & 0xffffu));
+    f[2 * i + 1] = spk::h2f((uint16_t)(w[i] >> 16));
+  }
+}
+
+// Dot products of R rows (row0..row0+R-1, clipped to out_dim) with x; lane 0
+// of the wave returns the fp32 sums.
+template <int N8, int R>
+__device__ __forceinline__ void rows_dot(const uint16_t* __restrict__ W, int in_dim, int row0,
+                                         int out_dim, const float* xf, int lane, float* sums) {
+  uint4 wv[R][N8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r;
+    if (row < out_dim) {
+      const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
+#pragma unroll
+      for (int k = 0; k < N8; ++k) wv[r][k] = ld_stream(src + k);
+    } else {
+#pragma unroll
+      for (int k = 0; k < N8; ++k) wv[r][k] = make_uint4(0, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N8; ++k) {
+      float wf[8];
+      unpack8(wv[r][k], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
+    }
+    sums[r] = spk::tree64_to_lane0(acc);
+  }
+}
+
+template <int N8>
+__device__ __forceinline__ void load_x(const uint16_t* __restrict__ x, int lane, float* xf) {
+  const uint4* src = reinterpret_cast<const uint4*>(x + lane * (8 * N8));
+#pragma unroll
+  for (int k = 0; k < N8; ++k) unpack8(src[k], xf + 8 * k);
+}
+
+template <int N8, int R>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ W,
+                                                   const uint16_t* __restrict__ x,
+                                                   uint16_t* __restrict__ y, int out_dim) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int in_dim = 512 * N8;
+  float xf[8 * N8];
+  load_x<N8>(x, lane, xf);
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  float sums[R];
+  rows_dot<N8, R>(W, in_dim, row0, out_dim, xf, lane, sums);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (row0 + r < out_dim) y[row0 + r] = spk::f2h(sums[r]);
+  }
+}
+
+// Any in_dim % 64 == 0: scalar loads, same order.
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const uint16_t* __restrict__ W,
+                                                           const uint16_t* __restrict__ x,
+                                                           uint16_t* __restrict__ y, int out_dim,
+                                                           int in_dim) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= out_dim) return;
+  const int span = in_dim / 64;
+  const uint16_t* wr = W + (size_t)row * in_dim + lane * span;
+  const uint16_t* xr = x + lane * span;
+  float acc = 0.0f;
+  for (int j = 0; j < span; ++j) acc = __builtin_fmaf(spk::h2f(wr[j]), spk::h2f(xr[j]), acc);
+  acc = spk::tree64_to_lane0(acc);
+  if (lane == 0) y[row] = spk::f2h(acc);
+}
+
+template <int N8, int R>
+__global__ __launch_bounds__(256) void lm_head_kernel(const uint16_t* __restrict__ W,
+                                                      const uint16_t* __restrict__ x,
+                                                      uint16_t* __restrict__ logits, int vocab,
+                                                      uint32_t E,
+                                                      unsigned long long* __restrict__ partial) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float xf[8 * N8];
+  load_x<N8>(x, lane, xf);
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  float sums[R];
+  rows_dot<N8, R>(W, 512 * N8, row0, vocab, xf, lane, sums);
+  unsigned long long key = 0ull;
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = row0 + r;
+      if (row < vocab) {
+        const uint16_t l16 = spk::f2h(sums[r]);
+        if (logits) logits[row] = l16;
+        key = umax64(key, argmax_key(spk::h2f(l16), (uint32_t)row, E));
+      }
+    }
+  }
+  key = block_max_u64<256>(key);
+  if (threadIdx.x == 0) partial[blockIdx.x] = key;
+}
+
+__global__ __launch_bounds__(1024) void argmax_partials_kernel(const unsigned long long* __restrict__ partial,
+                                                               int n, uint32_t E,
+                                                               uint32_t* __restrict__ out) {
+  unsigned long long key = 0ull;
+  for (int i = threadIdx.x; i < n; i += 1024) key = umax64(key, partial[i]);
+  key = block_max_u64<1024>(key);
+  if (threadIdx.x == 0) *out = key_to_index(key, E);
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ vals, int n,
+                                                      uint32_t E, uint32_t* __restrict__ out) {
+  unsigned long long key = 0ull;
+  for (int i = threadIdx.x; i < n; i += 1024)
+    key = umax64(key, argmax_key(spk::h2f(vals[i]), (uint32_t)i, E));
+  key = block_max_u64<1024>(key);
+  if (threadIdx.x == 0) *out = key_to_index(key, E);
+}
+
+constexpr int kLmRows = 8;  // rows per wavefront in the lm_head stream
+
+int launch_gemv(const uint16_t* W, const uint16_t* x, uint16_t* y, int out_dim, int in_dim,
+                hipStream_t s) {
+  const bool vec = (in_dim % 512 == 0) && in_dim <= 8 * 512 && spk::aligned(W, 16) &&
+                   spk::aligned(x, 16);
+  if (!vec) {
+    hipLaunchKernelGGL(gemv_generic_kernel, dim3((out_dim + 3) / 4), dim3(256), 0, s, W, x, y,
+                       out_dim, in_dim);
+    return spk::check_launch("spk_matvec_f16 (generic)");
+  }
+  // Rows per wave: enough workgroups to cover the chip for small outputs,
+  // more bytes in flight per lane for large ones.
+  const int R = out_dim >= 16384 ? 4 : 1;
+  const int rows_per_block = 4 * R;
+  dim3 grid((out_dim + rows_per_block - 1) / rows_per_block);
+#define SPK_GEMV_CASE(n8)                                                                      \
+  case n8:                                                                                     \
+    if (R == 4)                                                                                \
+      hipLaunchKernelGGL((gemv_kernel<n8, 4>), grid, dim3(256), 0, s, W, x, y, out_dim);       \
+    else                                                                                       \
+      hipLaunchKernelGGL((gemv_kernel<n8, 1>), grid, dim3(256), 0, s, W, x, y, out_dim);       \
+    break;
+  switch (in_dim / 512) {
+    SPK_GEMV_CASE(1)
+    SPK_GEMV_CASE(2)
+    SPK_GEMV_CASE(3)
+    SPK_GEMV_CASE(4)
+    SPK_GEMV_CASE(5)
+    SPK_GEMV_CASE(6)
+    SPK_GEMV_CASE(7)
+    SPK_GEMV_CASE(8)
+    default:
+      return spk::fail(SPK_ERR_SHAPE, "spk_matvec_f16: in_dim %d", in_dim);
+  }
+#undef SPK_GEMV_CASE
+  return spk::check_launch("spk_matvec_f16");
+}
+
+int check_gemv(const uint16_t* W, const uint16_t* x, const uint16_t* y, int out_dim, int in_dim,
+               const char* who) {
+  if (!W || !x || !y) return spk::fail(SPK_ERR_NULL, "%s: NULL pointer", who);
+  if (out_dim < 0 || in_dim <= 0 || in_dim % 64 != 0)
+    return spk::fail(SPK_ERR_SHAPE, "%s: out_dim %d in_dim %d (in_dim must be a positive multiple of 64)",
+                     who, out_dim, in_dim);
+  return SPK_OK;
+}
+
+}  // namespace
+
+extern "C" int spk_matvec_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, int32_t out_dim,
+                              int32_t in_dim, spk_stream_t stream) {
+  const int rc = check_gemv(W, x, y, out_dim, in_dim, "spk_matvec_f16");
+  if (rc) return rc;
+  if (out_dim == 0) return SPK_OK;
+  return launch_gemv(W, x, y, out_dim, in_dim, spk::to_hip(stream));
+}
+
+extern "C" int spk_matvec_f16_batched(const SpkMatvecDesc* d, int32_t count, spk_stream_t stream) {
+  if (count < 0 || (count > 0 && !d)) return spk::fail(SPK_ERR_ARG, "spk_matvec_f16_batched: bad descriptor list");
+  for (int i = 0; i < count; ++i) {
+    const int rc = check_gemv(d[i].W, d[i].x, d[i].y, d[i].out_dim, d[i].in_dim, "spk_matvec_f16_batched");
+    if (rc) return rc;
+  }
+  for (int i = 0; i < count; ++i) {
+    if (d[i].out_dim == 0) continue;
+    const int rc = launch_gemv(d[i].W, d[i].x, d[i].y, d[i].out_dim, d[i].in_dim, spk::to_hip(stream));
+    if (rc) return rc;
+  }
+  return SPK_OK;
+}
+
+extern "C" int spk_argmax_f16(const uint16_t* vals, int32_t n, uint32_t* out_index,
+                              spk_stream_t stream) {
+  if (!vals || !out_index) return spk::fail(SPK_ERR_NULL, "spk_argmax_f16: NULL pointer");
+  if (n <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_argmax_f16: n %d", n);
+  const uint32_t E = (uint32_t)((n + 255) / 256);
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, spk::to_hip(stream), vals, n, E, out_index);
+  return spk::check_launch("spk_argmax_f16");
+}
+
+extern "C" size_t spk_lm_head_workspace_size(int32_t vocab) {
+  if (vocab <= 0) return 0;
+  const size_t blocks = ((size_t)vocab + 4 * kLmRows - 1) / (4 * kLmRows);
+  return ((blocks * sizeof(unsigned long long) + 255) / 256) * 256;
+}
+
+extern "C" int spk_lm_head_argmax(const uint16_t* W, const uint16_t* x, int32_t vocab,
+                                  int32_t hidden, uint16_t* logits, uint32_t* out_index,
+                                  void* workspace, size_t workspace_bytes, spk_stream_t stream) {
+  if (!W || !x || !out_index || !workspace) return spk::fail(SPK_ERR_NULL, "spk_lm_head_argmax: NULL pointer");
+  if (vocab <= 0 || hidden <= 0 || hidden % 512 != 0 || hidden > 8 * 512)
+    return spk::fail(SPK_ERR_SHAPE, "spk_lm_head_argmax: vocab %d hidden %d (hidden must be a multiple of 512, <= 4096)",
+                     vocab, hidden);
+  if (!spk::aligned(W, 16) || !spk::aligned(x, 16) || !spk::aligned(workspace, 8))
+    return spk::fail(SPK_ERR_ALIGN, "spk_lm_head_argmax: W/x must be 16-byte aligned");
+  if (workspace_bytes < spk_lm_head_workspace_size(vocab))
+    return spk::fail(SPK_ERR_ARG, "spk_lm_head_argmax: workspace %zu < %zu bytes", workspace_bytes,
+                     spk_lm_head_workspace_size(vocab));
+  hipStream_t s = spk::to_hip(stream);
+  const uint32_t E = (uint32_t)((vocab + 255) / 256);
+  const int blocks = (vocab + 4 * kLmRows - 1) / (4 * kLmRows);
+  auto* partial = static_cast<unsigned long long*>(workspace);
+#define SPK_LM_CASE(n8)                                                                        \
+  case n8:                                                                                     \
+    hipLaunchKernelGGL((lm_head_kernel<n8, kLmRows>), dim3(blocks), dim3(256), 0, s, W, x,     \
+                       logits, vocab, E, partial);                                             \
+    break;
+  switch (hidden / 512) {
+    SPK_LM_CASE(1)
+    SPK_LM_CASE(2)
+    SPK_LM_CASE(3)
+    SPK_LM_CASE(4)
+    SPK_LM_CASE(5)
+    SPK_LM_CASE(6)
+    SPK_LM_CASE(7)
+    SPK_LM_CASE(8)
+    default:
+      return spk::fail(SPK_ERR_SHAPE, "spk_lm_head_argmax: hidden %d", hidden);
+  }
+#undef SPK_LM_CASE
+  int rc = spk::check_launch("spk_lm_head_argmax (stream)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(argmax_partials_kernel, dim3(1), dim3(1024), 0, s, partial, blocks, E, out_index);
+  return spk::check_launch("spk_lm_head_argmax (reduce)");
+}

@@ -1,0 +1,92 @@
+"""GPU parity of the decode GEMVs, lm_head and argmax against the oracle.
+
+Bar: bit-exact fp16 outputs and argmax indices (the oracle restates
+lm_head_tiled.comp's summation order and argmax.comp's tie rule)."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+CHAIN = [(6144, 1024), (2048, 1024), (1024, 2048), (3584, 1024), (3584, 1024), (1024, 3584)]
+
+
+def _t(dev, a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.float16)).to(dev)
+
+
+@pytest.mark.parametrize("out_dim,in_dim", CHAIN + [(16, 1024), (7, 64), (300, 192), (40000, 512)])
+def test_matvec_bitexact(dev, oracle, out_dim, in_dim):
+    from spock_amd import ops, synth
+    W = synth.gemv_weights(out_dim, in_dim, seed=out_dim * 7 + in_dim)
+    x = synth.gemv_input(in_dim, seed=in_dim)
+    y = ops.matvec_f16(_t(dev, W), _t(dev, x))
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16(W, x))
+
+
+def test_matvec_batched_equals_single(dev):
+    from spock_amd import ops, synth
+    items, singles = [], []
+    for i, (o, n) in enumerate(CHAIN):
+        W = _t(dev, synth.gemv_weights(o, n, seed=i))
+        x = _t(dev, synth.gemv_input(n, seed=50 + i))
+        items.append((W, x, torch.empty(o, dtype=torch.float16, device=dev)))
+        singles.append(ops.matvec_f16(W, x))
+    ops.matvec_f16_batched(items)
+    torch.cuda.synchronize()
+    for (_, _, y), s in zip(items, singles):
+        assert torch.equal(y, s)
+
+
+def test_lm_head_argmax_config3(dev, oracle):
+    from spock_amd import ops, synth
+    V, Hd = 248320, 1024
+    W = synth.gemv_weights(V, Hd, seed=31)
+    x = synth.gemv_input(Hd, seed=32)
+    logits = torch.empty(V, dtype=torch.float16, device=dev)
+    idx = ops.lm_head_argmax(_t(dev, W), _t(dev, x), logits=logits)
+    torch.cuda.synchronize()
+    e_idx, e_logits = oracle.lm_head_argmax(W, x)
+    assert np.array_equal(logits.cpu().numpy().view(np.uint16), e_logits)
+    assert int(idx.cpu()[0]) == e_idx
+    # without the logits buffer
+    idx2 = ops.lm_head_argmax(_t(dev, W), _t(dev, x))
+    torch.cuda.synchronize()
+    assert int(idx2.cpu()[0]) == e_idx
+
+
+def _tie_patterns():
+    n = 248320
+    E = (n + 255) // 256
+    pats = []
+    v = np.zeros(n, np.float16)
+    v[[E * 64, E * 128]] = 3.0  # argmax.comp's tree keeps lane 128's (bit-reversed order)
+    pats.append(v)
+    v = np.full(n, -1.0, np.float16)
+    v[[5, 6, E * 3 + 1]] = 2.0
+    pats.append(v)
+    v = np.full(n, np.nan, np.float16)
+    pats.append(v)
+    v = np.full(n, -np.inf, np.float16)
+    v[77777] = -65504.0
+    pats.append(v)
+    v = np.zeros(n, np.float16)
+    v[::2] = -0.0
+    pats.append(v)
+    rng = np.random.default_rng(0)
+    v = rng.integers(-3, 4, n).astype(np.float16)  # many ties
+    pats.append(v)
+    v = np.zeros(1000, np.float16)
+    v[[3, 999]] = 1.0
+    pats.append(v)
+    return pats
+
+
+@pytest.mark.parametrize("i", range(7))
+def test_argmax_tie_rule(dev, oracle, i):
+    from spock_amd import ops
+    v = _tie_patterns()[i]
+    out = ops.argmax_f16(_t(dev, v.view(np.uint16)))
+    torch.cuda.synchronize()
+    assert int(out.cpu()[0]) == oracle.argmax_f16(v.view(np.uint16))
