@@ -1,0 +1,294 @@
+"""Benchmark of the MI355X DeltaNet hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Headline (`value`): gated-DeltaNet chunk prefill throughput in tokens/s on
+the ragged packed workload -- 8 sequences with lengths drawn from U[512, 8192]
+(seeded), H=16, d_k=d_v=128, C=64, fp16 q/k/v inputs, fp32 compute -- one
+step = one spk_chunk_prefill call over the whole pack, inputs resident in HBM.
+The dominant-kernel roofline is fp32 MFMA (157.3 TFLOP/s) with the
+algorithmic work 2(5C^2d + 3Cd^2 + C^3/3) FLOP per (head, padded chunk).
+
+Secondary lines (same JSON object, "secondary"): the 104-token single-layer
+chunk prefill, the batched DeltaNet decode step at B = 1, 16, 64, 256, the
+decode GEMV chain and the tied lm_head + argmax, each against the HBM peak
+(8 TB/s) with the algorithmic bytes stated per call.  Buffers of workloads
+smaller than 512 MB are rotated across copies so that the 256 MB last-level
+cache cannot serve them.
+
+cpu_baseline: the reference's own chunk rule (oracle/_ref, compiled from
+src/runtime/deltanet_chunk.cpp, single-threaded) timed on a bounded sample of
+the same workload; the oracle restatement is used when _ref is absent.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "DeltaNet prefill tok/s + b=1 decode tok/s on 1 MI355X; % MFMA/HBM roofline"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+H, D, C = 16, 128, 64
+FLOP_PER_HEAD_CHUNK = 2 * (5 * C * C * D + 3 * C * D * D + C ** 3 / 3)  # 11,709,098.7
+DECODE_BYTES_PER_SEQ = (2 * H * D * D * 4 + 6144 * 2 + 2 * 6144 * 4 * 2 + 2048 * 2 + 64
+                        + 2048 * 2)  # 2,216,000
+DECODE_SHARED_BYTES = 6144 * 4 * 2 + 18 * 16 * 2 * 4 + 128 * 4  # conv w, A_log/dt_bias, norm w
+CHAIN = [(6144, 1024), (2048, 1024), (1024, 2048), (3584, 1024), (3584, 1024), (1024, 3584)]
+VOCAB, HIDDEN = 248320, 1024
+ROTATE_BYTES = 512 << 20
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_launches(fn, steps, warmup, rotate=1):
+    """Runs fn(i) warmup+steps times on the current stream; returns
+    (wall seconds over the timed steps, list of per-launch event ms)."""
+    import torch
+    for i in range(warmup):
+        fn(i % rotate)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        evs[i][0].record()
+        fn((warmup + i) % rotate)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, [a.elapsed_time(b) for a, b in evs]
+
+
+def bench_prefill(steps, warmup):
+    import torch
+    from spock_amd import ops, synth
+    dev = torch.device("cuda:0")
+    lens = synth.ragged_lengths(8, 512, 8192, seed=2024)
+    cu = synth.cu_seqlens_from(lens)
+    N = int(cu[-1])
+    log(f"[bench] prefill workload: 8 seqs, lengths {lens.tolist()}, N={N}")
+    inp = synth.chunk_inputs(H, N, seed=2)
+    q, k, v = (torch.from_numpy(inp[n]).to(dev).half() for n in ("q", "k", "v"))
+    g, beta = (torch.from_numpy(inp[n]).to(dev) for n in ("g", "beta"))
+    del inp
+    core = torch.empty((H, N, D), dtype=torch.float32, device=dev)
+    state = torch.empty((8, H, D, D), dtype=torch.float32, device=dev)
+    ws = torch.empty(ops.chunk_workspace_bytes(H, N, 8), dtype=torch.uint8, device=dev)
+    cu_dev = torch.from_numpy(cu).to(dev)
+    fn = lambda i: ops.chunk_prefill(q, k, v, g, beta, cu_seqlens=cu, out_core=core, out_state=state,
+                                     workspace=ws, cu_seqlens_dev=cu_dev)
+    wall, ms = timed_launches(fn, steps, warmup)
+    chunks = int(sum(math.ceil(L / C) for L in lens))
+    flops = chunks * H * FLOP_PER_HEAD_CHUNK
+    avg_s = statistics.mean(ms) / 1e3
+    achieved = flops / avg_s / 1e12
+    res = {
+        "tokens": N, "lengths": lens.tolist(), "head_chunks": chunks * H,
+        "flop_per_launch": flops, "wall_s": wall, "launch_ms": statistics.mean(ms),
+        "launch_ms_min": min(ms),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    return res
+
+
+def bench_config0(steps, warmup):
+    import torch
+    from spock_amd import ops, synth
+    dev = torch.device("cuda:0")
+    inp = synth.chunk_inputs(H, 104, seed=0)
+    t = {n: torch.from_numpy(a).to(dev) for n, a in inp.items()}
+    core = torch.empty((H, 104, D), device=dev)
+    state = torch.empty((1, H, D, D), device=dev)
+    ws = torch.empty(ops.chunk_workspace_bytes(H, 104, 1), dtype=torch.uint8, device=dev)
+    fn = lambda i: ops.chunk_prefill(t["q"], t["k"], t["v"], t["g"], t["beta"], out_core=core,
+                                     out_state=state, workspace=ws)
+    wall, ms = timed_launches(fn, steps, warmup)
+    flops = 2 * H * FLOP_PER_HEAD_CHUNK
+    avg = statistics.mean(ms) / 1e3
+    return {"workload": "config0: H16 T104->128 C64 fp32", "launch_us": round(avg * 1e6, 2),
+            "tok_per_s": round(104 / avg, 1), "achieved_tflops": round(flops / avg / 1e12, 4),
+            "frac": round(flops / avg / 1e12 / FP32_MFMA_PEAK_TFLOPS, 5)}
+
+
+def bench_decode(B, steps, warmup):
+    import torch
+    from spock_amd import ops, synth
+    dev = torch.device("cuda:0")
+    per_copy = B * DECODE_BYTES_PER_SEQ
+    copies = max(1, min(256, math.ceil(ROTATE_BYTES / per_copy)))
+    inp = synth.decode_inputs(B, seed=B)
+    h16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.float16)).to(dev)
+    f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    shared = {"conv_w": h16(inp["conv_w"]), "a_log_bias": f32(inp["a_log_bias"]),
+              "norm_w": f32(inp["norm_w"])}
+    base = {"qkv": h16(inp["qkv"]), "state": f32(inp["state"]), "conv_state": h16(inp["conv_state"]),
+            "z": h16(inp["z"]), "a": h16(inp["a"]), "b": h16(inp["b"])}
+    sets = [base] + [{n: t.clone() for n, t in base.items()} for _ in range(copies - 1)]
+
+    def fn(i):
+        s = sets[i]
+        ops.decode_step(s["qkv"], s["state"], s["conv_state"], shared["conv_w"], s["a"], s["b"],
+                        shared["a_log_bias"], s["z"], shared["norm_w"], layer_idx=3)
+
+    wall, ms = timed_launches(fn, steps, warmup, rotate=copies)
+    avg = statistics.mean(ms) / 1e3
+    nbytes = per_copy + DECODE_SHARED_BYTES
+    gbs = nbytes / avg / 1e9
+    return {"B": B, "launch_us": round(avg * 1e6, 2), "seq_steps_per_s": round(B / avg, 1),
+            "bytes_per_launch": nbytes, "achieved_gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "rotated_copies": copies}
+
+
+def bench_gemv_chain(steps, warmup):
+    import torch
+    from spock_amd import ops, synth
+    dev = torch.device("cuda:0")
+    nbytes = sum(o * n * 2 for o, n in CHAIN)
+    copies = math.ceil(ROTATE_BYTES / nbytes)
+    Ws = [[torch.from_numpy(synth.gemv_weights(o, n, seed=10 * c + j).view(np.float16)).to(dev)
+           for j, (o, n) in enumerate(CHAIN)] for c in range(min(copies, 2))]
+    # further copies are device-side clones of the two generated sets
+    while len(Ws) < copies:
+        Ws.append([w.clone() for w in Ws[len(Ws) % 2]])
+    x = torch.from_numpy(synth.gemv_input(1024, seed=5).view(np.float16)).to(dev)
+    outs = [torch.empty(o, dtype=torch.float16, device=dev) for o, _ in CHAIN]
+    # stage 1: qkv, z, gate, up from x; stage 2: out from z, down from gate
+    def fn(i):
+        W = Ws[i]
+        ops.matvec_f16_batched([(W[0], x, outs[0]), (W[1], x, outs[1]), (W[3], x, outs[3]),
+                                (W[4], x, outs[4])])
+        ops.matvec_f16_batched([(W[2], outs[1], outs[2]), (W[5], outs[3], outs[5])])
+
+    wall, ms = timed_launches(fn, steps, warmup, rotate=copies)
+    avg = statistics.mean(ms) / 1e3
+    gbs = nbytes / avg / 1e9
+    return {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "rotated_copies": copies,
+            "kernels": 6, "launches": 6}
+
+
+def bench_lm_head(steps, warmup):
+    import torch
+    from spock_amd import ops, synth
+    dev = torch.device("cuda:0")
+    W0 = torch.from_numpy(synth.gemv_weights(VOCAB, HIDDEN, seed=31).view(np.float16)).to(dev)
+    Ws = [W0, W0.clone()]
+    x = torch.from_numpy(synth.gemv_input(HIDDEN, seed=32).view(np.float16)).to(dev)
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = torch.empty(ops.lm_head_workspace_bytes(VOCAB), dtype=torch.uint8, device=dev)
+    fn = lambda i: ops.lm_head_argmax(Ws[i], x, out=out, workspace=ws)
+    wall, ms = timed_launches(fn, steps, warmup, rotate=2)
+    avg = statistics.mean(ms) / 1e3
+    nbytes = VOCAB * HIDDEN * 2
+    gbs = nbytes / avg / 1e9
+    return {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def cpu_baseline():
+    """The reference's chunk rule on a bounded sample: one 2048-token sequence
+    of the same shape (16 heads, fp32), single thread, median of 5 runs."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib
+    from spock_amd import synth
+    use_ref = oracle_lib.ref_available()
+    L = 2048
+    inp = synth.chunk_inputs(H, L, seed=3)
+    for n in ("q", "k", "v"):
+        inp[n] = inp[n].astype(np.float16).astype(np.float32)
+    oracle_lib.chunk_rule(**{k: v[:, :64] for k, v in inp.items()}, use_ref=use_ref)  # warm-up
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        oracle_lib.chunk_rule(**inp, use_ref=use_ref)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(L / med, 1), "unit": "tok/s", "cores": 1,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"one {L}-token sequence x 16 heads (fp32, C=64), median of 5 single-thread runs "
+                      f"of {'the reference run_deltanet_chunk_rule (oracle/_ref)' if use_ref else 'the oracle restatement'}; "
+                      f"{med:.2f} s per run"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(the DeltaNet hot path shards by sequence/head with no exchange; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from spock_amd import _lib
+    _lib.lib()
+    torch.cuda.init()
+    log(f"[bench] device {torch.cuda.get_device_name(0)}")
+
+    pre = bench_prefill(args.steps, args.warmup)
+    value = pre["tokens"] * args.steps / pre["wall_s"]
+    log(f"[bench] prefill {value:,.0f} tok/s, launch {pre['launch_ms']:.3f} ms, "
+        f"{pre['roofline']['achieved']} TFLOP/s")
+    secondary = {}
+    if not args.no_secondary:
+        secondary["config0_prefill"] = bench_config0(args.steps, args.warmup)
+        log(f"[bench] config0 {secondary['config0_prefill']}")
+        secondary["decode_step"] = []
+        for B in (1, 16, 64, 256):
+            r = bench_decode(B, args.steps, args.warmup)
+            secondary["decode_step"].append(r)
+            log(f"[bench] decode {r}")
+        secondary["gemv_chain"] = bench_gemv_chain(args.steps, args.warmup)
+        log(f"[bench] gemv chain {secondary['gemv_chain']}")
+        secondary["lm_head_argmax"] = bench_lm_head(args.steps, args.warmup)
+        log(f"[bench] lm_head {secondary['lm_head_argmax']}")
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+    if cpu:
+        log(f"[bench] cpu baseline {cpu}")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["wall_s"] / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64/Box-Muller; q,k L2-normalised, fp16 q/k/v inputs)",
+        "config": {"workload": "config2: ragged packed gated-DeltaNet chunk prefill, one layer, "
+                               "8 seqs L~U[512,8192] (seed 2024), H=16, dk=dv=128, C=64, "
+                               "fp16 q/k/v in, fp32 compute and state",
+                   "tokens": pre["tokens"], "lengths": pre["lengths"], "head_chunks": pre["head_chunks"],
+                   "parallelism": "single GPU"},
+        "roofline": pre["roofline"],
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

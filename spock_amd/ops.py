@@ -50,12 +50,14 @@ def chunk_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                   cu_seqlens: Optional[Sequence[int]] = None, use_qk_l2norm: bool = False,
                   q_scale: float = 0.0, out_core: Optional[torch.Tensor] = None,
                   out_state: Optional[torch.Tensor] = None,
-                  workspace: Optional[torch.Tensor] = None, core_head_stride: int = 0):
+                  workspace: Optional[torch.Tensor] = None, core_head_stride: int = 0,
+                  cu_seqlens_dev: Optional[torch.Tensor] = None):
     """Gated-DeltaNet chunk prefill (spk_chunk_prefill).
 
     q, k: [H][N][128], v: [H][N][128] (float32 or float16, device);
     g, beta: [H][N] float32; cu_seqlens: host sequence offsets (None = one
-    sequence).  Returns (core [H][N][128] f32, state [S][H][128][128] f32).
+    sequence; cu_seqlens_dev optionally holds the same offsets already on the
+    device, int32).  Returns (core [H][N][128] f32, state [S][H][128][128] f32).
     """
     H, N, dk = q.shape
     if dk != KEY_DIM or v.shape[-1] != VALUE_DIM:
@@ -75,7 +77,7 @@ def chunk_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     else:
         cu_host = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
         S = len(cu_host) - 1
-        cu_dev = torch.from_numpy(cu_host.copy()).to(dev)
+        cu_dev = cu_seqlens_dev if cu_seqlens_dev is not None else torch.from_numpy(cu_host.copy()).to(dev)
     if out_core is None:
         out_core = torch.empty((H, N, VALUE_DIM), dtype=torch.float32, device=dev)
     if out_state is None:
