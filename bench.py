@@ -200,6 +200,19 @@ def bench_lm_head(steps, warmup):
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def bench_copy(steps, warmup):
+    """A plain device-to-device copy of 512 MiB: the calibration workload for
+    the FETCH_SIZE / WRITE_SIZE counters (known bytes read and written)."""
+    import torch
+    n = 512 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    wall, ms = timed_launches(lambda i: dst.copy_(src), steps, warmup)
+    avg = statistics.mean(ms) / 1e3
+    return {"bytes_read_per_call": n, "bytes_written_per_call": n, "launch_us": round(avg * 1e6, 2),
+            "achieved_gbs": round(2 * n / avg / 1e9, 1)}
+
+
 def cpu_baseline():
     """The reference's chunk rule on a bounded sample: one 2048-token sequence
     of the same shape (16 heads, fp32), single thread, median of 5 runs."""
@@ -232,6 +245,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy"],
+                    help="run one workload and print its own JSON (for profiler runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -244,6 +259,13 @@ def main():
     _lib.lib()
     torch.cuda.init()
     log(f"[bench] device {torch.cuda.get_device_name(0)}")
+    if args.only:
+        fns = {"prefill": bench_prefill, "config0": bench_config0, "gemv": bench_gemv_chain,
+               "lm_head": bench_lm_head, "copy": bench_copy,
+               "decode": lambda s, w: [bench_decode(B, s, w) for B in (1, 16, 64, 256)]}
+        r = fns[args.only](args.steps, args.warmup)
+        print(json.dumps({"only": args.only, "result": r}, default=float), flush=True)
+        return
 
     pre = bench_prefill(args.steps, args.warmup)
     value = pre["tokens"] * args.steps / pre["wall_s"]

@@ -36,15 +36,19 @@ constexpr int kC = 64;
 constexpr int kD = 128;
 constexpr int kLDK = 132;  // LDS row stride (floats) of [64][128] tiles
 constexpr int kLDT = 68;   // LDS row stride of [64][64] tiles
-constexpr int kLDS2 = 33;  // LDS row stride of the 32-column state / v_new tiles
-// workspace record per (chunk, head), in floats
-constexpr int kWsU = 0;
+constexpr int kLdST = 132;  // LDS row stride of the transposed 32-column state tile
+constexpr int kLdVT = 68;   // LDS row stride of the transposed v_new tile
+// workspace record per (chunk, head), in floats.  Layouts are the ones the
+// state scan reads with 16-byte loads along its contraction index:
+//   U^T  [128 value cols][64 tokens]      W  [64 tokens][128 key dims]
+//   A    [64 tokens][64 tokens]           KdT [128 key dims][64 tokens], K*ks
+constexpr int kWsUT = 0;
 constexpr int kWsW = 8192;
 constexpr int kWsA = 16384;
-constexpr int kWsQs = 20480;
-constexpr int kWsKs = 20544;
-constexpr int kWsMisc = 20608;
-constexpr int kWsStride = 20672;  // 82688 bytes, a multiple of 256
+constexpr int kWsKdT = 20480;
+constexpr int kWsQs = 28672;
+constexpr int kWsMisc = 28736;
+constexpr int kWsStride = 28800;  // 115200 bytes, a multiple of 256
 
 __device__ __forceinline__ f4v mfma4(float a, float b, f4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -111,7 +115,7 @@ __device__ __forceinline__ void locate_chunk(const ChunkParams& p, int gchunk, i
   len = 0;
 }
 
-constexpr int kIntraSmemFloats = 3 * 64 * kLDK + 2 * 64 * kLDT + 4 * 16 * 17 + 4 * 64;
+constexpr int kIntraSmemFloats = 3 * 64 * kLDK + 2 * 64 * kLDT + 4 * 16 * 17 + 5 * 64;
 
 template <typename TIn>
 __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
@@ -126,6 +130,7 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
   float* sB = sG + 64;           // [64] beta
   float* sIQ = sB + 64;          // [64] 1/|q| (or 1), later beta*e^gcum
   float* sIK = sIQ + 64;         // [64] 1/|k| (or 1)
+  float* sKS = sIK + 64;         // [64] e^{gL - gcum}
 
   const int gchunk = blockIdx.x;
   const int h = blockIdx.y;
@@ -134,7 +139,7 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
   if (seq < 0) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int li = lane & 15;
   const int lg = lane >> 4;
   const TIn* q = static_cast<const TIn*>(p.q);
@@ -195,13 +200,22 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
       sK[r * kLDK + c] *= sIK[r];
     }
   }
+  __syncthreads();
   const float gL = sG[63];
   if (tid < 64) {
-    ws[kWsQs + tid] = (sIQ[tid] * p.q_scale) * expf(sG[tid]);
-    ws[kWsKs + tid] = sIK[tid] * expf(gL - sG[tid]);
+    ws[kWsQs + tid] = (sIQ[tid] * p.q_scale) * expf(sG[tid]);  // Q is re-read raw
+    sKS[tid] = expf(gL - sG[tid]);  // decay to the chunk end (sK is normalised)
   }
   if (tid == 0) ws[kWsMisc] = expf(gL);
   __syncthreads();
+  // (K * e^{gL-g})^T, row kd = 64 tokens: 16 lanes write one 256-byte row
+  for (int i = tid; i < 128 * 16; i += 256) {
+    const int kd = i >> 4;
+    const int t = (i & 15) * 4;
+    *reinterpret_cast<float4*>(ws + kWsKdT + kd * 64 + t) =
+        make_float4(sK[t * kLDK + kd] * sKS[t], sK[(t + 1) * kLDK + kd] * sKS[t + 1],
+                    sK[(t + 2) * kLDK + kd] * sKS[t + 2], sK[(t + 3) * kLDK + kd] * sKS[t + 3]);
+  }
 
   // ---- K K^T -> L (into LDS) and Q K^T -> A (into the workspace); 20 tiles
   for (int tt = wave; tt < 20; tt += 4) {
@@ -299,10 +313,10 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
     __syncthreads();
   }
 
-  // ---- U = T (V*beta), W = T (K*beta*e^g); wave w owns column tiles 2w, 2w+1
+  // ---- U = T (V*beta) (stored transposed), W = T (K*beta*e^g); wave w owns
+  // column tiles 2w, 2w+1
   for (int mat = 0; mat < 2; ++mat) {
     const float* Bm = mat == 0 ? sV : sQ;
-    float* out = ws + (mat == 0 ? kWsU : kWsW);
     for (int jj = 0; jj < 2; ++jj) {
       const int J = 2 * wave + jj;
       for (int I = 0; I < 4; ++I) {
@@ -312,35 +326,277 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
           const float b = Bm[(4 * s + lg) * kLDK + 16 * J + li];
           acc = mfma4(a, b, acc);
         }
+        if (mat == 0) {
+          *reinterpret_cast<float4*>(ws + kWsUT + (16 * J + li) * 64 + 16 * I + 4 * lg) =
+              make_float4(acc[0], acc[1], acc[2], acc[3]);
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) out[(16 * I + 4 * lg + r) * kD + 16 * J + li] = acc[r];
+          for (int r = 0; r < 4; ++r) ws[kWsW + (16 * I + 4 * lg + r) * kD + 16 * J + li] = acc[r];
+        }
       }
     }
   }
 }
 
-template <typename TIn>
-__global__ __launch_bounds__(256) void chunk_state_kernel(ChunkParams p) {
-  __shared__ float sS[128 * kLDS2];
-  __shared__ float sVn[64 * kLDS2];
+// Raw (unconverted) element types for operands loaded one chunk ahead: the
+// conversion and scaling happen at use, so a prefetch never waits on its load.
+template <typename TIn> struct RawOf;
+template <> struct RawOf<float> {
+  static __device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
+  static __device__ __forceinline__ float4 cvt4(const float4& r) { return r; }
+  static __device__ __forceinline__ float ld1(const float* p, size_t i) { return p[i]; }
+  static __device__ __forceinline__ float cvt1(float r) { return r; }
+};
+template <> struct RawOf<uint16_t> {
+  // 4 halves kept as two 32-bit words in .x/.y of a float4
+  static __device__ __forceinline__ float4 ld4(const uint16_t* p, size_t i) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p + i);
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), 0.f, 0.f);
+  }
+  static __device__ __forceinline__ float4 cvt4(const float4& r) {
+    const uint32_t x = __float_as_uint(r.x), y = __float_as_uint(r.y);
+    return make_float4(spk::h2f((uint16_t)(x & 0xffffu)), spk::h2f((uint16_t)(x >> 16)),
+                       spk::h2f((uint16_t)(y & 0xffffu)), spk::h2f((uint16_t)(y >> 16)));
+  }
+  static __device__ __forceinline__ float ld1(const uint16_t* p, size_t i) { return __uint_as_float((uint32_t)p[i]); }
+  static __device__ __forceinline__ float cvt1(float r) { return spk::h2f((uint16_t)__float_as_uint(r)); }
+};
 
-  // Workgroup -> (column tile, head, sequence).  Consecutive logical ids share
-  // (sequence, head) and are placed on one XCD (workgroups are dealt to the 8
-  // XCDs round-robin) so the four tiles reading the same W/Q/K/A hit one L2.
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-  const int tile = bid & 3;
-  const int h = (bid >> 2) % p.H;
-  const int seq = (bid >> 2) / p.H;
+// One wavefront's operands of one chunk, loaded a chunk ahead.
+struct StateRegs {
+  float4 a[8][2];   // stage A rows: W (waves 0,1) or raw Q (waves 2,3)
+  float4 at[4][2];  // stage C: A rows (waves 2,3)
+  float4 kd[4][2];  // stage D: (K*ks)^T rows, 4 tokens each
+  float4 u[2][2];   // stage B: U^T, 4 tokens each (waves 0,1)
+  float qs[2];      // stage A: Q scale per row (waves 2,3)
+  float gle;        // e^{gcum_last}
+};
+
+// Sequence with rank `slot` by decreasing length (ties: lower index first).
+__device__ __forceinline__ int lpt_sequence(const ChunkParams& p, int slot) {
+  if (p.cu == nullptr || p.S > 64) return slot;
+  for (int s = 0; s < p.S; ++s) {
+    const int Ls = p.cu[s + 1] - p.cu[s];
+    int rank = 0;
+    for (int s2 = 0; s2 < p.S; ++s2) {
+      const int L2 = p.cu[s2 + 1] - p.cu[s2];
+      rank += (L2 > Ls) || (L2 == Ls && s2 < s);
+    }
+    if (rank == slot) return s;
+  }
+  return slot;
+}
+
+// Sequential chunk scan of one workgroup for one wavefront role.  WROLE:
+// waves 0,1 compute v_new = U - W S for token blocks {2w, 2w+1}; otherwise
+// waves 2,3 compute the outputs o = Q*qs S + A v_new for token blocks
+// {0,3} / {1,2} (5 of the 10 blocks of the triangular A v_new each).  All
+// waves update 32 rows of the state.  Both roles execute the same barriers.
+template <typename TIn, bool WROLE>
+__device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, float* sVT, int h,
+                                           int n0, int t_begin, int L, int co, int wave, int lane) {
+  typedef RawOf<TIn> R;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int tb0 = WROLE ? 2 * wave : (wave == 2 ? 0 : 1);
+  const int tb1 = WROLE ? 2 * wave + 1 : (wave == 2 ? 3 : 2);
+  const TIn* q = static_cast<const TIn*>(p.q);
+  const int nchunks = (L + kC - 1) / kC;
+
+  // Issue every global load of chunk c for this lane; padding rows are read
+  // from row 0 (always valid) and zeroed at use, so there is no branch.
+  auto load = [&](StateRegs& g, int c) {
+    const int tok0 = t_begin + c * kC;
+    const int len = min(kC, L - c * kC);
+    const float* ws = p.ws + ((size_t)(co + c) * p.H + h) * kWsStride;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int M = mt ? tb1 : tb0;
+      const int tok = 16 * M + li;
+      if (WROLE) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          g.a[u][mt] = *reinterpret_cast<const float4*>(ws + kWsW + tok * kD + 16 * u + 4 * lg);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          g.u[mt][nt] = *reinterpret_cast<const float4*>(ws + kWsUT + (n0 + 16 * nt + li) * 64 + 16 * M + 4 * lg);
+      } else {
+        const int row = tok < len ? tok : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          g.a[u][mt] = R::ld4(q, ((size_t)h * p.N + tok0 + row) * kD + 16 * u + 4 * lg);
+        g.qs[mt] = ws[kWsQs + tok];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (u <= M) g.at[u][mt] = *reinterpret_cast<const float4*>(ws + kWsA + tok * 64 + 16 * u + 4 * lg);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        g.kd[u][mt] = *reinterpret_cast<const float4*>(ws + kWsKdT + (32 * wave + 16 * mt + li) * 64 + 16 * u + 4 * lg);
+    g.gle = ws[kWsMisc];
+  };
+
+  // One chunk step from the operands in `cur`.
+  auto step = [&](const StateRegs& cur, int c) {
+    const int tok0 = t_begin + c * kC;
+    const int len = min(kC, L - c * kC);
+
+    // ---- stage A: rows of [W ; Q*qs] times S
+    f4v acc[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
+    float qsc[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) qsc[mt] = (16 * (mt ? tb1 : tb0) + li) < len ? cur.qs[mt] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      float4 av[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        if (WROLE) {
+          av[mt] = cur.a[u][mt];
+        } else {
+          const float4 x = R::cvt4(cur.a[u][mt]);
+          av[mt] = make_float4(x.x * qsc[mt], x.y * qsc[mt], x.z * qsc[mt], x.w * qsc[mt]);
+        }
+      }
+      const float4 b0 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * u + 4 * lg]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&sST[(16 + li) * kLdST + 16 * u + 4 * lg]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const float a = elem(av[mt], e);
+          acc[mt][0] = mfma4(a, elem(b0, e), acc[mt][0]);
+          acc[mt][1] = mfma4(a, elem(b1, e), acc[mt][1]);
+        }
+      }
+    }
+
+    // ---- stage B: v_new = U - W S
+    if (WROLE) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const int tok = 16 * (mt ? tb1 : tb0) + 4 * lg;
+          *reinterpret_cast<float4*>(&sVT[(16 * nt + li) * kLdVT + tok]) =
+              make_float4(cur.u[mt][nt].x - acc[mt][nt][0], cur.u[mt][nt].y - acc[mt][nt][1],
+                          cur.u[mt][nt].z - acc[mt][nt][2], cur.u[mt][nt].w - acc[mt][nt][3]);
+        }
+    }
+    __syncthreads();
+
+    // ---- stage C: o = Q*qs S + A v_new
+    if (!WROLE) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int M = mt ? tb1 : tb0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (u <= M) {
+            const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
+            const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = elem(cur.at[u][mt], e);
+              acc[mt][0] = mfma4(a, elem(b0, e), acc[mt][0]);
+              acc[mt][1] = mfma4(a, elem(b1, e), acc[mt][1]);
+            }
+          }
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = 16 * M + 4 * lg + r;
+            if (tok < len)
+              p.core[((size_t)h * p.core_hs + tok0 + tok) * kD + n0 + 16 * nt + li] = acc[mt][nt][r];
+          }
+      }
+    }
+
+    // ---- stage D: S <- e^{gL} S + (K*ks)^T v_new, rows 32w..32w+31
+    f4v sacc[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const float4 s4 = *reinterpret_cast<const float4*>(
+            &sST[(16 * nt + li) * kLdST + 32 * wave + 16 * mt + 4 * lg]);
+        sacc[mt][nt] = f4v{s4.x * cur.gle, s4.y * cur.gle, s4.z * cur.gle, s4.w * cur.gle};
+      }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const float a = elem(cur.kd[u][mt], e);
+          sacc[mt][0] = mfma4(a, elem(b0, e), sacc[mt][0]);
+          sacc[mt][1] = mfma4(a, elem(b1, e), sacc[mt][1]);
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        *reinterpret_cast<float4*>(&sST[(16 * nt + li) * kLdST + 32 * wave + 16 * mt + 4 * lg]) =
+            make_float4(sacc[mt][nt][0], sacc[mt][nt][1], sacc[mt][nt][2], sacc[mt][nt][3]);
+    __syncthreads();
+  };
+
+  // Two register sets used alternately: the loads of chunk c+1 are in flight
+  // while chunk c computes.
+  StateRegs ra, rb;
+  if (nchunks > 0) load(ra, 0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; c += 2) {
+    if (c + 1 < nchunks) load(rb, c + 1);
+    step(ra, c);
+    if (c + 1 >= nchunks) break;
+    if (c + 2 < nchunks) load(ra, c + 2);
+    step(rb, c + 1);
+  }
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(256, 1) void chunk_state_kernel(ChunkParams p) {
+  // S tile and v_new stored transposed ([column][contraction index]) so one
+  // ds_read_b128 feeds four consecutive MFMA steps; strides 132 and 68 keep
+  // the 8-lane groups of a b128 access on distinct banks.
+  __shared__ float sST[32 * kLdST];
+  __shared__ float sVT[32 * kLdVT];
+
+  // Workgroup -> (column tile, head, sequence).  Groups (sequence, head) are
+  // dealt longest sequence first so the longest chunk scans start earliest,
+  // and the four column tiles of a group get workgroup ids congruent mod 8 --
+  // the same XCD (ids are dealt to the 8 XCDs round-robin) -- so they share
+  // one L2 for W, Q, K and A.
+  const int b = blockIdx.x;
+  const int groups = p.S * p.H;
+  int gi, tile;
+  if ((groups & 7) == 0) {
+    gi = (b >> 5) * 8 + (b & 7);
+    tile = (b >> 3) & 3;
+  } else {
+    gi = b >> 2;
+    tile = b & 3;
+  }
+  const int h = gi % p.H;
+  const int seq = lpt_sequence(p, gi / p.H);
   const int n0 = tile * 32;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const TIn* q = static_cast<const TIn*>(p.q);
-  const TIn* k = static_cast<const TIn*>(p.k);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
 
   int t_begin = 0, L = p.N, co = 0;
   if (p.cu) {
@@ -348,160 +604,25 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(ChunkParams p) {
     L = p.cu[seq + 1] - t_begin;
     for (int s = 0; s < seq; ++s) co += (p.cu[s + 1] - p.cu[s] + kC - 1) / kC;
   }
-  const int nchunks = (L + kC - 1) / kC;
 
   const float* init = p.init ? p.init + ((size_t)seq * p.H + h) * kD * kD : nullptr;
   for (int i = tid; i < 128 * 32; i += 256) {
     const int r = i >> 5;
     const int c = i & 31;
-    sS[r * kLDS2 + c] = init ? init[r * kD + n0 + c] : 0.0f;
+    sST[c * kLdST + r] = init ? init[r * kD + n0 + c] : 0.0f;
   }
+
+  if (wave < 2)
+    state_scan<TIn, true>(p, sST, sVT, h, n0, t_begin, L, co, wave, lane);
+  else
+    state_scan<TIn, false>(p, sST, sVT, h, n0, t_begin, L, co, wave, lane);
   __syncthreads();
-
-  for (int c = 0; c < nchunks; ++c) {
-    const int gchunk = co + c;
-    const int tok0 = t_begin + c * kC;
-    const int len = min(kC, L - c * kC);
-    const float* ws = p.ws + ((size_t)gchunk * p.H + h) * kWsStride;
-
-    // ---- stage A: P = [W ; Q*qs] S, wave w rows 32w..32w+31
-    f4v acc[2][2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
-    const bool wrows = wave < 2;
-#pragma unroll 2
-    for (int u = 0; u < 8; ++u) {
-      float4 a4[2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int row = 32 * wave + 16 * mt + li;
-        if (wrows) {
-          a4[mt] = load4(ws + kWsW, (size_t)row * kD + 16 * u + 4 * lg);
-        } else {
-          const int tok = row - 64;
-          if (tok < len) {
-            const float sc = ws[kWsQs + tok];
-            float4 x = load4(q, ((size_t)h * p.N + tok0 + tok) * kD + 16 * u + 4 * lg);
-            a4[mt] = make_float4(x.x * sc, x.y * sc, x.z * sc, x.w * sc);
-          } else {
-            a4[mt] = make_float4(0.f, 0.f, 0.f, 0.f);
-          }
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int kr = 16 * u + 4 * lg + e;
-        const float b0 = sS[kr * kLDS2 + li];
-        const float b1 = sS[kr * kLDS2 + 16 + li];
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const float a = elem(a4[mt], e);
-          acc[mt][0] = mfma4(a, b0, acc[mt][0]);
-          acc[mt][1] = mfma4(a, b1, acc[mt][1]);
-        }
-      }
-    }
-
-    // ---- stage B: v_new = U - W S (waves 0, 1)
-    if (wrows) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = 32 * wave + 16 * mt + 4 * lg + r;
-            const int n = 16 * nt + li;
-            sVn[tok * kLDS2 + n] = ws[kWsU + tok * kD + n0 + n] - acc[mt][nt][r];
-          }
-    }
-    __syncthreads();
-
-    // ---- stage C: o = Q*qs S + A v_new (waves 2, 3: tokens 32(w-2)..+31)
-    if (!wrows) {
-      const int tb = 32 * (wave - 2);
-      const int nu = (wave == 2) ? 2 : 4;
-      for (int u = 0; u < nu; ++u) {
-        float4 a4[2];
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          a4[mt] = load4(ws + kWsA, (size_t)(tb + 16 * mt + li) * 64 + 16 * u + 4 * lg);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int kt = 16 * u + 4 * lg + e;
-          const float b0 = sVn[kt * kLDS2 + li];
-          const float b1 = sVn[kt * kLDS2 + 16 + li];
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-            const float a = elem(a4[mt], e);
-            acc[mt][0] = mfma4(a, b0, acc[mt][0]);
-            acc[mt][1] = mfma4(a, b1, acc[mt][1]);
-          }
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = tb + 16 * mt + 4 * lg + r;
-            if (tok < len)
-              p.core[((size_t)h * p.core_hs + tok0 + tok) * kD + n0 + 16 * nt + li] = acc[mt][nt][r];
-          }
-    }
-
-    // ---- stage D: S <- e^{gL} S + (K*ks)^T v_new, wave w rows 32w..32w+31
-    const float gle = ws[kWsMisc];
-    f4v sacc[2][2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          sacc[mt][nt][r] = sS[(32 * wave + 16 * mt + 4 * lg + r) * kLDS2 + 16 * nt + li] * gle;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      float a[2][4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = 16 * u + 4 * lg + e;
-        const float ks = t < len ? ws[kWsKs + t] : 0.0f;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          a[mt][e] = t < len ? load1(k, ((size_t)h * p.N + tok0 + t) * kD + 32 * wave + 16 * mt + li) * ks
-                             : 0.0f;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = 16 * u + 4 * lg + e;
-        const float b0 = sVn[t * kLDS2 + li];
-        const float b1 = sVn[t * kLDS2 + 16 + li];
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          sacc[mt][0] = mfma4(a[mt][e], b0, sacc[mt][0]);
-          sacc[mt][1] = mfma4(a[mt][e], b1, sacc[mt][1]);
-        }
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          sS[(32 * wave + 16 * mt + 4 * lg + r) * kLDS2 + 16 * nt + li] = sacc[mt][nt][r];
-    __syncthreads();
-  }
 
   float* out = p.state + ((size_t)seq * p.H + h) * kD * kD;
   for (int i = tid; i < 128 * 32; i += 256) {
     const int r = i >> 5;
     const int c = i & 31;
-    out[r * kD + n0 + c] = sS[r * kLDS2 + c];
+    out[r * kD + n0 + c] = sST[c * kLdST + r];
   }
 }
 

@@ -55,7 +55,7 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
   const int seq = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int nh = p.nh;
   uint16_t* qkv = p.qkv + (long long)seq * p.qkv_stride;
 
