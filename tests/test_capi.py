@@ -1,0 +1,65 @@
+"""The C ABI surface, without a GPU: the library loads, exports every
+function include/spock_hip.h declares, and rejects invalid arguments before
+touching the device."""
+import ctypes as C
+import re
+
+import pytest
+
+from conftest import ROOT
+
+
+def _declared():
+    hdr = (ROOT / "include" / "spock_hip.h").read_text()
+    hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
+    return sorted(set(re.findall(r"\b(spk_[a-z0-9_]+)\s*\(", hdr)))
+
+
+def test_header_and_binding_agree():
+    from spock_amd import _lib
+    assert set(_declared()) == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    from spock_amd import _lib
+    lib = _lib.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.spk_abi_version() >> 16 == 1
+
+
+def test_struct_layouts_match_header():
+    from spock_amd import _lib
+    # field order and C sizes of the argument structs (x86-64 SysV)
+    assert C.sizeof(_lib.SpkMatvecDesc) == 32
+    assert _lib.SpkChunkArgs.q.offset == 32 and _lib.SpkChunkArgs.workspace_bytes.offset == 136
+    assert _lib.SpkDecodeArgs.qkv.offset == 24 and C.sizeof(_lib.SpkDecodeArgs) == 136
+
+
+def test_argument_errors_without_device():
+    from spock_amd import _lib
+    lib = _lib.lib()
+    assert lib.spk_chunk_prefill(None, None) == -1                      # SPK_ERR_NULL
+    a = _lib.SpkChunkArgs()
+    a.num_heads, a.total_tokens, a.key_dim, a.value_dim, a.chunk_size = 16, 10, 64, 128, 64
+    assert lib.spk_chunk_prefill(C.byref(a), None) == -2                # unsupported key_dim
+    assert b"key_dim" in lib.spk_last_error()
+    a.key_dim = 128
+    a.num_seqs = 1
+    assert lib.spk_chunk_prefill(C.byref(a), None) == -1                # out_state/workspace missing
+    assert lib.spk_matvec_f16(None, None, None, 4, 64, None) == -1
+    assert lib.spk_matvec_f16(1, 1, 1, 4, 63, None) == -2               # in_dim % 64
+    assert lib.spk_argmax_f16(1, 0, 1, None) == -2
+    d = _lib.SpkDecodeArgs()
+    d.batch, d.num_heads = 1, 16
+    assert lib.spk_deltanet_decode_step(C.byref(d), None) == -1         # qkv missing
+    assert lib.spk_chunk_prefill_workspace_size(16, 104, 1, 64) == (2 + 1) * 16 * 115200
+    assert lib.spk_lm_head_workspace_size(248320) % 256 == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from spock_amd import _lib
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(_lib.SpockError, match="no CPU fallback"):
+        _lib.lib()
