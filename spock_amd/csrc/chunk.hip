@@ -35,7 +35,6 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int kC = 64;
 constexpr int kD = 128;
 constexpr int kLDK = 132;  // LDS row stride (floats) of [64][128] tiles
-constexpr int kLDT = 68;   // LDS row stride of [64][64] tiles
 constexpr int kLdST = 132;  // LDS row stride of the transposed 32-column state tile
 constexpr int kLdVT = 68;   // LDS row stride of the transposed v_new tile
 // workspace record per (chunk, head), in floats.  Layouts are the ones the
@@ -115,22 +114,69 @@ __device__ __forceinline__ void locate_chunk(const ChunkParams& p, int gchunk, i
   len = 0;
 }
 
-constexpr int kIntraSmemFloats = 3 * 64 * kLDK + 2 * 64 * kLDT + 4 * 16 * 17 + 5 * 64;
+// Raw (unconverted) element types: operands are loaded early and converted
+// (and scaled) at use, so a load never stalls on arithmetic.
+template <typename TIn> struct RawOf;
+template <> struct RawOf<float> {
+  static __device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
+  static __device__ __forceinline__ float4 cvt4(const float4& r) { return r; }
+};
+template <> struct RawOf<uint16_t> {
+  // 4 halves kept as two 32-bit words in .x/.y of a float4
+  static __device__ __forceinline__ float4 ld4(const uint16_t* p, size_t i) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p + i);
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), 0.f, 0.f);
+  }
+  static __device__ __forceinline__ float4 cvt4(const float4& r) {
+    const uint32_t x = __float_as_uint(r.x), y = __float_as_uint(r.y);
+    return make_float4(spk::h2f((uint16_t)(x & 0xffffu)), spk::h2f((uint16_t)(x >> 16)),
+                       spk::h2f((uint16_t)(y & 0xffffu)), spk::h2f((uint16_t)(y >> 16)));
+  }
+};
+
+// V staged transposed in LDS: [128 value cols][64 tokens (+pad)], fp16 for
+// fp16 inputs (4 tokens = one 8-byte read) and fp32 otherwise.
+template <typename TIn> struct VStage;
+template <> struct VStage<uint16_t> {
+  static constexpr int kLd = 72;  // halves per row (144 B)
+  typedef uint16_t T;
+  static __device__ __forceinline__ void put(T* s, int col, int tok, const float4& raw, int e) {
+    const uint32_t w = __float_as_uint(e < 2 ? raw.x : raw.y);
+    s[col * kLd + tok] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
+  }
+  static __device__ __forceinline__ float4 get4(const T* s, int col, int tok) {
+    const uint2 u = *reinterpret_cast<const uint2*>(s + col * kLd + tok);
+    return make_float4(spk::h2f((uint16_t)(u.x & 0xffffu)), spk::h2f((uint16_t)(u.x >> 16)),
+                       spk::h2f((uint16_t)(u.y & 0xffffu)), spk::h2f((uint16_t)(u.y >> 16)));
+  }
+};
+template <> struct VStage<float> {
+  static constexpr int kLd = 68;
+  typedef float T;
+  static __device__ __forceinline__ void put(T* s, int col, int tok, const float4& raw, int e) {
+    s[col * kLd + tok] = elem(raw, e);
+  }
+  static __device__ __forceinline__ float4 get4(const T* s, int col, int tok) {
+    return *reinterpret_cast<const float4*>(s + col * kLd + tok);
+  }
+};
+
+// L and T are block lower triangular: the 10 blocks (I >= J) of 16x16 are
+// stored packed, block (I,J) at (I(I+1)/2 + J) * 256, row-major with stride 16.
+__device__ __forceinline__ int blk(int I, int J) { return (I * (I + 1) / 2 + J) * 256; }
+
+constexpr float kLog2e = 1.44269504f;
 
 template <typename TIn>
 __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
-  __shared__ float smem[kIntraSmemFloats];
-  float* sK = smem;              // [64][kLDK] K (L2-normalised if requested)
-  float* sQ = sK + 64 * kLDK;    // [64][kLDK] Q, later K * beta * e^gcum
-  float* sV = sQ + 64 * kLDK;    // [64][kLDK] V, later V * beta
-  float* sL = sV + 64 * kLDK;    // [64][kLDT] L
-  float* sT = sL + 64 * kLDT;    // [64][kLDT] T = (I + L)^-1
-  float* sX = sT + 64 * kLDT;    // [4][16][17] per-wave product scratch
-  float* sG = sX + 4 * 16 * 17;  // [64] gcum
-  float* sB = sG + 64;           // [64] beta
-  float* sIQ = sB + 64;          // [64] 1/|q| (or 1), later beta*e^gcum
-  float* sIK = sIQ + 64;         // [64] 1/|k| (or 1)
-  float* sKS = sIK + 64;         // [64] e^{gL - gcum}
+  typedef RawOf<TIn> R;
+  typedef VStage<TIn> VS;
+  __shared__ float sK[64 * kLDK];                       // K rows (normalised if requested)
+  __shared__ typename VS::T sVT[128 * VS::kLd];         // V^T
+  __shared__ float sL[10 * 256];                        // L blocks
+  __shared__ float sT[10 * 256];                        // T blocks, later T diag(beta [e^g])
+  __shared__ float sX[4 * 256];                         // per-wave product scratch
+  __shared__ float sG[64], sB[64], sE[64], sKS[64], sIQ[64], sIK[64];
 
   const int gchunk = blockIdx.x;
   const int h = blockIdx.y;
@@ -147,68 +193,92 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
   const TIn* v = static_cast<const TIn*>(p.v);
   float* ws = p.ws + ((size_t)gchunk * p.H + h) * kWsStride;
 
-  // ---- stage chunk rows; padding rows (t >= len) are zero, g = beta = 0
+  // ---- Q row block `wave` straight into MFMA A-operand registers (raw)
+  float4 qa[8];
+  {
+    const int row = 16 * wave + li;
+    const int rr = row < len ? row : 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) qa[u] = R::ld4(q, ((size_t)h * p.N + t0 + rr) * kD + 16 * u + 4 * lg);
+  }
+  // ---- stage K rows (fp32) and V^T; padding rows are zero, g = beta = 0
   for (int i = tid; i < 64 * 32; i += 256) {
     const int r = i >> 5;
     const int c = (i & 31) * 4;
-    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), kv = qv, vv = qv;
+    float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 vr = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < len) {
       const size_t off = ((size_t)h * p.N + t0 + r) * kD + c;
-      qv = load4(q, off);
-      kv = load4(k, off);
-      vv = load4(v, off);
+      kv = R::cvt4(R::ld4(k, off));
+      vr = R::ld4(v, off);
     }
-    *reinterpret_cast<float4*>(&sQ[r * kLDK + c]) = qv;
     *reinterpret_cast<float4*>(&sK[r * kLDK + c]) = kv;
-    *reinterpret_cast<float4*>(&sV[r * kLDK + c]) = vv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) VS::put(sVT, c + e, r, vr, e);
   }
   if (tid < 64) {
     const bool valid = tid < len;
     sG[tid] = valid ? p.g[(size_t)h * p.N + t0 + tid] : 0.0f;
     sB[tid] = valid ? p.beta[(size_t)h * p.N + t0 + tid] : 0.0f;
   }
-  for (int i = tid; i < 64 * kLDT; i += 256) {
-    sL[i] = 0.0f;
-    sT[i] = 0.0f;
-  }
   __syncthreads();
-  if (tid == 0) {  // running cumulative sum (deltanet_chunk.cpp:137-142)
+
+  // ---- gcum (running sum in token order, deltanet_chunk.cpp:137-142) and,
+  // if requested, inverse L2 norms (eps inside the sqrt, :27-39)
+  if (tid == 0) {
+    float gv[64];
+#pragma unroll
+    for (int r = 0; r < 64; r += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(&sG[r]);
+      gv[r] = x.x; gv[r + 1] = x.y; gv[r + 2] = x.z; gv[r + 3] = x.w;
+    }
     float run = 0.0f;
+#pragma unroll
     for (int r = 0; r < 64; ++r) {
-      run = run + sG[r];
-      sG[r] = run;
+      run = run + gv[r];
+      gv[r] = run;
     }
+#pragma unroll
+    for (int r = 0; r < 64; r += 4)
+      *reinterpret_cast<float4*>(&sG[r]) = make_float4(gv[r], gv[r + 1], gv[r + 2], gv[r + 3]);
   }
-  if (p.l2) {  // deltanet_chunk.cpp:27-39, eps inside the sqrt
+  if (p.l2 && tid >= 64 && tid < 192) {
+    // rows of Q come from global (this block owns them only as MFMA operands),
+    // so their norms are taken from global too
+    const int r = (tid - 64) & 63;
+    float ss = 0.0f;
     if (tid < 128) {
-      const int r = tid & 63;
-      const float* row = (tid < 64 ? sQ : sK) + r * kLDK;
-      float ss = 0.0f;
-      for (int d = 0; d < kD; ++d) ss = ss + row[d] * row[d];
-      (tid < 64 ? sIQ : sIK)[r] = 1.0f / sqrtf(ss + 1e-6f);
+      const int rr = r < len ? r : 0;
+      for (int c = 0; c < kD; c += 4) {
+        const float4 x = R::cvt4(R::ld4(q, ((size_t)h * p.N + t0 + rr) * kD + c));
+        ss = ss + x.x * x.x; ss = ss + x.y * x.y; ss = ss + x.z * x.z; ss = ss + x.w * x.w;
+      }
+      sIQ[r] = 1.0f / sqrtf(ss + 1e-6f);
+    } else {
+      for (int c = 0; c < kD; ++c) ss = ss + sK[r * kLDK + c] * sK[r * kLDK + c];
+      sIK[r] = 1.0f / sqrtf(ss + 1e-6f);
     }
-  } else if (tid < 64) {
-    sIQ[tid] = 1.0f;
-    sIK[tid] = 1.0f;
   }
   __syncthreads();
   if (p.l2) {
     for (int i = tid; i < 64 * kD; i += 256) {
       const int r = i >> 7;
-      const int c = i & 127;
-      sQ[r * kLDK + c] *= sIQ[r];
-      sK[r * kLDK + c] *= sIK[r];
+      sK[r * kLDK + (i & 127)] *= sIK[r];
     }
   }
-  __syncthreads();
   const float gL = sG[63];
   if (tid < 64) {
-    ws[kWsQs + tid] = (sIQ[tid] * p.q_scale) * expf(sG[tid]);  // Q is re-read raw
-    sKS[tid] = expf(gL - sG[tid]);  // decay to the chunk end (sK is normalised)
+    const float iq = p.l2 ? sIQ[tid] : 1.0f;
+    const float eg = expf(sG[tid]);
+    sE[tid] = eg;
+    sKS[tid] = expf(gL - sG[tid]);
+    ws[kWsQs + tid] = (iq * p.q_scale) * eg;  // the scan re-reads Q raw
+    if (!p.l2) sIQ[tid] = 1.0f;
   }
   if (tid == 0) ws[kWsMisc] = expf(gL);
   __syncthreads();
-  // (K * e^{gL-g})^T, row kd = 64 tokens: 16 lanes write one 256-byte row
+
+  // ---- (K e^{gL-g})^T, 16 lanes per 256-byte row
   for (int i = tid; i < 128 * 16; i += 256) {
     const int kd = i >> 4;
     const int t = (i & 15) * 4;
@@ -217,70 +287,67 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
                     sK[(t + 2) * kLDK + kd] * sKS[t + 2], sK[(t + 3) * kLDK + kd] * sKS[t + 3]);
   }
 
-  // ---- K K^T -> L (into LDS) and Q K^T -> A (into the workspace); 20 tiles
-  for (int tt = wave; tt < 20; tt += 4) {
-    const bool isq = tt >= 10;
-    const int t = isq ? tt - 10 : tt;
-    const int I = t >= 6 ? 3 : t >= 3 ? 2 : t >= 1 ? 1 : 0;
-    const int J = t - I * (I + 1) / 2;
-    const float* A = isq ? sQ : sK;
-    f4v acc = {0.f, 0.f, 0.f, 0.f};
+  // ---- K K^T row block 3-w -> L, Q K^T row block w -> A: 5 tiles per wave
+  {
+    const int Ik = 3 - wave;
+    const float iq = sIQ[16 * wave + li];
+    float4 qf[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const float4 a4 = *reinterpret_cast<const float4*>(&A[(16 * I + li) * kLDK + 16 * u + 4 * lg]);
-      const float4 b4 = *reinterpret_cast<const float4*>(&sK[(16 * J + li) * kLDK + 16 * u + 4 * lg]);
-      acc = mfma4(a4.x, b4.x, acc);
-      acc = mfma4(a4.y, b4.y, acc);
-      acc = mfma4(a4.z, b4.z, acc);
-      acc = mfma4(a4.w, b4.w, acc);
+      const float4 x = R::cvt4(qa[u]);
+      qf[u] = make_float4(x.x * iq, x.y * iq, x.z * iq, x.w * iq);
     }
+    for (int tt = 0; tt < 5; ++tt) {
+      const bool isq = tt > 3 - wave;
+      const int I = isq ? wave : Ik;
+      const int J = isq ? tt - (4 - wave) : tt;
+      f4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * I + 4 * lg + r;
+      for (int u = 0; u < 8; ++u) {
+        const float4 b4 = *reinterpret_cast<const float4*>(&sK[(16 * J + li) * kLDK + 16 * u + 4 * lg]);
+        const float4 a4 = isq ? qf[u] : *reinterpret_cast<const float4*>(&sK[(16 * I + li) * kLDK + 16 * u + 4 * lg]);
+        acc = mfma4(a4.x, b4.x, acc);
+        acc = mfma4(a4.y, b4.y, acc);
+        acc = mfma4(a4.z, b4.z, acc);
+        acc = mfma4(a4.w, b4.w, acc);
+      }
       const int j = 16 * J + li;
-      if (!isq) {
-        if (j < i) sL[i * kLDT + j] = sB[i] * acc[r] * expf(sG[i] - sG[j]);
-      } else {
-        ws[kWsA + i * 64 + j] = (j <= i) ? acc[r] * p.q_scale * expf(sG[i] - sG[j]) : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * lg + r;
+        const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
+        if (!isq) {
+          sL[blk(I, J) + (4 * lg + r) * 16 + li] = (j < i) ? sB[i] * acc[r] * dec : 0.0f;
+        } else {
+          ws[kWsA + i * 64 + j] = (j <= i) ? acc[r] * p.q_scale * dec : 0.0f;
+        }
       }
     }
-  }
-  for (int e = tid; e < 64 * 64; e += 256) {  // strictly-upper blocks of A are zero
-    const int i = e >> 6;
-    const int j = e & 63;
-    if ((j >> 4) > (i >> 4)) ws[kWsA + e] = 0.0f;
+    // strictly-upper blocks of this wave's A row block are zero
+    for (int e = lane; e < (3 - wave) * 256; e += 64)
+      ws[kWsA + (16 * wave + (e >> 4) % 16) * 64 + 16 * (wave + 1) + (e >> 8) * 16 + (e & 15)] = 0.0f;
   }
   __syncthreads();
 
-  // ---- B operands of U and W: V*beta in place, Q slot <- K*beta*e^gcum
-  if (tid < 64) sIQ[tid] = sB[tid] * expf(sG[tid]);
-  __syncthreads();
-  for (int i = tid; i < 64 * kD; i += 256) {
-    const int r = i >> 7;
-    const int c = i & 127;
-    sV[r * kLDK + c] = sV[r * kLDK + c] * sB[r];
-    sQ[r * kLDK + c] = sK[r * kLDK + c] * sIQ[r];
-  }
-
-  // ---- diagonal 16x16 blocks of T: lane j < 16 of wave w solves column j of
-  // block w in registers, T_ij = -sum_{m<i} L_im T_mj (T_mj = 0 for m < j).
+  // ---- diagonal blocks of T: lane j < 16 of wave w solves column j of block w
   if (li == lane) {
-    const int b0 = 16 * wave;
+    const float* Lb = sL + blk(wave, wave);
     const int j = lane;
     float tc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       float s = 0.0f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) s = __builtin_fmaf(sL[(b0 + i) * kLDT + b0 + m], tc[m], s);
+      for (int m = 0; m < i; ++m) s = __builtin_fmaf(Lb[i * 16 + m], tc[m], s);
       tc[i] = (i == j) ? 1.0f : (i < j ? 0.0f : -s);
     }
+    float* Tb = sT + blk(wave, wave);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sT[(b0 + i) * kLDT + b0 + j] = tc[i];
+    for (int i = 0; i < 16; ++i) Tb[i * 16 + j] = tc[i];
   }
   __syncthreads();
 
-  // ---- off-diagonal blocks, by distance d = I - J
+  // ---- off-diagonal blocks by distance d = I - J: T_IJ = -T_II sum_M L_IM T_MJ
   for (int d = 1; d < 4; ++d) {
     const bool active = wave < 4 - d;
     const int J = wave;
@@ -289,86 +356,83 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
       f4v acc = {0.f, 0.f, 0.f, 0.f};
       for (int M = J; M < I; ++M) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const float a = sL[(16 * I + li) * kLDT + 16 * M + 4 * s + lg];
-          const float b = sT[(16 * M + 4 * s + lg) * kLDT + 16 * J + li];
-          acc = mfma4(a, b, acc);
-        }
+        for (int s = 0; s < 4; ++s)
+          acc = mfma4(sL[blk(I, M) + li * 16 + 4 * s + lg], sT[blk(M, J) + (4 * s + lg) * 16 + li], acc);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sX[wave * 272 + (4 * lg + r) * 17 + li] = acc[r];
+      for (int r = 0; r < 4; ++r) sX[wave * 256 + (4 * lg + r) * 16 + li] = acc[r];
     }
     __syncthreads();
     if (active) {
       f4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float a = sT[(16 * I + li) * kLDT + 16 * I + 4 * s + lg];
-        const float b = sX[wave * 272 + (4 * s + lg) * 17 + li];
-        acc = mfma4(a, b, acc);
-      }
+      for (int s = 0; s < 4; ++s)
+        acc = mfma4(sT[blk(I, I) + li * 16 + 4 * s + lg], sX[wave * 256 + (4 * s + lg) * 16 + li], acc);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sT[(16 * I + 4 * lg + r) * kLDT + 16 * J + li] = -acc[r];
+      for (int r = 0; r < 4; ++r) sT[blk(I, J) + (4 * lg + r) * 16 + li] = -acc[r];
     }
     __syncthreads();
   }
 
-  // ---- U = T (V*beta) (stored transposed), W = T (K*beta*e^g); wave w owns
-  // column tiles 2w, 2w+1
-  for (int mat = 0; mat < 2; ++mat) {
-    const float* Bm = mat == 0 ? sV : sQ;
-    for (int jj = 0; jj < 2; ++jj) {
-      const int J = 2 * wave + jj;
-      for (int I = 0; I < 4; ++I) {
-        f4v acc = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < 4 * (I + 1); ++s) {
-          const float a = sT[(16 * I + li) * kLDT + 4 * s + lg];
-          const float b = Bm[(4 * s + lg) * kLDK + 16 * J + li];
-          acc = mfma4(a, b, acc);
-        }
-        if (mat == 0) {
-          *reinterpret_cast<float4*>(ws + kWsUT + (16 * J + li) * 64 + 16 * I + 4 * lg) =
-              make_float4(acc[0], acc[1], acc[2], acc[3]);
-        } else {
+  // ---- columns of T scaled by beta, then U = (T diag(beta)) V, stored as U^T
+  for (int e = tid; e < 10 * 256; e += 256) {
+    const int b = e >> 8;
+    const int I = b >= 6 ? 3 : b >= 3 ? 2 : b >= 1 ? 1 : 0;
+    const int J = b - I * (I + 1) / 2;
+    sT[e] *= sB[16 * J + (e & 15)];
+  }
+  __syncthreads();
 #pragma unroll
-          for (int r = 0; r < 4; ++r) ws[kWsW + (16 * I + 4 * lg + r) * kD + 16 * J + li] = acc[r];
-        }
+  for (int jj = 0; jj < 2; ++jj) {
+    const int n = 16 * (2 * wave + jj) + li;
+    for (int I = 0; I < 4; ++I) {
+      f4v acc = {0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u <= I; ++u) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&sT[blk(I, u) + li * 16 + 4 * lg]);
+        const float4 b4 = VS::get4(sVT, n, 16 * u + 4 * lg);
+        acc = mfma4(a4.x, b4.x, acc);
+        acc = mfma4(a4.y, b4.y, acc);
+        acc = mfma4(a4.z, b4.z, acc);
+        acc = mfma4(a4.w, b4.w, acc);
       }
+      *reinterpret_cast<float4*>(ws + kWsUT + n * 64 + 16 * I + 4 * lg) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
+  }
+  __syncthreads();
+  // ---- columns scaled by e^gcum, then W = (T diag(beta e^g)) K
+  for (int e = tid; e < 10 * 256; e += 256) {
+    const int b = e >> 8;
+    const int I = b >= 6 ? 3 : b >= 3 ? 2 : b >= 1 ? 1 : 0;
+    const int J = b - I * (I + 1) / 2;
+    sT[e] *= sE[16 * J + (e & 15)];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const int n = 16 * (2 * wave + jj) + li;
+    for (int I = 0; I < 4; ++I) {
+      f4v acc = {0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u <= I; ++u) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&sT[blk(I, u) + li * 16 + 4 * lg]);
+        const int t = 16 * u + 4 * lg;
+        acc = mfma4(a4.x, sK[t * kLDK + n], acc);
+        acc = mfma4(a4.y, sK[(t + 1) * kLDK + n], acc);
+        acc = mfma4(a4.z, sK[(t + 2) * kLDK + n], acc);
+        acc = mfma4(a4.w, sK[(t + 3) * kLDK + n], acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ws[kWsW + (16 * I + 4 * lg + r) * kD + n] = acc[r];
     }
   }
 }
 
-// Raw (unconverted) element types for operands loaded one chunk ahead: the
-// conversion and scaling happen at use, so a prefetch never waits on its load.
-template <typename TIn> struct RawOf;
-template <> struct RawOf<float> {
-  static __device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
-  static __device__ __forceinline__ float4 cvt4(const float4& r) { return r; }
-  static __device__ __forceinline__ float ld1(const float* p, size_t i) { return p[i]; }
-  static __device__ __forceinline__ float cvt1(float r) { return r; }
-};
-template <> struct RawOf<uint16_t> {
-  // 4 halves kept as two 32-bit words in .x/.y of a float4
-  static __device__ __forceinline__ float4 ld4(const uint16_t* p, size_t i) {
-    const uint2 u = *reinterpret_cast<const uint2*>(p + i);
-    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), 0.f, 0.f);
-  }
-  static __device__ __forceinline__ float4 cvt4(const float4& r) {
-    const uint32_t x = __float_as_uint(r.x), y = __float_as_uint(r.y);
-    return make_float4(spk::h2f((uint16_t)(x & 0xffffu)), spk::h2f((uint16_t)(x >> 16)),
-                       spk::h2f((uint16_t)(y & 0xffffu)), spk::h2f((uint16_t)(y >> 16)));
-  }
-  static __device__ __forceinline__ float ld1(const uint16_t* p, size_t i) { return __uint_as_float((uint32_t)p[i]); }
-  static __device__ __forceinline__ float cvt1(float r) { return spk::h2f((uint16_t)__float_as_uint(r)); }
-};
-
 // One wavefront's operands of one chunk, loaded a chunk ahead.
 struct StateRegs {
-  float4 a[8][2];   // stage A rows: W (waves 0,1) or raw Q (waves 2,3)
-  float4 at[4][2];  // stage C: A rows (waves 2,3)
-  float4 kd[4][2];  // stage D: (K*ks)^T rows, 4 tokens each
-  float4 u[2][2];   // stage B: U^T, 4 tokens each (waves 0,1)
-  float qs[2];      // stage A: Q scale per row (waves 2,3)
+  float4 a[8];      // stage A row block: W (v_new waves) or raw Q (output waves)
+  float4 at[4];     // stage C: A rows (output waves)
+  float4 kd[4];     // stage D: (K*ks)^T rows, 4 tokens each
+  float4 u[2];      // stage B: U^T, 4 tokens each (v_new waves)
+  float qs;         // stage A: Q scale of this lane's row (output waves)
   float gle;        // e^{gcum_last}
 };
 
@@ -387,19 +451,18 @@ __device__ __forceinline__ int lpt_sequence(const ChunkParams& p, int slot) {
   return slot;
 }
 
-// Sequential chunk scan of one workgroup for one wavefront role.  WROLE:
-// waves 0,1 compute v_new = U - W S for token blocks {2w, 2w+1}; otherwise
-// waves 2,3 compute the outputs o = Q*qs S + A v_new for token blocks
-// {0,3} / {1,2} (5 of the 10 blocks of the triangular A v_new each).  All
-// waves update 32 rows of the state.  Both roles execute the same barriers.
+// Sequential chunk scan of one workgroup (8 wavefronts, two per SIMD) for one
+// wavefront role.  WROLE (waves 0-3): v_new = U - W S for token block w.
+// Output role (waves 4-7): o = Q*qs S + A v_new for token block w-4.  Every
+// wave also updates state rows 16w..16w+15.  A SIMD holds waves s and s+4, one
+// of each role.  Both roles execute the same barriers.
 template <typename TIn, bool WROLE>
 __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, float* sVT, int h,
                                            int n0, int t_begin, int L, int co, int wave, int lane) {
   typedef RawOf<TIn> R;
   const int li = lane & 15;
   const int lg = lane >> 4;
-  const int tb0 = WROLE ? 2 * wave : (wave == 2 ? 0 : 1);
-  const int tb1 = WROLE ? 2 * wave + 1 : (wave == 2 ? 3 : 2);
+  const int M = WROLE ? wave : wave - 4;  // token block of stages A-C
   const TIn* q = static_cast<const TIn*>(p.q);
   const int nchunks = (L + kC - 1) / kC;
 
@@ -409,33 +472,27 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
     const int tok0 = t_begin + c * kC;
     const int len = min(kC, L - c * kC);
     const float* ws = p.ws + ((size_t)(co + c) * p.H + h) * kWsStride;
+    const int tok = 16 * M + li;
+    if (WROLE) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int M = mt ? tb1 : tb0;
-      const int tok = 16 * M + li;
-      if (WROLE) {
+      for (int u = 0; u < 8; ++u)
+        g.a[u] = *reinterpret_cast<const float4*>(ws + kWsW + tok * kD + 16 * u + 4 * lg);
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          g.a[u][mt] = *reinterpret_cast<const float4*>(ws + kWsW + tok * kD + 16 * u + 4 * lg);
+      for (int nt = 0; nt < 2; ++nt)
+        g.u[nt] = *reinterpret_cast<const float4*>(ws + kWsUT + (n0 + 16 * nt + li) * 64 + 16 * M + 4 * lg);
+    } else {
+      const int row = tok < len ? tok : 0;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          g.u[mt][nt] = *reinterpret_cast<const float4*>(ws + kWsUT + (n0 + 16 * nt + li) * 64 + 16 * M + 4 * lg);
-      } else {
-        const int row = tok < len ? tok : 0;
+      for (int u = 0; u < 8; ++u)
+        g.a[u] = R::ld4(q, ((size_t)h * p.N + tok0 + row) * kD + 16 * u + 4 * lg);
+      g.qs = ws[kWsQs + tok];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          g.a[u][mt] = R::ld4(q, ((size_t)h * p.N + tok0 + row) * kD + 16 * u + 4 * lg);
-        g.qs[mt] = ws[kWsQs + tok];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (u <= M) g.at[u][mt] = *reinterpret_cast<const float4*>(ws + kWsA + tok * 64 + 16 * u + 4 * lg);
-      }
+      for (int u = 0; u < 4; ++u)
+        if (u <= M) g.at[u] = *reinterpret_cast<const float4*>(ws + kWsA + tok * 64 + 16 * u + 4 * lg);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-        g.kd[u][mt] = *reinterpret_cast<const float4*>(ws + kWsKdT + (32 * wave + 16 * mt + li) * 64 + 16 * u + 4 * lg);
+      g.kd[u] = *reinterpret_cast<const float4*>(ws + kWsKdT + (16 * wave + li) * 64 + 16 * u + 4 * lg);
     g.gle = ws[kWsMisc];
   };
 
@@ -444,113 +501,83 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
     const int tok0 = t_begin + c * kC;
     const int len = min(kC, L - c * kC);
 
-    // ---- stage A: rows of [W ; Q*qs] times S
-    f4v acc[2][2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f4v{0.f, 0.f, 0.f, 0.f};
-    float qsc[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) qsc[mt] = (16 * (mt ? tb1 : tb0) + li) < len ? cur.qs[mt] : 0.0f;
+    // ---- stage A: row block M of [W ; Q*qs] times S
+    f4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    const float qsc = (16 * M + li) < len ? cur.qs : 0.0f;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      float4 av[2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        if (WROLE) {
-          av[mt] = cur.a[u][mt];
-        } else {
-          const float4 x = R::cvt4(cur.a[u][mt]);
-          av[mt] = make_float4(x.x * qsc[mt], x.y * qsc[mt], x.z * qsc[mt], x.w * qsc[mt]);
-        }
+      float4 av;
+      if (WROLE) {
+        av = cur.a[u];
+      } else {
+        const float4 x = R::cvt4(cur.a[u]);
+        av = make_float4(x.x * qsc, x.y * qsc, x.z * qsc, x.w * qsc);
       }
       const float4 b0 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * u + 4 * lg]);
       const float4 b1 = *reinterpret_cast<const float4*>(&sST[(16 + li) * kLdST + 16 * u + 4 * lg]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const float a = elem(av[mt], e);
-          acc[mt][0] = mfma4(a, elem(b0, e), acc[mt][0]);
-          acc[mt][1] = mfma4(a, elem(b1, e), acc[mt][1]);
-        }
+        acc0 = mfma4(elem(av, e), elem(b0, e), acc0);
+        acc1 = mfma4(elem(av, e), elem(b1, e), acc1);
       }
     }
 
     // ---- stage B: v_new = U - W S
     if (WROLE) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const int tok = 16 * (mt ? tb1 : tb0) + 4 * lg;
-          *reinterpret_cast<float4*>(&sVT[(16 * nt + li) * kLdVT + tok]) =
-              make_float4(cur.u[mt][nt].x - acc[mt][nt][0], cur.u[mt][nt].y - acc[mt][nt][1],
-                          cur.u[mt][nt].z - acc[mt][nt][2], cur.u[mt][nt].w - acc[mt][nt][3]);
-        }
+      const int tok = 16 * M + 4 * lg;
+      *reinterpret_cast<float4*>(&sVT[li * kLdVT + tok]) =
+          make_float4(cur.u[0].x - acc0[0], cur.u[0].y - acc0[1], cur.u[0].z - acc0[2], cur.u[0].w - acc0[3]);
+      *reinterpret_cast<float4*>(&sVT[(16 + li) * kLdVT + tok]) =
+          make_float4(cur.u[1].x - acc1[0], cur.u[1].y - acc1[1], cur.u[1].z - acc1[2], cur.u[1].w - acc1[3]);
     }
     __syncthreads();
 
     // ---- stage C: o = Q*qs S + A v_new
     if (!WROLE) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int M = mt ? tb1 : tb0;
+      for (int u = 0; u < 4; ++u) {
+        if (u <= M) {
+          const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
+          const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (u <= M) {
-            const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
-            const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float a = elem(cur.at[u][mt], e);
-              acc[mt][0] = mfma4(a, elem(b0, e), acc[mt][0]);
-              acc[mt][1] = mfma4(a, elem(b1, e), acc[mt][1]);
-            }
+          for (int e = 0; e < 4; ++e) {
+            acc0 = mfma4(elem(cur.at[u], e), elem(b0, e), acc0);
+            acc1 = mfma4(elem(cur.at[u], e), elem(b1, e), acc1);
           }
         }
+      }
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = 16 * M + 4 * lg + r;
-            if (tok < len)
-              p.core[((size_t)h * p.core_hs + tok0 + tok) * kD + n0 + 16 * nt + li] = acc[mt][nt][r];
-          }
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 16 * M + 4 * lg + r;
+        if (tok < len) {
+          float* o = p.core + ((size_t)h * p.core_hs + tok0 + tok) * kD + n0 + li;
+          o[0] = acc0[r];
+          o[16] = acc1[r];
+        }
       }
     }
 
-    // ---- stage D: S <- e^{gL} S + (K*ks)^T v_new, rows 32w..32w+31
-    f4v sacc[2][2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const float4 s4 = *reinterpret_cast<const float4*>(
-            &sST[(16 * nt + li) * kLdST + 32 * wave + 16 * mt + 4 * lg]);
-        sacc[mt][nt] = f4v{s4.x * cur.gle, s4.y * cur.gle, s4.z * cur.gle, s4.w * cur.gle};
-      }
+    // ---- stage D: S <- e^{gL} S + (K*ks)^T v_new, rows 16w..16w+15
+    const float4 s0 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * wave + 4 * lg]);
+    const float4 s1 = *reinterpret_cast<const float4*>(&sST[(16 + li) * kLdST + 16 * wave + 4 * lg]);
+    f4v sacc0 = {s0.x * cur.gle, s0.y * cur.gle, s0.z * cur.gle, s0.w * cur.gle};
+    f4v sacc1 = {s1.x * cur.gle, s1.y * cur.gle, s1.z * cur.gle, s1.w * cur.gle};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
       const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const float a = elem(cur.kd[u][mt], e);
-          sacc[mt][0] = mfma4(a, elem(b0, e), sacc[mt][0]);
-          sacc[mt][1] = mfma4(a, elem(b1, e), sacc[mt][1]);
-        }
+        sacc0 = mfma4(elem(cur.kd[u], e), elem(b0, e), sacc0);
+        sacc1 = mfma4(elem(cur.kd[u], e), elem(b1, e), sacc1);
       }
     }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-        *reinterpret_cast<float4*>(&sST[(16 * nt + li) * kLdST + 32 * wave + 16 * mt + 4 * lg]) =
-            make_float4(sacc[mt][nt][0], sacc[mt][nt][1], sacc[mt][nt][2], sacc[mt][nt][3]);
+    // every wave has read sST (stage A) before the barrier above and only its
+    // own rows here, so the rows can be replaced in place
+    *reinterpret_cast<float4*>(&sST[li * kLdST + 16 * wave + 4 * lg]) =
+        make_float4(sacc0[0], sacc0[1], sacc0[2], sacc0[3]);
+    *reinterpret_cast<float4*>(&sST[(16 + li) * kLdST + 16 * wave + 4 * lg]) =
+        make_float4(sacc1[0], sacc1[1], sacc1[2], sacc1[3]);
     __syncthreads();
   };
 
@@ -569,7 +596,7 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
 }
 
 template <typename TIn>
-__global__ __launch_bounds__(256, 1) void chunk_state_kernel(ChunkParams p) {
+__global__ __launch_bounds__(512, 1) void chunk_state_kernel(ChunkParams p) {
   // S tile and v_new stored transposed ([column][contraction index]) so one
   // ds_read_b128 feeds four consecutive MFMA steps; strides 132 and 68 keep
   // the 8-lane groups of a b128 access on distinct banks.
@@ -606,20 +633,20 @@ __global__ __launch_bounds__(256, 1) void chunk_state_kernel(ChunkParams p) {
   }
 
   const float* init = p.init ? p.init + ((size_t)seq * p.H + h) * kD * kD : nullptr;
-  for (int i = tid; i < 128 * 32; i += 256) {
+  for (int i = tid; i < 128 * 32; i += 512) {
     const int r = i >> 5;
     const int c = i & 31;
     sST[c * kLdST + r] = init ? init[r * kD + n0 + c] : 0.0f;
   }
 
-  if (wave < 2)
+  if (wave < 4)
     state_scan<TIn, true>(p, sST, sVT, h, n0, t_begin, L, co, wave, lane);
   else
     state_scan<TIn, false>(p, sST, sVT, h, n0, t_begin, L, co, wave, lane);
   __syncthreads();
 
   float* out = p.state + ((size_t)seq * p.H + h) * kD * kD;
-  for (int i = tid; i < 128 * 32; i += 256) {
+  for (int i = tid; i < 128 * 32; i += 512) {
     const int r = i >> 5;
     const int c = i & 31;
     out[r * kD + n0 + c] = sST[c * kLdST + r];
@@ -728,9 +755,9 @@ extern "C" int spk_chunk_prefill(const SpkChunkArgs* a, spk_stream_t stream) {
   }
   dim3 g2((unsigned)(4 * p.H * S));
   if (a->input_dtype == SPK_F32)
-    hipLaunchKernelGGL(chunk_state_kernel<float>, g2, dim3(256), 0, s, p);
+    hipLaunchKernelGGL(chunk_state_kernel<float>, g2, dim3(512), 0, s, p);
   else
-    hipLaunchKernelGGL(chunk_state_kernel<uint16_t>, g2, dim3(256), 0, s, p);
+    hipLaunchKernelGGL(chunk_state_kernel<uint16_t>, g2, dim3(512), 0, s, p);
   return spk::check_launch("spk_chunk_prefill (state)");
 }
 
