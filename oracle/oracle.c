@@ -490,17 +490,19 @@ void orc_conv_l2_qk(size_t conv_dim, size_t ks, size_t key_total, size_t num_hea
   }
 }
 
-/* Column reduction used by the HIP decode kernel: rows split in 8 contiguous
- * groups of 16, fma-accumulated in row order from 0, then combined as
- * ((p0+p1)+(p2+p3))+((p4+p5)+(p6+p7)). */
+/* Column reduction used by the HIP decode kernel: rows split in 32 contiguous
+ * groups of 4, fma-accumulated from 0 in row order, then a balanced pairwise
+ * tree over the 32 partials, adjacent pairs first. */
 static float col_dot128(const float* S, size_t j, const float* x) {
-  float p[8];
-  for (size_t gi = 0; gi < 8; ++gi) {
+  float p[32];
+  for (size_t gi = 0; gi < 32; ++gi) {
     float acc = 0.0f;
-    for (size_t i = gi * 16; i < gi * 16 + 16; ++i) acc = fmaf(S[i * 128 + j], x[i], acc);
+    for (size_t i = gi * 4; i < gi * 4 + 4; ++i) acc = fmaf(S[i * 128 + j], x[i], acc);
     p[gi] = acc;
   }
-  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  for (size_t n = 32; n > 1; n >>= 1)
+    for (size_t i = 0; i < n / 2; ++i) p[i] = p[2 * i] + p[2 * i + 1];
+  return p[0];
 }
 
 /* One head of the recurrence (deltanet_recurrent_gbeta_norm_gate.comp:243-291):

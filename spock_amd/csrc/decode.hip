@@ -14,8 +14,8 @@
 // Reduction orders (fixed, and restated by the CPU oracle):
 //   conv taps summed i = 0..3; L2 / RMS sums use the shaders' 128-wide tree
 //   (s[l] += s[l+64], then 32..1: lane-local add, then wave shuffles);
-//   S^T x per column: 8 row groups of 16 rows, fma-accumulated from 0 in row
-//   order, combined ((p0+p1)+(p2+p3))+((p4+p5)+(p6+p7)).
+//   S^T x per column: 32 row groups of 4 rows, fma-accumulated from 0 in row
+//   order, then combined by a balanced pairwise tree (adjacent pairs first).
 #include "capi_common.hpp"
 #include "numerics.hpp"
 
@@ -42,8 +42,17 @@ struct DecodeParams {
   const float* norm_w;
 };
 
-__device__ __forceinline__ float tree8(const float* p) {
-  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+// Balanced pairwise tree over 32 partials in LDS column `col` of s_part
+// (adjacent pairs first: level 1 sums (0,1), (2,3), ...).
+__device__ __forceinline__ float tree32(const float (*part)[128], int col) {
+  float v[32];
+#pragma unroll
+  for (int r = 0; r < 32; ++r) v[r] = part[r][col];
+#pragma unroll
+  for (int n = 32; n > 1; n >>= 1)
+#pragma unroll
+    for (int i = 0; i < n / 2; ++i) v[i] = v[2 * i] + v[2 * i + 1];
+  return v[0];
 }
 
 // CONV: run the conv/L2 phase.  REC: run the recurrence.  GB_TAIL: g/beta from
@@ -60,10 +69,10 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
   uint16_t* qkv = p.qkv + (long long)seq * p.qkv_stride;
 
   __shared__ float s_q[128], s_k[128], s_v[128], s_delta[128];
-  __shared__ float s_part[8][128];
+  __shared__ float s_part[32][128];
 
   const int c4 = tid & 31;  // owns columns 4*c4 .. 4*c4+3
-  const int rg = tid >> 5;  // owns rows 16*rg .. 16*rg+15
+  const int rq = tid >> 5;  // owns row groups 4*rq .. 4*rq+3, i.e. rows 16*rq .. 16*rq+15
   float4 S[16];
   float* st_head = nullptr;
   if (REC) {
@@ -71,7 +80,7 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
     st_head = st_seq + (long long)h * 128 * 128;
 #pragma unroll
     for (int m = 0; m < 16; ++m)
-      S[m] = *reinterpret_cast<const float4*>(st_head + (rg * 16 + m) * 128 + c4 * 4);
+      S[m] = *reinterpret_cast<const float4*>(st_head + (rq * 16 + m) * 128 + c4 * 4);
   }
 
   if (CONV) {
@@ -150,61 +159,58 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  // decay + kv partials
+  // decay + kv partials, one per 4-row group
   const float eg = spk::expf_det(g);
-  float kp0 = 0.f, kp1 = 0.f, kp2 = 0.f, kp3 = 0.f;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const float ki = s_k[rg * 16 + m];
-    S[m].x = S[m].x * eg;
-    S[m].y = S[m].y * eg;
-    S[m].z = S[m].z * eg;
-    S[m].w = S[m].w * eg;
-    kp0 = __builtin_fmaf(S[m].x, ki, kp0);
-    kp1 = __builtin_fmaf(S[m].y, ki, kp1);
-    kp2 = __builtin_fmaf(S[m].z, ki, kp2);
-    kp3 = __builtin_fmaf(S[m].w, ki, kp3);
+  for (int gq = 0; gq < 4; ++gq) {
+    float kp0 = 0.f, kp1 = 0.f, kp2 = 0.f, kp3 = 0.f;
+#pragma unroll
+    for (int m = 4 * gq; m < 4 * gq + 4; ++m) {
+      const float ki = s_k[rq * 16 + m];
+      S[m].x = S[m].x * eg;
+      S[m].y = S[m].y * eg;
+      S[m].z = S[m].z * eg;
+      S[m].w = S[m].w * eg;
+      kp0 = __builtin_fmaf(S[m].x, ki, kp0);
+      kp1 = __builtin_fmaf(S[m].y, ki, kp1);
+      kp2 = __builtin_fmaf(S[m].z, ki, kp2);
+      kp3 = __builtin_fmaf(S[m].w, ki, kp3);
+    }
+    *reinterpret_cast<float4*>(&s_part[4 * rq + gq][c4 * 4]) = make_float4(kp0, kp1, kp2, kp3);
   }
-  *reinterpret_cast<float4*>(&s_part[rg][c4 * 4]) = make_float4(kp0, kp1, kp2, kp3);
   __syncthreads();
   if (tid < 128) {
-    float pp[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) pp[r] = s_part[r][tid];
-    const float kv = tree8(pp);
+    const float kv = tree32(s_part, tid);
     s_delta[tid] = (s_v[tid] - kv) * beta;
   }
   __syncthreads();
 
-  // rank-1 update, state write-back, output partials
+  // rank-1 update, state write-back, output partials per 4-row group
   const float4 d4 = *reinterpret_cast<const float4*>(&s_delta[c4 * 4]);
-  float op0 = 0.f, op1 = 0.f, op2 = 0.f, op3 = 0.f;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const float ki = s_k[rg * 16 + m];
-    const float qi = s_q[rg * 16 + m];
-    S[m].x = __builtin_fmaf(ki, d4.x, S[m].x);
-    S[m].y = __builtin_fmaf(ki, d4.y, S[m].y);
-    S[m].z = __builtin_fmaf(ki, d4.z, S[m].z);
-    S[m].w = __builtin_fmaf(ki, d4.w, S[m].w);
-    *reinterpret_cast<float4*>(st_head + (rg * 16 + m) * 128 + c4 * 4) = S[m];
-    op0 = __builtin_fmaf(S[m].x, qi, op0);
-    op1 = __builtin_fmaf(S[m].y, qi, op1);
-    op2 = __builtin_fmaf(S[m].z, qi, op2);
-    op3 = __builtin_fmaf(S[m].w, qi, op3);
+  for (int gq = 0; gq < 4; ++gq) {
+    float op0 = 0.f, op1 = 0.f, op2 = 0.f, op3 = 0.f;
+#pragma unroll
+    for (int m = 4 * gq; m < 4 * gq + 4; ++m) {
+      const float ki = s_k[rq * 16 + m];
+      const float qi = s_q[rq * 16 + m];
+      S[m].x = __builtin_fmaf(ki, d4.x, S[m].x);
+      S[m].y = __builtin_fmaf(ki, d4.y, S[m].y);
+      S[m].z = __builtin_fmaf(ki, d4.z, S[m].z);
+      S[m].w = __builtin_fmaf(ki, d4.w, S[m].w);
+      *reinterpret_cast<float4*>(st_head + (rq * 16 + m) * 128 + c4 * 4) = S[m];
+      op0 = __builtin_fmaf(S[m].x, qi, op0);
+      op1 = __builtin_fmaf(S[m].y, qi, op1);
+      op2 = __builtin_fmaf(S[m].z, qi, op2);
+      op3 = __builtin_fmaf(S[m].w, qi, op3);
+    }
+    *reinterpret_cast<float4*>(&s_part[4 * rq + gq][c4 * 4]) = make_float4(op0, op1, op2, op3);
   }
-  *reinterpret_cast<float4*>(&s_part[rg][c4 * 4]) = make_float4(op0, op1, op2, op3);
   __syncthreads();
 
   if (wave == 0) {
-    float pa[8], pb[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      pa[r] = s_part[r][lane];
-      pb[r] = s_part[r][lane + 64];
-    }
-    const float oa = tree8(pa);
-    const float ob = tree8(pb);
+    const float oa = tree32(s_part, lane);
+    const float ob = tree32(s_part, lane + 64);
     uint16_t* out = qkv + 2 * nh * 128 + h * 128;
     if (NORM_GATE) {
       float v = oa * oa + ob * ob;

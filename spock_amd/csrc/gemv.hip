@@ -212,6 +212,68 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
   if (threadIdx.x == 0) *out = key_to_index(key, E);
 }
 
+// Several GEMVs in one launch: workgroup ranges are assigned to descriptors by
+// prefix sums; each workgroup runs 4 wavefronts x kBatchRows rows of one
+// descriptor with the same per-row order as gemv_kernel (bit-identical
+// results), the row span per lane (in_dim / 64, a multiple of 8 halves) being
+// a runtime count of 16-byte loads.
+constexpr int kMaxBatch = 8;
+constexpr int kBatchRows = 2;
+struct GemvBatch {
+  const uint16_t* W[kMaxBatch];
+  const uint16_t* x[kMaxBatch];
+  uint16_t* y[kMaxBatch];
+  int out_dim[kMaxBatch];
+  int n8[kMaxBatch];
+  int first_block[kMaxBatch + 1];
+  int count;
+};
+
+__global__ __launch_bounds__(256) void gemv_batched_kernel(GemvBatch b) {
+  int d = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxBatch; ++i)
+    if (i < b.count && (int)blockIdx.x >= b.first_block[i]) d = i;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n8 = b.n8[d];
+  const int in_dim = 512 * n8;
+  const int out_dim = b.out_dim[d];
+  const uint16_t* __restrict__ W = b.W[d];
+  float xf[64];
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(b.x[d] + lane * (8 * n8));
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < n8) unpack8(src[k], xf + 8 * k);
+  }
+  const int row0 = (((int)blockIdx.x - b.first_block[d]) * 4 + wave) * kBatchRows;
+  uint4 wv[kBatchRows][8];
+#pragma unroll
+  for (int r = 0; r < kBatchRows; ++r) {
+    const int row = row0 + r < out_dim ? row0 + r : out_dim - 1;
+    const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * n8));
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < n8) wv[r][k] = ld_stream(src + k);
+  }
+#pragma unroll
+  for (int r = 0; r < kBatchRows; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k < n8) {
+        float wf[8];
+        unpack8(wv[r][k], wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
+      }
+    }
+    acc = spk::tree64_to_lane0(acc);
+    if (lane == 0 && row0 + r < out_dim) b.y[d][row0 + r] = spk::f2h(acc);
+  }
+}
+
 constexpr int kLmRows = 8;  // rows per wavefront in the lm_head stream
 
 int launch_gemv(const uint16_t* W, const uint16_t* x, uint16_t* y, int out_dim, int in_dim,
@@ -276,12 +338,40 @@ extern "C" int spk_matvec_f16_batched(const SpkMatvecDesc* d, int32_t count, spk
     const int rc = check_gemv(d[i].W, d[i].x, d[i].y, d[i].out_dim, d[i].in_dim, "spk_matvec_f16_batched");
     if (rc) return rc;
   }
+  hipStream_t s = spk::to_hip(stream);
+  GemvBatch b;
+  b.count = 0;
+  int blocks = 0;
+  auto flush = [&]() -> int {
+    if (b.count == 0) return SPK_OK;
+    b.first_block[b.count] = blocks;
+    hipLaunchKernelGGL(gemv_batched_kernel, dim3(blocks), dim3(256), 0, s, b);
+    b.count = 0;
+    blocks = 0;
+    return spk::check_launch("spk_matvec_f16_batched");
+  };
   for (int i = 0; i < count; ++i) {
     if (d[i].out_dim == 0) continue;
-    const int rc = launch_gemv(d[i].W, d[i].x, d[i].y, d[i].out_dim, d[i].in_dim, spk::to_hip(stream));
-    if (rc) return rc;
+    const bool vec = d[i].in_dim % 512 == 0 && d[i].in_dim <= 8 * 512 && spk::aligned(d[i].W, 16) &&
+                     spk::aligned(d[i].x, 16);
+    if (!vec) {  // rare shapes: their own launch, same per-row order
+      const int rc = launch_gemv(d[i].W, d[i].x, d[i].y, d[i].out_dim, d[i].in_dim, s);
+      if (rc) return rc;
+      continue;
+    }
+    b.W[b.count] = d[i].W;
+    b.x[b.count] = d[i].x;
+    b.y[b.count] = d[i].y;
+    b.out_dim[b.count] = d[i].out_dim;
+    b.n8[b.count] = d[i].in_dim / 512;
+    b.first_block[b.count] = blocks;
+    blocks += (d[i].out_dim + 4 * kBatchRows - 1) / (4 * kBatchRows);
+    if (++b.count == kMaxBatch) {
+      const int rc = flush();
+      if (rc) return rc;
+    }
   }
-  return SPK_OK;
+  return flush();
 }
 
 extern "C" int spk_argmax_f16(const uint16_t* vals, int32_t n, uint32_t* out_index,
