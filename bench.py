@@ -49,6 +49,20 @@ VOCAB, HIDDEN = 248320, 1024
 ROTATE_BYTES = 512 << 20
 
 
+def measured_traffic(profile: str, source: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, scaled by the copy-kernel calibration) and recorded in
+    profiles/<profile> together with the SHA-256 of the kernel source it was
+    measured on; None when the source has changed since."""
+    import hashlib
+    p = ROOT / "profiles" / profile
+    if not p.exists():
+        return None
+    kv = dict(ln.split("=", 1) for ln in p.read_text().splitlines() if "=" in ln and not ln.startswith("#"))
+    sha = hashlib.sha256((ROOT / source).read_bytes()).hexdigest()
+    return int(kv["traffic_bytes"]) if kv.get("source_sha256") == sha else None
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -105,7 +119,9 @@ def bench_prefill(steps, warmup):
         "flop_per_launch": flops, "wall_s": wall, "launch_ms": ms,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic("chunk_prefill_config2_traffic.txt",
+                                                 "spock_amd/csrc/chunk.hip")},
     }
     return res
 
