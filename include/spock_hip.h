@@ -194,6 +194,138 @@ int spk_lm_head_argmax(const uint16_t* W, const uint16_t* x, int32_t vocab, int3
                        size_t workspace_bytes, spk_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Qwen3.5 text model: the rest of the per-token decode loop and the prefill
+ * element-wise operations (DecodeSession::decode, vk_session.cpp:2560-3400).
+ * Results are bit-identical to the CPU restatement; every operation's order
+ * is stated in oracle/model.h.  Hidden size 1024; attention 8 query heads,
+ * 2 KV heads, head_dim 256, rotary dim 64; KV cache per layer
+ * [max_seq][K 2x256 | V 2x256] fp16 (vk_session.cpp:322-328).
+ * ---------------------------------------------------------------------- */
+
+enum { SPK_GEMV_IN_PLAIN = 0, SPK_GEMV_IN_RMSNORM = 1, SPK_GEMV_IN_SILU_GATE = 2 };
+
+/* Input of a fused projection, computed once per workgroup:
+ *   PLAIN      x                                         (matvec_tiled.comp)
+ *   RMSNORM    fp16(RMSNorm(h) * (1 + x2)), in_dim 1024  (rms_norm.comp before
+ *              the projection, vk_session.cpp:2606-2613, :3283-3289);
+ *              h = x, or row token[0] of x when token != NULL (the embedding
+ *              lookup of embedding_lookup.comp, token read on the device;
+ *              ids outside [0, token_rows) select row 0), in which case
+ *              h_out (nullable) receives that row: the residual stream
+ *   SILU_GATE  fp16(silu(x) * x2)                        (silu_gate.comp) */
+typedef struct SpkGemvInput {
+  int32_t kind;
+  int32_t in_dim;          /* multiple of 512, <= 4096 */
+  const uint16_t* x;
+  const uint16_t* x2;
+  const int32_t* token;
+  int32_t token_rows;
+  uint16_t* h_out;
+} SpkGemvInput;
+
+/* y = fp16(W . x), or fp16(residual + fp16(W . x)) (residual_add.comp after
+ * the projection) when residual != NULL; y may equal residual (in-place update
+ * of the stream) but must not alias the input vectors. */
+typedef struct SpkGemvOutput {
+  const uint16_t* W;         /* [out_dim][in_dim] fp16, 16-byte aligned */
+  uint16_t* y;
+  const uint16_t* residual;
+  int32_t out_dim;
+} SpkGemvOutput;
+
+/* Up to 8 projections of one input in one launch.  Replaces the
+ * rms_norm + matvec (+ residual_add / silu_gate) dispatch runs of
+ * vk_session.cpp:2606-2870 and :3276-3360. */
+int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count,
+                   spk_stream_t stream);
+
+/* Full-attention token mixer: split_q_gate.comp, rms_norm_per_head.comp (q and
+ * k, weights applied as 1 + w), rope_apply.comp (pairs (i, i+32) of the first
+ * 64 dims, table rope[pos][64] = (cos, sin) pairs), kv_cache_store.comp,
+ * attention_decode.comp (softmax(q.K^T / 16) V, GQA 4:1) and sigmoid_gate.comp
+ * (dispatches vk_session.cpp:2676-2790). */
+typedef struct SpkAttnArgs {
+  const uint16_t* qg;        /* q_proj output per token [8][256 query | 256 gate] */
+  const uint16_t* k;         /* k_proj output per token [2][256] */
+  const uint16_t* v;         /* v_proj output per token [2][256] */
+  const uint16_t* q_norm_w;  /* [256] */
+  const uint16_t* k_norm_w;  /* [256] */
+  const float* rope;         /* [max_seq][64] */
+  uint16_t* kv_cache;        /* this layer's [max_seq][1024] */
+  int32_t max_seq;
+  const int32_t* pos_dev;    /* decode: device int32 position of the token */
+  uint16_t* out;             /* gated output per token [2048] */
+  void* workspace;
+  size_t workspace_bytes;
+} SpkAttnArgs;
+
+/* Workspace bytes for `tokens` queries over positions [0, positions). */
+size_t spk_attention_workspace_size(int32_t positions, int32_t tokens);
+/* One token at position *pos_dev (< max_seq; read on the device, so the call
+ * can be recorded once and replayed); workspace for (max_seq, 1). */
+int spk_attention_decode(const SpkAttnArgs* args, spk_stream_t stream);
+/* `tokens` consecutive tokens at positions pos0.. (rows of qg/k/v/out are
+ * per token); workspace for (pos0 + tokens, tokens). */
+int spk_attention_prefill(const SpkAttnArgs* args, int32_t pos0, int32_t tokens,
+                          spk_stream_t stream);
+
+/* RMSNorm(1 + w) of `rows` rows of n = 1024 (rms_norm.comp) or n = 256
+ * (rms_norm_per_head.comp). */
+int spk_rmsnorm_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int32_t rows, int32_t n,
+                    spk_stream_t stream);
+/* silu_gate.comp: y = fp16(silu(g) * u) */
+int spk_silu_gate_f16(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n,
+                      spk_stream_t stream);
+/* residual_add.comp: y = fp16(a + b) */
+int spk_residual_add_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, int64_t n,
+                         spk_stream_t stream);
+/* embedding_lookup.comp for n_tokens device token ids (rows of 1024; ids
+ * outside [0, vocab) give zero rows). */
+int spk_embedding_f16(const uint16_t* E, const int32_t* tokens, int32_t n_tokens, int32_t vocab,
+                      uint16_t* y, spk_stream_t stream);
+/* *p += delta on the device (advances a device position counter). */
+int spk_add_i32(int32_t* p, int32_t delta, spk_stream_t stream);
+
+/* ---- prompt-length (prefill) forms ------------------------------------- */
+
+/* C[M][N] = fp16(A[M][K] . W[N][K]^T), or fp16(residual + fp16(...)) when
+ * residual != NULL (may equal C; must not alias A or W); fp16 operands, fp32
+ * accumulation on the matrix cores.  The prompt-wide form of every decode
+ * matvec (matvec_tiled.comp over all prompt tokens).  K % 32 == 0; A, W
+ * 16-byte aligned with lda, ldw multiples of 8.  Not bit-identical to the
+ * matvec's summation order. */
+int spk_gemm_f16(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, uint16_t* C,
+                 int64_t ldc, const uint16_t* residual, int32_t M, int32_t N, int32_t K,
+                 spk_stream_t stream);
+
+/* DeltaNet prompt conv: for every token t of qkv [tokens][ld] (raw in_proj_qkv
+ * output, fp16), the deltanet_conv_l2_qk.comp operations of decode (window of
+ * the raw inputs t-3..t, earlier ones from conv_state [6144][4]; SiLU; fp16;
+ * L2 of each Q/K head block), written head-major for the chunk rule: q_hm,
+ * k_hm, v_hm [16][tokens][128] fp16.  conv_state then holds the last 4 raw
+ * inputs.  Replaces the per-token collect loop of vk_session.cpp:1464-1716. */
+int spk_deltanet_prefill_conv(const uint16_t* qkv, int64_t ld, uint16_t* conv_state,
+                              const uint16_t* conv_weight, int32_t tokens, uint16_t* q_hm,
+                              uint16_t* k_hm, uint16_t* v_hm, spk_stream_t stream);
+/* g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) for every token
+ * (deltanet_recurrent_gbeta_norm_gate.comp:102-116); a, b [tokens][ld] fp16;
+ * g, beta head-major [16][tokens] fp32. */
+int spk_deltanet_prefill_gbeta(const uint16_t* a, const uint16_t* b, int64_t ld,
+                               const float* a_log_bias, int32_t layer_idx, int32_t tokens,
+                               float* g, float* beta, spk_stream_t stream);
+/* Gated RMSNorm of the chunk rule's fp32 output (the fused decode shader's
+ * :182-224 on every token): core row (h, t) at core + (h*core_head_stride +
+ * t)*128, z [tokens][z_ld] fp16, out [tokens][out_ld] fp16. */
+int spk_deltanet_norm_gate(const float* core, int64_t core_head_stride, const uint16_t* z,
+                           int64_t z_ld, const float* norm_weight, float eps, int32_t tokens,
+                           uint16_t* out, int64_t out_ld, spk_stream_t stream);
+/* history[*count] = *token (when *count < capacity), *count += 1, *pos += 1:
+ * the greedy loop's bookkeeping, kept on the device so one recorded decode
+ * step serves every token. */
+int spk_record_token(const int32_t* token, int32_t* pos, int32_t* count, int32_t* history,
+                     int32_t capacity, spk_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Diagnostics (no reference counterpart).
  * ---------------------------------------------------------------------- */
 

@@ -34,6 +34,21 @@ SIGNATURES = {
     "spk_lm_head_workspace_size": (_sz, [_i32]),
     "spk_lm_head_argmax": (C.c_int, [_p, _p, _i32, _i32, _p, _p, _p, _sz, _p]),
     "spk_selftest_numerics": (C.c_int, [_p, _i32, _p, _p]),
+    # Qwen3.5 model kernels
+    "spk_gemv_fused": (C.c_int, [_p, _p, _i32, _p]),
+    "spk_attention_workspace_size": (_sz, [_i32, _i32]),
+    "spk_attention_decode": (C.c_int, [_p, _p]),
+    "spk_attention_prefill": (C.c_int, [_p, _i32, _i32, _p]),
+    "spk_rmsnorm_f16": (C.c_int, [_p, _p, _p, _i32, _i32, _p]),
+    "spk_silu_gate_f16": (C.c_int, [_p, _p, _p, _i64, _p]),
+    "spk_residual_add_f16": (C.c_int, [_p, _p, _p, _i64, _p]),
+    "spk_embedding_f16": (C.c_int, [_p, _p, _i32, _i32, _p, _p]),
+    "spk_add_i32": (C.c_int, [_p, _i32, _p]),
+    "spk_record_token": (C.c_int, [_p, _p, _p, _p, _i32, _p]),
+    "spk_gemm_f16": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _i32, _i32, _i32, _p]),
+    "spk_deltanet_prefill_conv": (C.c_int, [_p, _i64, _p, _p, _i32, _p, _p, _p, _p]),
+    "spk_deltanet_prefill_gbeta": (C.c_int, [_p, _p, _i64, _p, _i32, _i32, _p, _p, _p]),
+    "spk_deltanet_norm_gate": (C.c_int, [_p, _i64, _p, _i64, _p, _f32, _i32, _p, _i64, _p]),
 }
 
 
@@ -61,6 +76,24 @@ class SpkDecodeArgs(C.Structure):
         ("z", _p), ("z_stride", _i64),
         ("norm_weight", _p),
     ]
+
+
+SPK_GEMV_IN_PLAIN, SPK_GEMV_IN_RMSNORM, SPK_GEMV_IN_SILU_GATE = 0, 1, 2
+
+
+class SpkGemvInput(C.Structure):
+    _fields_ = [("kind", _i32), ("in_dim", _i32), ("x", _p), ("x2", _p), ("token", _p),
+                ("token_rows", _i32), ("h_out", _p)]
+
+
+class SpkGemvOutput(C.Structure):
+    _fields_ = [("W", _p), ("y", _p), ("residual", _p), ("out_dim", _i32)]
+
+
+class SpkAttnArgs(C.Structure):
+    _fields_ = [("qg", _p), ("k", _p), ("v", _p), ("q_norm_w", _p), ("k_norm_w", _p), ("rope", _p),
+                ("kv_cache", _p), ("max_seq", _i32), ("pos_dev", _p), ("out", _p), ("workspace", _p),
+                ("workspace_bytes", _sz)]
 
 
 class SpkMatvecDesc(C.Structure):

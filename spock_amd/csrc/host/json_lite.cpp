@@ -137,6 +137,15 @@ const std::vector<Value>& Value::as_array() const {
   if (kind_ != Kind::Array) throw std::runtime_error("JSON value is not an array");
   return arr_;
 }
+const std::string& Value::as_string() const {
+  if (kind_ != Kind::String) throw std::runtime_error("JSON value is not a string");
+  return str_;
+}
+const std::string& Value::get_string(const std::string& key) const {
+  const Value* v = get(key);
+  if (v == nullptr) throw std::runtime_error("missing string field: " + key);
+  return v->as_string();
+}
 const Value* Value::get(const std::string& key) const {
   if (kind_ != Kind::Object) return nullptr;
   auto it = obj_.find(key);

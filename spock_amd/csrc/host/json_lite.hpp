@@ -21,12 +21,16 @@ class Value {
   bool is_null() const { return kind_ == Kind::Null; }
   bool is_bool() const { return kind_ == Kind::Bool; }
   bool is_number() const { return kind_ == Kind::Number; }
+  bool is_string() const { return kind_ == Kind::String; }
   bool is_array() const { return kind_ == Kind::Array; }
   bool is_object() const { return kind_ == Kind::Object; }
 
   bool as_bool() const;
   double as_double() const;
   const std::vector<Value>& as_array() const;
+  const std::string& as_string() const;
+  // String member; error when absent or not a string.
+  const std::string& get_string(const std::string& key) const;
   // Member lookup on an object; nullptr when absent (or not an object).
   const Value* get(const std::string& key) const;
   // Integer member; `fallback` when absent, error when present but not integral.

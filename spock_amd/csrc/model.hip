@@ -1,0 +1,658 @@
+// model.hip -- the remaining per-token kernels of the Qwen3.5-0.8B decode loop
+// (src/runtime/vk_session.cpp:2560-3400): projections with their input norm /
+// SiLU gate fused in front and the residual add fused behind, the full-
+// attention token mixer, and the element-wise operations the prefill needs.
+//
+// Every result is bit-identical to the CPU restatement (oracle/model.h lists
+// the operation order); the orders are:
+//   RMSNorm(1+w), n = 1024: 256 partials of 4 contiguous squares (fma chain),
+//     tree s[t] += s[t+stride] for stride 128..1, nf = 1/sqrt(sum/1024 + eps),
+//     y = fp16((x*nf)*(1+w))                                  (rms_norm.comp)
+//   per-head RMSNorm, n = 256: partials x_t^2, same tree   (rms_norm_per_head.comp)
+//   GEMV: 64 lanes x contiguous spans, fma chains from 0, then the 32..1 tree
+//   attention: blocks of 64 positions; per block max, exp, 64-lane tree of the
+//     weights and fma chains over positions; blocks combined in order.
+#include "capi_common.hpp"
+#include "numerics.hpp"
+
+#include <float.h>
+
+namespace {
+
+constexpr int kHidden = 1024;
+constexpr int kHeadDim = 256;
+constexpr int kQHeads = 8;
+constexpr int kKvHeads = 2;
+constexpr int kKvRow = 1024;  // K 2x256 | V 2x256 halves per cached position
+constexpr int kAttnBlock = 64;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& u, float* f) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = spk::h2f((uint16_t)(w[i] & 0xffffu));
+    f[2 * i + 1] = spk::h2f((uint16_t)(w[i] >> 16));
+  }
+}
+
+__device__ __forceinline__ float round16(float v) { return spk::h2f(spk::f2h(v)); }
+
+// Sum of 256 per-thread partials in the rms_norm.comp tree order; every thread
+// of the 256-thread block gets the result.  `red` is 256 floats of LDS.
+__device__ __forceinline__ float block_tree256(float p, float* red) {
+  const int t = threadIdx.x;
+  red[t] = p;
+  __syncthreads();
+  if (t < 128) red[t] = red[t] + red[t + 128];
+  __syncthreads();
+  if (t < 64) red[t] = red[t] + red[t + 64];
+  __syncthreads();
+  if (t < 64) {
+    float v = red[t];
+    v = spk::tree64_to_lane0(v);
+    if (t == 0) red[256] = v;
+  }
+  __syncthreads();
+  const float r = red[256];
+  __syncthreads();
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Fused GEMV: y_o = fp16(W_o . x) (+ residual), x = one of
+//   PLAIN      x
+//   RMSNORM    fp16(RMSNorm(h) * (1 + w)),  h = x (or row token[0] of x)
+//   SILU_GATE  fp16(silu(gate) * up)
+// computed once per workgroup into LDS (fp16-rounded values as floats).
+// ---------------------------------------------------------------------------
+constexpr int kMaxOut = 8;
+constexpr int kMaxIn = 4096;
+
+struct FusedGemv {
+  int kind;
+  int in_dim;
+  const uint16_t* x;
+  const uint16_t* x2;
+  const int32_t* token;
+  int token_rows;
+  uint16_t* h_out;
+  int count;
+  const uint16_t* W[kMaxOut];
+  uint16_t* y[kMaxOut];
+  const uint16_t* res[kMaxOut];
+  int out_dim[kMaxOut];
+  int first_block[kMaxOut + 1];
+};
+
+template <int N8, int R>
+__global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
+  __shared__ float xs[kMaxIn];
+  __shared__ float red[257];
+  int d = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxOut; ++i)
+    if (i < a.count && (int)blockIdx.x >= a.first_block[i]) d = i;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  constexpr int in_dim = 512 * N8;
+  const int out_dim = a.out_dim[d];
+  const int row0 = (((int)blockIdx.x - a.first_block[d]) * 4 + wave) * R;
+  // Weight rows first: they do not depend on x, so their latency overlaps the prologue.
+  uint4 wv[R][N8];
+  {
+    const uint16_t* __restrict__ W = a.W[d];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = row0 + r < out_dim ? row0 + r : out_dim - 1;
+      const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
+#pragma unroll
+      for (int k = 0; k < N8; ++k) wv[r][k] = ld_stream(src + k);
+    }
+  }
+  if (a.kind == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
+    const uint16_t* h = a.x;
+    if (a.token) {  // ids outside [0, token_rows) select row 0 instead of reading out of bounds
+      const int id = a.token[0];
+      h += (size_t)((id >= 0 && id < a.token_rows) ? id : 0) * kHidden;
+    }
+    const uint2 hv = *reinterpret_cast<const uint2*>(h + 4 * tid);
+    const uint2 wv2 = *reinterpret_cast<const uint2*>(a.x2 + 4 * tid);
+    const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
+                        spk::h2f(hv.y >> 16)};
+    const float w[4] = {spk::h2f(wv2.x & 0xffffu), spk::h2f(wv2.x >> 16), spk::h2f(wv2.y & 0xffffu),
+                        spk::h2f(wv2.y >> 16)};
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p = __builtin_fmaf(v[i], v[i], p);
+    const float sum = block_tree256(p, red);
+    const float nf = 1.0f / __builtin_sqrtf(sum / 1024.0f + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[4 * tid + i] = round16((v[i] * nf) * (1.0f + w[i]));
+    if (a.h_out && blockIdx.x == 0) *reinterpret_cast<uint2*>(a.h_out + 4 * tid) = hv;
+  } else if (a.kind == SPK_GEMV_IN_SILU_GATE) {
+    for (int i = tid; i < in_dim; i += 256) {
+      const float g = spk::h2f(a.x[i]);
+      xs[i] = round16(spk::silu_det(g) * spk::h2f(a.x2[i]));
+    }
+  } else {
+    for (int i = tid; i < in_dim; i += 256) xs[i] = spk::h2f(a.x[i]);
+  }
+  __syncthreads();
+  float xf[8 * N8];
+#pragma unroll
+  for (int k = 0; k < 8 * N8; k += 4) {
+    const float4 t = *reinterpret_cast<const float4*>(&xs[lane * (8 * N8) + k]);
+    xf[k] = t.x;
+    xf[k + 1] = t.y;
+    xf[k + 2] = t.z;
+    xf[k + 3] = t.w;
+  }
+  uint16_t* __restrict__ y = a.y[d];
+  const uint16_t* __restrict__ res = a.res[d];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N8; ++k) {
+      float wf[8];
+      unpack8(wv[r][k], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
+    }
+    acc = spk::tree64_to_lane0(acc);
+    const int row = row0 + r;
+    if (lane == 0 && row < out_dim) {
+      uint16_t o = spk::f2h(acc);
+      if (res) o = spk::f2h(spk::h2f(res[row]) + spk::h2f(o));
+      y[row] = o;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Attention decode (attention_decode.comp + rms_norm_per_head + rope_apply +
+// kv_cache_store + sigmoid_gate for one token), position read from device.
+// Kernel 1: one workgroup per (64-position block, KV head), wave w = query
+// head 4*kvh + w.  Block of the current position also norms/ropes the new
+// K row and stores K/V into the cache.  Writes per (query head, block):
+// m_b, S_b, O_b[256].  Kernel 2: per query head, combine blocks in order,
+// normalise, sigmoid gate.
+// ---------------------------------------------------------------------------
+constexpr int kPartFloats = 2 + kHeadDim;  // m, S, O[256]
+
+// Per-head RMSNorm(1+w) of the 256 values a wave holds (lane l: d = 4l..4l+3),
+// in the s[t] += s[t+stride] (stride 128..1) order; returns fp16-rounded values.
+__device__ __forceinline__ void head_norm_wave(float (&v)[4], const uint16_t* w, int lane) {
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = v[i] * v[i];
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) {  // strides 128, 64, ..., 4 (lane distance sh)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = s[i] + __shfl_down(s[i], sh, 64);
+  }
+  float sum = (s[0] + s[2]) + (s[1] + s[3]);  // strides 2 then 1 inside lane 0
+  sum = __shfl(sum, 0, 64);
+  const float nf = 1.0f / __builtin_sqrtf(sum / 256.0f + 1e-6f);
+  const uint2 wv = *reinterpret_cast<const uint2*>(w + 4 * lane);
+  const float wf[4] = {spk::h2f(wv.x & 0xffffu), spk::h2f(wv.x >> 16), spk::h2f(wv.y & 0xffffu),
+                       spk::h2f(wv.y >> 16)};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = round16((v[i] * nf) * (1.0f + wf[i]));
+}
+
+// rope_apply.comp pairs (i, i+32), i < 32: lanes 0..7 hold d < 32, lanes 8..15 d in [32, 64).
+__device__ __forceinline__ void rope_wave(float (&v)[4], const float* cs, int lane) {
+  float o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = __shfl_xor(v[i], 8, 64);
+  if (lane < 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 4 * lane + i;
+      const int p = d & 31;
+      const float c = cs[2 * p], s = cs[2 * p + 1];
+      if (d < 32)
+        v[i] = round16(v[i] * c - o[i] * s);
+      else
+        v[i] = round16(v[i] * c + o[i] * s);
+    }
+  }
+}
+
+__device__ __forceinline__ void load4h(const uint16_t* p, float (&v)[4]) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  v[0] = spk::h2f(u.x & 0xffffu);
+  v[1] = spk::h2f(u.x >> 16);
+  v[2] = spk::h2f(u.y & 0xffffu);
+  v[3] = spk::h2f(u.y >> 16);
+}
+
+__device__ __forceinline__ uint2 pack4h(const float (&v)[4]) {
+  uint2 u;
+  u.x = (uint32_t)spk::f2h(v[0]) | ((uint32_t)spk::f2h(v[1]) << 16);
+  u.y = (uint32_t)spk::f2h(v[2]) | ((uint32_t)spk::f2h(v[3]) << 16);
+  return u;
+}
+
+struct AttnArgs {
+  const uint16_t* qg;  // [T][4096] (T = 1 for decode)
+  const uint16_t* k;   // [T][512]
+  const uint16_t* v;   // [T][512]
+  const uint16_t* q_norm_w;
+  const uint16_t* k_norm_w;
+  const float* rope;
+  uint16_t* kv;        // layer cache [max_seq][1024]
+  int max_seq;
+  const int32_t* pos_dev;  // decode: device position
+  int pos0;                // prefill: first position
+  uint16_t* out;       // [T][2048]
+  float* part;         // [T][8][max_blocks][kPartFloats]
+  int max_blocks;      // blocks of 64 positions the grid covers
+  int store_kv;        // decode: the current position's block stores its K/V row
+};
+
+// One query-head wave over one block of positions [64b, 64b+64) of npos valid
+// ones: writes m_b, S_b, O_b.  q (fp16-rounded floats) is in qs[256] (LDS);
+// cur_k/cur_v (LDS, fp16 bits) stand in for the cache row of position `cur`.
+__device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t* kv, int kvh, int b, int npos,
+                                                int cur, const uint16_t* cur_k, const uint16_t* cur_v, int lane,
+                                                float* part) {
+  const int p = kAttnBlock * b + lane;
+  float sc = -INFINITY;
+  if (p < npos) {
+    const uint16_t* kp = (p == cur) ? cur_k : kv + (size_t)p * kKvRow + kvh * kHeadDim;
+    float dot = 0.0f;
+    for (int d8 = 0; d8 < kHeadDim; d8 += 8) {
+      const uint4 u = *reinterpret_cast<const uint4*>(kp + d8);
+      float kf[8];
+      unpack8(u, kf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(qs[d8 + e], kf[e], dot);
+    }
+    sc = dot * 0.0625f;
+  }
+  float m = sc;
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh, 64));
+  const float w = (p < npos) ? spk::expf_det(sc - m) : 0.0f;
+  const float S = spk::tree64_to_lane0(w);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int nvalid = min(kAttnBlock, npos - kAttnBlock * b);
+  for (int j = 0; j < nvalid; ++j) {
+    const int pj = kAttnBlock * b + j;
+    const float wj = __shfl(w, j, 64);
+    const uint16_t* vp = (pj == cur) ? cur_v : kv + (size_t)pj * kKvRow + 512 + kvh * kHeadDim;
+    float vf[4];
+    load4h(vp + 4 * lane, vf);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(wj, vf[i], acc[i]);
+  }
+  if (lane == 0) {
+    part[0] = m;
+    part[1] = S;
+  }
+  *reinterpret_cast<float4*>(part + 2 + 4 * lane) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
+// grid (max_blocks, kv_heads, T); block 256.
+__global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
+  __shared__ float qs[4][kHeadDim];
+  __shared__ __align__(16) uint16_t cur_k[kHeadDim];
+  __shared__ __align__(16) uint16_t cur_v[kHeadDim];
+  const int b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int pos = a.pos_dev ? a.pos_dev[0] : a.pos0 + t;
+  if (pos < 0 || pos >= a.max_seq) return;
+  const int npos = pos + 1;
+  if (kAttnBlock * b >= npos) return;
+  const float* cs = a.rope + (size_t)pos * 64;
+  const bool has_cur = a.store_kv && (pos / kAttnBlock) == b;
+  const int qh = kvh * 4 + wave;
+  {
+    float v[4];
+    load4h(a.qg + (size_t)t * 4096 + qh * 512 + 4 * lane, v);
+    head_norm_wave(v, a.q_norm_w, lane);
+    rope_wave(v, cs, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = v[i];
+  }
+  if (has_cur && wave == 0) {  // new K row: norm + rope; V row as projected
+    float v[4];
+    load4h(a.k + (size_t)t * 512 + kvh * kHeadDim + 4 * lane, v);
+    head_norm_wave(v, a.k_norm_w, lane);
+    rope_wave(v, cs, lane);
+    const uint2 kb = pack4h(v);
+    const uint2 vb = *reinterpret_cast<const uint2*>(a.v + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
+    *reinterpret_cast<uint2*>(cur_k + 4 * lane) = kb;
+    *reinterpret_cast<uint2*>(cur_v + 4 * lane) = vb;
+    uint16_t* row = a.kv + (size_t)pos * kKvRow;  // kv_cache_store.comp:27-48
+    *reinterpret_cast<uint2*>(row + kvh * kHeadDim + 4 * lane) = kb;
+    *reinterpret_cast<uint2*>(row + 512 + kvh * kHeadDim + 4 * lane) = vb;
+  }
+  __syncthreads();
+  float* part = a.part + (((size_t)t * kQHeads + qh) * a.max_blocks + b) * kPartFloats;
+  attn_block_wave(qs[wave], a.kv, kvh, b, npos, has_cur ? pos : -1, cur_k, cur_v, lane, part);
+}
+
+// Prefill: K/V rows of positions pos0..pos0+T-1, before any block pass reads
+// them.  grid (T, kv_heads); one wave.
+__global__ __launch_bounds__(64) void attn_store_kv_kernel(AttnArgs a) {
+  const int t = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
+  const int pos = a.pos0 + t;
+  if (pos < 0 || pos >= a.max_seq) return;
+  float v[4];
+  load4h(a.k + (size_t)t * 512 + kvh * kHeadDim + 4 * lane, v);
+  head_norm_wave(v, a.k_norm_w, lane);
+  rope_wave(v, a.rope + (size_t)pos * 64, lane);
+  uint16_t* row = a.kv + (size_t)pos * kKvRow;
+  *reinterpret_cast<uint2*>(row + kvh * kHeadDim + 4 * lane) = pack4h(v);
+  *reinterpret_cast<uint2*>(row + 512 + kvh * kHeadDim + 4 * lane) =
+      *reinterpret_cast<const uint2*>(a.v + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
+}
+
+// grid (8 query heads, T); block 256 (thread = output dim).
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  const int qh = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  const int pos = a.pos_dev ? a.pos_dev[0] : a.pos0 + t;
+  if (pos < 0 || pos >= a.max_seq) return;
+  const int nb = (pos + kAttnBlock) / kAttnBlock;
+  const float* part = a.part + ((size_t)t * kQHeads + qh) * a.max_blocks * kPartFloats;
+  float M = -INFINITY;
+  for (int b = 0; b < nb; ++b) M = fmaxf(M, part[(size_t)b * kPartFloats]);
+  float tot = 0.0f, o = 0.0f;
+  for (int b = 0; b < nb; ++b) {
+    const float* pb = part + (size_t)b * kPartFloats;
+    const float c = spk::expf_det(pb[0] - M);
+    tot = tot + pb[1] * c;
+    o = o + pb[2 + d] * c;
+  }
+  const float att = round16(o * (1.0f / (tot + 1e-30f)));
+  const float g = spk::h2f(a.qg[(size_t)t * 4096 + qh * 512 + 256 + d]);
+  const float sig = 1.0f / (1.0f + spk::expf_det(-g));
+  a.out[(size_t)t * 2048 + qh * kHeadDim + d] = spk::f2h(att * sig);
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise kernels
+// ---------------------------------------------------------------------------
+
+// RMSNorm(1+w) of rows of 1024 (one 256-thread block per row).
+__global__ __launch_bounds__(256) void rmsnorm1024_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ w,
+                                                          uint16_t* __restrict__ y) {
+  __shared__ float red[257];
+  const int tid = threadIdx.x;
+  const size_t base = (size_t)blockIdx.x * kHidden + 4 * tid;
+  float v[4], wf[4];
+  load4h(x + base, v);
+  load4h(w + 4 * tid, wf);
+  float p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p = __builtin_fmaf(v[i], v[i], p);
+  const float sum = block_tree256(p, red);
+  const float nf = 1.0f / __builtin_sqrtf(sum / 1024.0f + 1e-6f);
+  float o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (v[i] * nf) * (1.0f + wf[i]);
+  *reinterpret_cast<uint2*>(y + base) = pack4h(o);
+}
+
+// Per-head RMSNorm(1+w) over rows of 256 (one wave per row, 4 rows per block).
+__global__ __launch_bounds__(256) void rmsnorm256_kernel(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ w,
+                                                         uint16_t* __restrict__ y, int rows) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float v[4];
+  load4h(x + (size_t)row * kHeadDim + 4 * lane, v);
+  head_norm_wave(v, w, lane);
+  *reinterpret_cast<uint2*>(y + (size_t)row * kHeadDim + 4 * lane) = pack4h(v);
+}
+
+__global__ void silu_gate_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                 uint16_t* __restrict__ y, long long n) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+    y[i] = spk::f2h(spk::silu_det(spk::h2f(g[i])) * spk::h2f(u[i]));
+}
+
+__global__ void residual_add_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                                    uint16_t* __restrict__ y, long long n) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+    y[i] = spk::f2h(spk::h2f(a[i]) + spk::h2f(b[i]));
+}
+
+// embedding_lookup.comp: y[t] = E[tokens[t]] (rows of 1024); ids outside
+// [0, vocab) give a zero row.
+__global__ __launch_bounds__(128) void embedding_kernel(const uint16_t* __restrict__ E,
+                                                        const int32_t* __restrict__ tokens, int vocab,
+                                                        uint16_t* __restrict__ y) {
+  const int t = blockIdx.x;
+  const int id = tokens[t];
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (id >= 0 && id < vocab) v = reinterpret_cast<const uint4*>(E + (size_t)id * kHidden)[threadIdx.x];
+  reinterpret_cast<uint4*>(y + (size_t)t * kHidden)[threadIdx.x] = v;
+}
+
+__global__ void add_i32_kernel(int32_t* p, int32_t delta) {
+  if (threadIdx.x == 0) p[0] += delta;
+}
+
+__global__ void record_token_kernel(const int32_t* token, int32_t* pos, int32_t* count, int32_t* history, int cap) {
+  if (threadIdx.x == 0) {
+    const int i = count[0];
+    if (i >= 0 && i < cap) history[i] = token[0];
+    count[0] = i + 1;
+    pos[0] = pos[0] + 1;
+  }
+}
+
+int grid_for(long long n) {
+  long long b = (n + 255) / 256;
+  return (int)(b > 4096 ? 4096 : (b < 1 ? 1 : b));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+
+extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count,
+                              spk_stream_t stream) {
+  if (!in || (count > 0 && !outs)) return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: NULL argument");
+  if (count < 1 || count > kMaxOut) return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: count %d (1..%d)", count, kMaxOut);
+  const int in_dim = in->in_dim;
+  if (in->kind < SPK_GEMV_IN_PLAIN || in->kind > SPK_GEMV_IN_SILU_GATE)
+    return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: input kind %d", in->kind);
+  if (in_dim <= 0 || in_dim % 512 != 0 || in_dim > kMaxIn)
+    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: in_dim %d (multiple of 512, <= %d)", in_dim, kMaxIn);
+  if (in->kind == SPK_GEMV_IN_RMSNORM && in_dim != kHidden)
+    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: RMSNorm input needs in_dim %d", kHidden);
+  if (!in->x || (in->kind != SPK_GEMV_IN_PLAIN && !in->x2))
+    return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: NULL input vector");
+  if (in->kind != SPK_GEMV_IN_RMSNORM && (in->token || in->h_out))
+    return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: token/h_out need the RMSNorm input");
+  if (in->token && in->token_rows <= 0)
+    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: token_rows %d", in->token_rows);
+  if (!spk::aligned(in->x, 16) || (in->x2 && !spk::aligned(in->x2, 16)) || (in->h_out && !spk::aligned(in->h_out, 16)))
+    return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: input vectors must be 16-byte aligned");
+  FusedGemv a;
+  a.kind = in->kind;
+  a.in_dim = in_dim;
+  a.x = in->x;
+  a.x2 = in->x2;
+  a.token = in->token;
+  a.token_rows = in->token_rows;
+  a.h_out = in->h_out;
+  a.count = count;
+  const int n8 = in_dim / 512;
+  const int R = n8 <= 2 ? 2 : 1;
+  int blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    const SpkGemvOutput& o = outs[i];
+    if (!o.W || !o.y) return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: output %d has a NULL pointer", i);
+    if (o.out_dim <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: output %d out_dim %d", i, o.out_dim);
+    if (!spk::aligned(o.W, 16)) return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: W %d must be 16-byte aligned", i);
+    // y may be the residual (in-place update of the stream) but never an input of this launch.
+    if (o.y == in->x || o.y == in->x2)
+      return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: output %d aliases the input vector", i);
+    a.W[i] = o.W;
+    a.y[i] = o.y;
+    a.res[i] = o.residual;
+    a.out_dim[i] = o.out_dim;
+    a.first_block[i] = blocks;
+    blocks += (o.out_dim + 4 * R - 1) / (4 * R);
+  }
+  for (int i = count; i < kMaxOut; ++i) {
+    a.W[i] = nullptr; a.y[i] = nullptr; a.res[i] = nullptr; a.out_dim[i] = 0; a.first_block[i] = blocks;
+  }
+  a.first_block[kMaxOut] = blocks;
+  hipStream_t s = spk::to_hip(stream);
+  switch (n8) {
+    case 1: hipLaunchKernelGGL((fused_gemv_kernel<1, 2>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((fused_gemv_kernel<2, 2>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((fused_gemv_kernel<3, 1>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((fused_gemv_kernel<4, 1>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((fused_gemv_kernel<5, 1>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((fused_gemv_kernel<6, 1>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 7: hipLaunchKernelGGL((fused_gemv_kernel<7, 1>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((fused_gemv_kernel<8, 1>), dim3(blocks), dim3(256), 0, s, a); break;
+    default: return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: in_dim %d", in_dim);
+  }
+  return spk::check_launch("spk_gemv_fused");
+}
+
+extern "C" size_t spk_attention_workspace_size(int32_t positions, int32_t tokens) {
+  if (positions <= 0 || tokens <= 0) return 0;
+  const size_t nb = ((size_t)positions + kAttnBlock - 1) / kAttnBlock;
+  return (((size_t)tokens * kQHeads * nb * kPartFloats * sizeof(float)) + 255) / 256 * 256;
+}
+
+static int attention_common(const SpkAttnArgs* p, int T, int positions, const char* who, AttnArgs& a) {
+  if (!p) return spk::fail(SPK_ERR_NULL, "%s: NULL args", who);
+  if (!p->qg || !p->k || !p->v || !p->q_norm_w || !p->k_norm_w || !p->rope || !p->kv_cache || !p->out ||
+      !p->workspace)
+    return spk::fail(SPK_ERR_NULL, "%s: NULL pointer", who);
+  if (p->max_seq <= 0 || T <= 0) return spk::fail(SPK_ERR_SHAPE, "%s: max_seq %d tokens %d", who, p->max_seq, T);
+  if (p->workspace_bytes < spk_attention_workspace_size(positions, T))
+    return spk::fail(SPK_ERR_ARG, "%s: workspace %zu < %zu bytes", who, p->workspace_bytes,
+                     spk_attention_workspace_size(positions, T));
+  const void* ptrs[] = {p->qg, p->k, p->v, p->q_norm_w, p->k_norm_w, p->kv_cache, p->out, p->workspace};
+  for (const void* q : ptrs)
+    if (!spk::aligned(q, 16)) return spk::fail(SPK_ERR_ALIGN, "%s: buffers must be 16-byte aligned", who);
+  a.qg = p->qg;
+  a.k = p->k;
+  a.v = p->v;
+  a.q_norm_w = p->q_norm_w;
+  a.k_norm_w = p->k_norm_w;
+  a.rope = p->rope;
+  a.kv = p->kv_cache;
+  a.max_seq = p->max_seq;
+  a.out = p->out;
+  a.part = static_cast<float*>(p->workspace);
+  a.max_blocks = (positions + kAttnBlock - 1) / kAttnBlock;
+  return SPK_OK;
+}
+
+extern "C" int spk_attention_decode(const SpkAttnArgs* p, spk_stream_t stream) {
+  AttnArgs a;
+  int rc = attention_common(p, 1, p ? p->max_seq : 0, "spk_attention_decode", a);
+  if (rc) return rc;
+  if (!p->pos_dev) return spk::fail(SPK_ERR_NULL, "spk_attention_decode: NULL pos_dev");
+  a.pos_dev = p->pos_dev;
+  a.pos0 = 0;
+  a.store_kv = 1;
+  hipStream_t s = spk::to_hip(stream);
+  hipLaunchKernelGGL(attn_blocks_kernel, dim3(a.max_blocks, kKvHeads, 1), dim3(256), 0, s, a);
+  rc = spk::check_launch("spk_attention_decode (blocks)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(kQHeads, 1), dim3(256), 0, s, a);
+  return spk::check_launch("spk_attention_decode (combine)");
+}
+
+extern "C" int spk_attention_prefill(const SpkAttnArgs* p, int32_t pos0, int32_t tokens, spk_stream_t stream) {
+  if (!p) return spk::fail(SPK_ERR_NULL, "spk_attention_prefill: NULL args");
+  if (pos0 < 0 || tokens <= 0 || pos0 + tokens > p->max_seq)
+    return spk::fail(SPK_ERR_SHAPE, "spk_attention_prefill: positions [%d, %d) exceed max_seq %d", pos0,
+                     pos0 + tokens, p->max_seq);
+  AttnArgs a;
+  int rc = attention_common(p, tokens, pos0 + tokens, "spk_attention_prefill", a);
+  if (rc) return rc;
+  a.pos_dev = nullptr;
+  a.pos0 = pos0;
+  a.store_kv = 0;
+  hipStream_t s = spk::to_hip(stream);
+  // Tokens read the K/V rows of earlier tokens of the same call: all rows are
+  // stored by one launch before the block passes read them.
+  hipLaunchKernelGGL(attn_store_kv_kernel, dim3(tokens, kKvHeads), dim3(64), 0, s, a);
+  rc = spk::check_launch("spk_attention_prefill (store)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_blocks_kernel, dim3(a.max_blocks, kKvHeads, tokens), dim3(256), 0, s, a);
+  rc = spk::check_launch("spk_attention_prefill (blocks)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(kQHeads, tokens), dim3(256), 0, s, a);
+  return spk::check_launch("spk_attention_prefill (combine)");
+}
+
+extern "C" int spk_rmsnorm_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int32_t rows, int32_t n,
+                               spk_stream_t stream) {
+  if (!x || !w || !y) return spk::fail(SPK_ERR_NULL, "spk_rmsnorm_f16: NULL pointer");
+  if (rows <= 0 || (n != kHidden && n != kHeadDim))
+    return spk::fail(SPK_ERR_SHAPE, "spk_rmsnorm_f16: rows %d n %d (n must be 1024 or 256)", rows, n);
+  if (!spk::aligned(x, 8) || !spk::aligned(w, 8) || !spk::aligned(y, 8))
+    return spk::fail(SPK_ERR_ALIGN, "spk_rmsnorm_f16: 8-byte alignment required");
+  hipStream_t s = spk::to_hip(stream);
+  if (n == kHidden)
+    hipLaunchKernelGGL(rmsnorm1024_kernel, dim3(rows), dim3(256), 0, s, x, w, y);
+  else
+    hipLaunchKernelGGL(rmsnorm256_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, w, y, rows);
+  return spk::check_launch("spk_rmsnorm_f16");
+}
+
+extern "C" int spk_silu_gate_f16(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n, spk_stream_t stream) {
+  if (!g || !u || !y) return spk::fail(SPK_ERR_NULL, "spk_silu_gate_f16: NULL pointer");
+  if (n <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_silu_gate_f16: n %lld", (long long)n);
+  hipLaunchKernelGGL(silu_gate_kernel, dim3(grid_for(n)), dim3(256), 0, spk::to_hip(stream), g, u, y, (long long)n);
+  return spk::check_launch("spk_silu_gate_f16");
+}
+
+extern "C" int spk_residual_add_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, int64_t n,
+                                    spk_stream_t stream) {
+  if (!a || !b || !y) return spk::fail(SPK_ERR_NULL, "spk_residual_add_f16: NULL pointer");
+  if (n <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_residual_add_f16: n %lld", (long long)n);
+  hipLaunchKernelGGL(residual_add_kernel, dim3(grid_for(n)), dim3(256), 0, spk::to_hip(stream), a, b, y, (long long)n);
+  return spk::check_launch("spk_residual_add_f16");
+}
+
+extern "C" int spk_embedding_f16(const uint16_t* E, const int32_t* tokens, int32_t n_tokens, int32_t vocab,
+                                 uint16_t* y, spk_stream_t stream) {
+  if (!E || !tokens || !y) return spk::fail(SPK_ERR_NULL, "spk_embedding_f16: NULL pointer");
+  if (n_tokens <= 0 || vocab <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_embedding_f16: %d tokens, vocab %d", n_tokens, vocab);
+  if (!spk::aligned(E, 16) || !spk::aligned(y, 16)) return spk::fail(SPK_ERR_ALIGN, "spk_embedding_f16: 16-byte alignment");
+  hipLaunchKernelGGL(embedding_kernel, dim3(n_tokens), dim3(128), 0, spk::to_hip(stream), E, tokens, vocab, y);
+  return spk::check_launch("spk_embedding_f16");
+}
+
+extern "C" int spk_add_i32(int32_t* p, int32_t delta, spk_stream_t stream) {
+  if (!p) return spk::fail(SPK_ERR_NULL, "spk_add_i32: NULL pointer");
+  hipLaunchKernelGGL(add_i32_kernel, dim3(1), dim3(64), 0, spk::to_hip(stream), p, delta);
+  return spk::check_launch("spk_add_i32");
+}
+
+extern "C" int spk_record_token(const int32_t* token, int32_t* pos, int32_t* count, int32_t* history,
+                                int32_t capacity, spk_stream_t stream) {
+  if (!token || !pos || !count || !history) return spk::fail(SPK_ERR_NULL, "spk_record_token: NULL pointer");
+  hipLaunchKernelGGL(record_token_kernel, dim3(1), dim3(64), 0, spk::to_hip(stream), token, pos, count, history,
+                     capacity);
+  return spk::check_launch("spk_record_token");
+}

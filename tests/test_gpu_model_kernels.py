@@ -1,0 +1,375 @@
+"""GPU parity of the Qwen3.5 model kernels (include/spock_hip.h, model section)
+against the oracle (oracle/model.h).
+
+Bar: bit-exact fp16 outputs for every decode-path kernel (fused projections,
+attention, norms, gates, DeltaNet prompt conv / g / beta / gated norm), whose
+operation order the oracle restates; the MFMA prompt GEMM is checked against
+an fp64 product within the fp32-accumulation error bound K 2^-24 sum|a w| plus
+one fp16 rounding (its accumulation order is the matrix cores', not the
+matvec's), and must be correctly rounded for the typical element.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _h(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.float16)).to(dev)
+
+
+def _f(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+
+
+def _u16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def _rand16(seed, n, std=1.0):
+    from spock_amd import synth
+    return synth.f16(synth.normal(seed, n, std=std))
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _om():
+    import oracle_model
+    return oracle_model.lib()
+
+
+def _orc_matvec(W, x):
+    out = np.zeros(W.shape[0], np.uint16)
+    _om().orc_matmul_rows(_p(W), _p(x), _p(out), W.shape[0], W.shape[1], 1)
+    return out
+
+
+def _gemv(inp, outs):
+    from spock_amd import _lib
+    arr = (_lib.SpkGemvOutput * len(outs))()
+    for i, (W, y, res, n) in enumerate(outs):
+        arr[i].W, arr[i].y, arr[i].residual, arr[i].out_dim = W, y, res, n
+    _lib.check(_lib.lib().spk_gemv_fused(C.byref(inp), arr, len(outs), _stream()), "spk_gemv_fused")
+
+
+def test_gemv_rmsnorm_with_embedding_row(dev):
+    from spock_amd import _lib
+    print("[gemv rmsnorm+token]", flush=True)
+    V = 512
+    E = _rand16(1, V * 1024, 0.02).reshape(V, 1024)
+    w = _rand16(2, 1024, 0.02)
+    shapes = [6144, 2048, 16, 16]
+    Ws = [_rand16(10 + i, n * 1024, 0.02).reshape(n, 1024) for i, n in enumerate(shapes)]
+    tok = 317
+    dE, dw = _h(E, dev), _h(w, dev)
+    dWs = [_h(W, dev) for W in Ws]
+    ys = [torch.empty(n, dtype=torch.float16, device=dev) for n in shapes]
+    h_out = torch.empty(1024, dtype=torch.float16, device=dev)
+    dtok = torch.tensor([tok], dtype=torch.int32, device=dev)
+    inp = _lib.SpkGemvInput()
+    inp.kind, inp.in_dim, inp.x, inp.x2 = _lib.SPK_GEMV_IN_RMSNORM, 1024, dE.data_ptr(), dw.data_ptr()
+    inp.token, inp.token_rows, inp.h_out = dtok.data_ptr(), V, h_out.data_ptr()
+    _gemv(inp, [(W.data_ptr(), y.data_ptr(), None, n) for W, y, n in zip(dWs, ys, shapes)])
+    torch.cuda.synchronize()
+    xn = np.zeros(1024, np.uint16)
+    _om().orc_rmsnorm1024(_p(np.ascontiguousarray(E[tok])), _p(w), _p(xn))
+    assert np.array_equal(_u16(h_out), E[tok])
+    for W, y in zip(Ws, ys):
+        assert np.array_equal(_u16(y), _orc_matvec(W, xn))
+
+
+@pytest.mark.parametrize("in_dim,silu", [(2048, False), (3584, True), (1024, False), (512, True)])
+def test_gemv_plain_or_silu_with_residual_in_place(dev, in_dim, silu):
+    from spock_amd import _lib
+    print(f"[gemv in={in_dim} silu={silu}]", flush=True)
+    n = 1024
+    W = _rand16(20, n * in_dim, 0.02).reshape(n, in_dim)
+    x = _rand16(21, in_dim)
+    u = _rand16(22, in_dim)
+    r = _rand16(23, n)
+    dW, dx, du, dr = _h(W, dev), _h(x, dev), _h(u, dev), _h(r, dev)
+    inp = _lib.SpkGemvInput()
+    inp.kind = _lib.SPK_GEMV_IN_SILU_GATE if silu else _lib.SPK_GEMV_IN_PLAIN
+    inp.in_dim, inp.x, inp.x2 = in_dim, dx.data_ptr(), du.data_ptr() if silu else None
+    _gemv(inp, [(dW.data_ptr(), dr.data_ptr(), dr.data_ptr(), n)])
+    torch.cuda.synchronize()
+    xin = x
+    if silu:
+        xin = np.zeros(in_dim, np.uint16)
+        _om().orc_silu_gate(_p(x), _p(u), _p(xin), in_dim)
+    d = _orc_matvec(W, xin)
+    exp = np.zeros(n, np.uint16)
+    _om().orc_residual_add(_p(r), _p(d), _p(exp), n)
+    assert np.array_equal(_u16(dr), exp)
+
+
+def test_gemv_rejects_aliasing_and_shapes(dev):
+    from spock_amd import _lib
+    x = torch.zeros(1024, dtype=torch.float16, device=dev)
+    W = torch.zeros(16, 1024, dtype=torch.float16, device=dev)
+    inp = _lib.SpkGemvInput()
+    inp.kind, inp.in_dim, inp.x = _lib.SPK_GEMV_IN_PLAIN, 1024, x.data_ptr()
+    arr = (_lib.SpkGemvOutput * 1)()
+    arr[0].W, arr[0].y, arr[0].out_dim = W.data_ptr(), x.data_ptr(), 16
+    assert _lib.lib().spk_gemv_fused(C.byref(inp), arr, 1, _stream()) == -5
+    inp.kind, inp.in_dim = _lib.SPK_GEMV_IN_RMSNORM, 2048
+    assert _lib.lib().spk_gemv_fused(C.byref(inp), arr, 1, _stream()) == -2
+
+
+def _attn_inputs(seed, max_seq, pos, T=1):
+    import oracle_model
+    rope = np.zeros(max_seq * 64, np.float32)
+    oracle_model.lib().orc_rope_table(max_seq, _p(rope))
+    kv = np.zeros(max_seq * 1024, np.uint16)
+    kv[: pos * 1024] = _rand16(seed, pos * 1024)
+    qg = _rand16(seed + 1, T * 4096)
+    k = _rand16(seed + 2, T * 512)
+    v = _rand16(seed + 3, T * 512)
+    qn = _rand16(seed + 4, 256, 0.02)
+    kn = _rand16(seed + 5, 256, 0.02)
+    return rope, kv, qg, k, v, qn, kn
+
+
+def _oracle_attention(rope, kv, qg, k, v, qn, kn, pos0, T):
+    """Per token in order: norms, RoPE, cache store, attention, sigmoid gate."""
+    L = _om()
+    kv = kv.copy()
+    out = np.zeros(T * 2048, np.uint16)
+    for t in range(T):
+        pos = pos0 + t
+        q = np.zeros(2048, np.uint16)
+        for h in range(8):
+            L.orc_head_rmsnorm256(_p(np.ascontiguousarray(qg[t * 4096 + h * 512: t * 4096 + h * 512 + 256])),
+                                  _p(qn), _p(q[h * 256:]))
+        kk = np.zeros(512, np.uint16)
+        for h in range(2):
+            L.orc_head_rmsnorm256(_p(np.ascontiguousarray(k[t * 512 + h * 256: t * 512 + h * 256 + 256])),
+                                  _p(kn), _p(kk[h * 256:]))
+        cs = np.ascontiguousarray(rope[pos * 64: pos * 64 + 64])
+        L.orc_rope_apply(_p(q), 8, _p(cs))
+        L.orc_rope_apply(_p(kk), 2, _p(cs))
+        kv[pos * 1024: pos * 1024 + 512] = kk
+        kv[pos * 1024 + 512: pos * 1024 + 1024] = v[t * 512: t * 512 + 512]
+        for h in range(8):
+            att = np.zeros(256, np.uint16)
+            L.orc_attend(_p(q[h * 256:]), _p(kv), h // 4, pos + 1, _p(att))
+            gate = np.ascontiguousarray(qg[t * 4096 + h * 512 + 256: t * 4096 + h * 512 + 512])
+            L.orc_sigmoid_gate(_p(att), _p(gate), _p(out[t * 2048 + h * 256:]), 256)
+    return out, kv
+
+
+def _attn_args(dev, rope, kv, qg, k, v, qn, kn, max_seq, T, positions):
+    from spock_amd import _lib
+    d = {n: _h(a, dev) for n, a in (("kv", kv), ("qg", qg), ("k", k), ("v", v), ("qn", qn), ("kn", kn))}
+    d["rope"] = _f(rope, dev)
+    d["out"] = torch.empty(T * 2048, dtype=torch.float16, device=dev)
+    ws = int(_lib.lib().spk_attention_workspace_size(positions, T))
+    d["ws"] = torch.empty(ws, dtype=torch.uint8, device=dev)
+    a = _lib.SpkAttnArgs()
+    a.qg, a.k, a.v = d["qg"].data_ptr(), d["k"].data_ptr(), d["v"].data_ptr()
+    a.q_norm_w, a.k_norm_w, a.rope = d["qn"].data_ptr(), d["kn"].data_ptr(), d["rope"].data_ptr()
+    a.kv_cache, a.max_seq, a.out = d["kv"].data_ptr(), max_seq, d["out"].data_ptr()
+    a.workspace, a.workspace_bytes = d["ws"].data_ptr(), ws
+    return a, d
+
+
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 511])
+def test_attention_decode_bitexact(dev, pos):
+    from spock_amd import _lib
+    print(f"[attention decode pos={pos}]", flush=True)
+    max_seq = 512
+    rope, kv, qg, k, v, qn, kn = _attn_inputs(100 + pos, max_seq, pos)
+    a, d = _attn_args(dev, rope, kv, qg, k, v, qn, kn, max_seq, 1, max_seq)
+    dpos = torch.tensor([pos], dtype=torch.int32, device=dev)
+    a.pos_dev = dpos.data_ptr()
+    _lib.check(_lib.lib().spk_attention_decode(C.byref(a), _stream()), "spk_attention_decode")
+    torch.cuda.synchronize()
+    exp, ekv = _oracle_attention(rope, kv, qg, k, v, qn, kn, pos, 1)
+    assert np.array_equal(_u16(d["kv"]), ekv)
+    assert np.array_equal(_u16(d["out"]), exp)
+
+
+@pytest.mark.parametrize("pos0,T", [(0, 1), (0, 70), (30, 100), (190, 66)])
+def test_attention_prefill_bitexact(dev, pos0, T):
+    from spock_amd import _lib
+    print(f"[attention prefill pos0={pos0} T={T}]", flush=True)
+    max_seq = 256
+    rope, kv, qg, k, v, qn, kn = _attn_inputs(200 + T, max_seq, pos0, T)
+    a, d = _attn_args(dev, rope, kv, qg, k, v, qn, kn, max_seq, T, pos0 + T)
+    _lib.check(_lib.lib().spk_attention_prefill(C.byref(a), pos0, T, _stream()), "spk_attention_prefill")
+    torch.cuda.synchronize()
+    exp, ekv = _oracle_attention(rope, kv, qg, k, v, qn, kn, pos0, T)
+    assert np.array_equal(_u16(d["kv"]), ekv)
+    assert np.array_equal(_u16(d["out"]), exp)
+
+
+def test_attention_decode_position_out_of_range_writes_nothing(dev):
+    from spock_amd import _lib
+    max_seq = 128
+    rope, kv, qg, k, v, qn, kn = _attn_inputs(7, max_seq, 5)
+    a, d = _attn_args(dev, rope, kv, qg, k, v, qn, kn, max_seq, 1, max_seq)
+    d["out"].fill_(0)
+    dpos = torch.tensor([max_seq], dtype=torch.int32, device=dev)
+    a.pos_dev = dpos.data_ptr()
+    _lib.check(_lib.lib().spk_attention_decode(C.byref(a), _stream()), "spk_attention_decode")
+    torch.cuda.synchronize()
+    assert np.array_equal(_u16(d["kv"]), kv)
+    assert not _u16(d["out"]).any()
+
+
+@pytest.mark.parametrize("n,rows", [(1024, 7), (256, 13)])
+def test_rmsnorm_rows_bitexact(dev, n, rows):
+    from spock_amd import _lib
+    x = _rand16(30 + n, rows * n)
+    w = _rand16(31, n, 0.02)
+    dx, dw = _h(x, dev), _h(w, dev)  # held until the kernel has run
+    y = torch.empty(rows * n, dtype=torch.float16, device=dev)
+    _lib.check(_lib.lib().spk_rmsnorm_f16(dx.data_ptr(), dw.data_ptr(), y.data_ptr(), rows, n, _stream()),
+               "spk_rmsnorm_f16")
+    torch.cuda.synchronize()
+    exp = np.zeros(rows * n, np.uint16)
+    fn = _om().orc_rmsnorm1024 if n == 1024 else _om().orc_head_rmsnorm256
+    for r in range(rows):
+        fn(_p(np.ascontiguousarray(x[r * n:(r + 1) * n])), _p(w), _p(exp[r * n:]))
+    assert np.array_equal(_u16(y), exp)
+
+
+def test_elementwise_gates_bitexact(dev):
+    from spock_amd import _lib
+    n = 100_003
+    g, u = _rand16(40, n, 3.0), _rand16(41, n)
+    dg, du = _h(g, dev), _h(u, dev)
+    y1 = torch.empty(n, dtype=torch.float16, device=dev)  # dg, du held above
+    y2 = torch.empty(n, dtype=torch.float16, device=dev)
+    L = _lib.lib()
+    _lib.check(L.spk_silu_gate_f16(dg.data_ptr(), du.data_ptr(), y1.data_ptr(), n, _stream()), "silu")
+    _lib.check(L.spk_residual_add_f16(dg.data_ptr(), du.data_ptr(), y2.data_ptr(), n, _stream()), "residual")
+    torch.cuda.synchronize()
+    e1, e2 = np.zeros(n, np.uint16), np.zeros(n, np.uint16)
+    _om().orc_silu_gate(_p(g), _p(u), _p(e1), n)
+    _om().orc_residual_add(_p(g), _p(u), _p(e2), n)
+    assert np.array_equal(_u16(y1), e1)
+    assert np.array_equal(_u16(y2), e2)
+
+
+def test_embedding_rows(dev):
+    from spock_amd import _lib
+    V = 300
+    E = _rand16(50, V * 1024, 0.02).reshape(V, 1024)
+    ids = np.array([0, 299, 17, -1, 300, 17], np.int32)
+    y = torch.empty(len(ids) * 1024, dtype=torch.float16, device=dev)
+    dE, dids = _h(E, dev), torch.from_numpy(ids).to(dev)
+    _lib.check(_lib.lib().spk_embedding_f16(dE.data_ptr(), dids.data_ptr(), len(ids), V, y.data_ptr(), _stream()),
+               "spk_embedding_f16")
+    torch.cuda.synchronize()
+    got = _u16(y).reshape(len(ids), 1024)
+    for i, t in enumerate(ids):
+        assert np.array_equal(got[i], E[t] if 0 <= t < V else np.zeros(1024, np.uint16))
+
+
+@pytest.mark.parametrize("T", [1, 5, 64, 133])
+def test_deltanet_prefill_conv_bitexact(dev, oracle, T):
+    from spock_amd import _lib
+    print(f"[dn prefill conv T={T}]", flush=True)
+    qkv = _rand16(60 + T, T * 6144).reshape(T, 6144)
+    cs0 = _rand16(61, 6144 * 4)
+    cw = _rand16(62, 6144 * 4, 0.3)
+    dq, dcs, dcw = _h(qkv, dev), _h(cs0, dev), _h(cw, dev)
+    hm = [torch.empty(16 * T * 128, dtype=torch.float16, device=dev) for _ in range(3)]
+    _lib.check(_lib.lib().spk_deltanet_prefill_conv(dq.data_ptr(), 6144, dcs.data_ptr(), dcw.data_ptr(), T,
+                                                    *[x.data_ptr() for x in hm], _stream()), "prefill conv")
+    torch.cuda.synchronize()
+    cs = cs0.copy()
+    exp = np.zeros((T, 6144), np.uint16)
+    for t in range(T):
+        row = qkv[t].copy()
+        oracle.lib().orc_conv_l2_qk(6144, 4, 2048, 16, _p(row), _p(cs), _p(cw))
+        exp[t] = row
+    assert np.array_equal(_u16(dcs), cs)
+    for j, x in enumerate(hm):
+        got = _u16(x).reshape(16, T, 128)
+        want = exp[:, j * 2048:(j + 1) * 2048].reshape(T, 16, 128).transpose(1, 0, 2)
+        assert np.array_equal(got, want), ["q", "k", "v"][j]
+
+
+def test_deltanet_prefill_gbeta_and_norm_gate_bitexact(dev, oracle):
+    from spock_amd import _lib
+    T, layer = 37, 2
+    a, b = _rand16(70, T * 16), _rand16(71, T * 16)
+    alb = np.stack([np.linspace(-1, 1, 3 * 16, dtype=np.float32),
+                    oracle.h2f(_rand16(72, 3 * 16, 0.1))], -1).astype(np.float32)
+    g = torch.empty(16 * T, dtype=torch.float32, device=dev)
+    beta = torch.empty(16 * T, dtype=torch.float32, device=dev)
+    da, db, dalb = _h(a, dev), _h(b, dev), _f(alb, dev)  # held until the kernels have run
+    _lib.check(_lib.lib().spk_deltanet_prefill_gbeta(da.data_ptr(), db.data_ptr(), 16, dalb.data_ptr(), layer, T,
+                                                     g.data_ptr(), beta.data_ptr(), _stream()), "gbeta")
+    core = np.random.default_rng(3).standard_normal((16, T, 128)).astype(np.float32)
+    z = _rand16(73, T * 2048)
+    nw = np.random.default_rng(4).uniform(0.5, 1.5, 128).astype(np.float32)
+    out = torch.empty(T * 2048, dtype=torch.float16, device=dev)
+    dcore, dz, dnw = _f(core, dev), _h(z, dev), _f(nw, dev)
+    _lib.check(_lib.lib().spk_deltanet_norm_gate(dcore.data_ptr(), T, dz.data_ptr(), 2048, dnw.data_ptr(), 1e-6, T,
+                                                 out.data_ptr(), 2048, _stream()), "norm gate")
+    torch.cuda.synchronize()
+    # g / beta: the decode shader's formula, one IEEE fp32 operation at a time
+    av = oracle.h2f(a).reshape(T, 16).T
+    bv = oracle.h2f(b).reshape(T, 16).T
+    al = alb.reshape(3, 16, 2)[layer]
+    f32 = np.float32
+    sp = oracle.logf((f32(1.0) + oracle.expf((av + al[:, 1:2]).astype(f32))).astype(f32))
+    eg = -oracle.expf(al[:, 0:1].astype(f32)) * sp
+    eb = f32(1.0) / (f32(1.0) + oracle.expf(-bv))
+    assert np.array_equal(g.cpu().numpy().reshape(16, T).view(np.uint32), eg.astype(f32).view(np.uint32))
+    assert np.array_equal(beta.cpu().numpy().reshape(16, T).view(np.uint32), eb.astype(f32).view(np.uint32))
+    # gated norm: 128-wide tree, fp16(w * o * r), then * silu(z)
+    s = (core * core).astype(f32)
+    for stride in (64, 32, 16, 8, 4, 2, 1):
+        s = (s[..., :stride] + s[..., stride:2 * stride]).astype(f32)
+    r = (f32(1.0) / np.sqrt((s[..., 0] / f32(128.0) + f32(1e-6)).astype(f32))).astype(f32)
+    weighted = oracle.h2f(oracle.f2h((nw * (core * r[..., None]).astype(f32)).astype(f32)))
+    zz = oracle.h2f(z).reshape(T, 16, 128).transpose(1, 0, 2)
+    silu = (zz / (f32(1.0) + oracle.expf(-zz))).astype(f32)
+    exp = oracle.f2h((weighted * silu).astype(f32)).transpose(1, 0, 2).reshape(-1)
+    assert np.array_equal(_u16(out), exp)
+
+
+@pytest.mark.parametrize("M,N,K,res", [(512, 6144, 1024, False), (37, 16, 1024, False), (100, 1000, 64, True),
+                                       (70, 1024, 3584, True)])
+def test_gemm_f16_against_fp64(dev, M, N, K, res):
+    from spock_amd import _lib
+    print(f"[gemm {M}x{N}x{K}]", flush=True)
+    A = _rand16(80, M * K).reshape(M, K)
+    W = _rand16(81, N * K, 0.02).reshape(N, K)
+    R = _rand16(82, M * N)
+    dA, dW = _h(A, dev), _h(W, dev)
+    C_ = _h(R, dev) if res else torch.empty(M * N, dtype=torch.float16, device=dev)
+    _lib.check(_lib.lib().spk_gemm_f16(dA.data_ptr(), K, dW.data_ptr(), K, C_.data_ptr(), N,
+                                       C_.data_ptr() if res else None, M, N, K, _stream()), "spk_gemm_f16")
+    torch.cuda.synchronize()
+    a64 = A.view(np.float16).astype(np.float64)
+    w64 = W.view(np.float16).astype(np.float64)
+    dot = a64 @ w64.T
+    # fp32 accumulation in any order: |acc - dot| <= K 2^-24 sum|a w|; then one
+    # fp16 rounding of the product and, with a residual, one of the sum
+    bound = K * 2.0 ** -24 * (np.abs(a64) @ np.abs(w64).T)
+    ulp = lambda v: 2.0 ** (np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -14))) - 10)
+    r16 = lambda v: v.astype(np.float16).astype(np.float64)
+    got = _u16(C_).reshape(M, N).view(np.float16).astype(np.float64)
+    want = r16(dot)
+    tol = bound + ulp(dot)
+    if res:
+        r = R.view(np.float16).reshape(M, N).astype(np.float64)
+        want = r16(r + want)
+        tol = tol + ulp(r + dot)
+    assert np.all(np.abs(got - (r + dot if res else dot)) <= tol), "outside the accumulation error bound"
+    # and the typical element equals the correctly rounded value
+    assert np.mean(got == want) > 0.95

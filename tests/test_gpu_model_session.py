@@ -1,0 +1,93 @@
+"""GPU parity of the Qwen3.5-shaped decode session (include/spock_model.h)
+against the oracle's full model (oracle/model.h) on seeded synthetic artifacts.
+
+* Decode: from an identical state (the oracle's, after its prefill), every
+  decode step gives bit-identical greedy tokens, fp16 logits and hidden state
+  (the per-token operation order is the oracle's), with and without the
+  recorded HIP graph.
+* Prefill with MFMA projections and the MFMA chunk rule: close to the oracle
+  (fp32 accumulation order differs), same greedy token.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, VOCAB, SEED, MAX_SEQ = 4, 8192, 11, 256
+
+
+@pytest.fixture(scope="module")
+def small_artifact(tmp_path_factory):
+    from spock_amd import model
+    p = tmp_path_factory.mktemp("art") / "small"
+    model.write_synthetic_artifact(p, layers=LAYERS, vocab=VOCAB, seed=SEED)
+    return p
+
+
+def _prompt(n, seed=5):
+    from spock_amd import synth
+    return (synth.splitmix64(seed, n) % np.uint64(VOCAB)).astype(np.int32)
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_decode_from_oracle_state_bitexact(dev, small_artifact, use_graph):
+    import oracle_model
+    from spock_amd import model
+    print(f"[session decode graph={use_graph}]", flush=True)
+    om = oracle_model.OracleModel(small_artifact, max_seq=MAX_SEQ)
+    prompt = _prompt(70)
+    tok = om.prefill(prompt)
+    snap = om.snapshot()
+    want = []
+    t = tok
+    for i in range(12):
+        t, logits, hidden = om.decode(t, want_logits=True)
+        want.append(t)
+    with model.Session(small_artifact, max_seq=MAX_SEQ, use_graph=use_graph) as s:
+        s.set_state(snap["dn_state"], snap["conv"], snap["kv"], snap["pos"], tok)
+        got = s.decode(12)
+        glogits, ghidden = s.last_output()
+        st = s.get_state()
+    assert got.tolist() == want
+    assert np.array_equal(ghidden, hidden)
+    assert np.array_equal(glogits, logits)
+    assert st["pos"] == 70 + 12
+    assert np.array_equal(st["dn_state"].view(np.uint32), om.snapshot()["dn_state"].view(np.uint32))
+    assert np.array_equal(st["conv"], om.snapshot()["conv"])
+    assert np.array_equal(st["kv"], om.snapshot()["kv"])
+
+
+def test_prefill_close_to_oracle(dev, small_artifact):
+    import oracle_model
+    from spock_amd import model
+    print("[session prefill]", flush=True)
+    om = oracle_model.OracleModel(small_artifact, max_seq=MAX_SEQ)
+    prompt = _prompt(133, seed=9)
+    tok, logits, hidden = om.prefill(prompt, want_logits=True)
+    with model.Session(small_artifact, max_seq=MAX_SEQ) as s:
+        gtok = s.prefill(prompt)
+        glogits, ghidden = s.last_output()
+        st = s.get_state()
+    lf = logits.view(np.float16).astype(np.float32)
+    gf = glogits.view(np.float16).astype(np.float32)
+    diff = float(np.max(np.abs(lf - gf)))
+    sd = float(np.max(np.abs(st["dn_state"] - om.snapshot()["dn_state"])))
+    print(f"prefill: max |logit diff| {diff:.4g}, max |state diff| {sd:.3g}, tokens {gtok} vs {tok}")
+    assert gtok == tok
+    assert diff <= 0.05
+    assert sd <= 1e-2
+    assert st["pos"] == 133
+
+
+def test_generate_api_and_errors(dev, small_artifact):
+    from spock_amd import model
+    with model.Session(small_artifact, max_seq=64) as s:
+        r = s.generate(_prompt(20), 10)
+        assert len(r.tokens) == 10 and r.decode_steps == 9 and r.used_graph
+        assert all(0 <= t < VOCAB for t in r.tokens)
+        r2 = s.generate(_prompt(20), 10)  # decode() resets: same prompt, same tokens
+        assert r2.tokens.tolist() == r.tokens.tolist()
+        with pytest.raises(model.ModelError, match="max_seq"):
+            s.generate(_prompt(60), 10)
+        with pytest.raises(model.ModelError, match="vocab"):
+            s.prefill([VOCAB + 1])
