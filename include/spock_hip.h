@@ -325,6 +325,27 @@ int spk_deltanet_norm_gate(const float* core, int64_t core_head_stride, const ui
 int spk_record_token(const int32_t* token, int32_t* pos, int32_t* count, int32_t* history,
                      int32_t capacity, spk_stream_t stream);
 
+/* ---- prompt-wide kernels in the CPU restatement's operation order -------
+ * The parity forms of spk_gemm_f16 and spk_chunk_prefill: bit-identical to
+ * the oracle, so a prompt prefilled with them leaves exactly the state (and
+ * greedy tokens) of the CPU path.  They trade the matrix cores for the
+ * reference's sequential reduction orders. */
+
+/* Y[t][r] (+ residual as in spk_gemm_f16) for every row t of X: each output
+ * bit-identical to spk_matvec_f16 of X's row t (the matvec_tiled /
+ * lm_head_tiled order).  in_dim % 64 == 0, in_dim <= 4096. */
+int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t ldx, uint16_t* Y,
+                        int64_t ldy, const uint16_t* residual, int32_t rows, int32_t out_dim,
+                        int32_t in_dim, spk_stream_t stream);
+
+/* run_deltanet_chunk_rule (deltanet_chunk.cpp:53-284) with the reference's
+ * loop nests and sequential reductions, exp = the library's deterministic exp;
+ * one sequence (cu_seqlens NULL), dk == dv == 128, chunk_size == 64;
+ * initial_state must not alias out_state.  Same argument struct as
+ * spk_chunk_prefill; workspace of spk_chunk_prefill_ordered_workspace_size(). */
+size_t spk_chunk_prefill_ordered_workspace_size(int32_t num_heads, int32_t total_tokens);
+int spk_chunk_prefill_ordered(const SpkChunkArgs* args, spk_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Diagnostics (no reference counterpart).
  * ---------------------------------------------------------------------- */

@@ -41,10 +41,19 @@ typedef struct SpkGenerateStats {
 
 const char* spk_model_last_error(void);
 
+/* spk_model_open flags */
+enum {
+  SPK_MODEL_NO_GRAPH = 1,       /* launch the decode step's kernels one by one */
+  SPK_MODEL_MATRIX_PREFILL = 2  /* prompt on the matrix cores (spk_gemm_f16, MFMA
+                                   chunk rule) instead of the default order of
+                                   the CPU restatement (bit-identical prefill) */
+};
+
 /* Opens <repack_dir>, uploads every tensor, allocates the per-layer state for
- * max_seq positions (<= 0: 2048, the reference's MAX_SEQ).  use_graph != 0
- * replays the decode step as a HIP graph.  NULL on error. */
-SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int32_t use_graph);
+ * max_seq positions (<= 0: 2048, the reference's MAX_SEQ).  By default the
+ * decode step is replayed as a HIP graph and the prompt is prefilled in the
+ * CPU restatement's order.  NULL on error. */
+SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int32_t flags);
 void spk_model_close(SpkModel* m);
 
 /* Model shape as read from the artifact. */

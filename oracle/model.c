@@ -336,8 +336,8 @@ static void dn_mixer(const OrcModel* m, OrcModelState* st, const OrcLayer* ly, c
 #pragma omp parallel for schedule(static)
       for (int32_t h = 0; h < ORC_DN_HEADS; ++h) {
         const size_t o = (size_t)h * T;
-        orc_chunk_rule(1, (size_t)T, 128, 128, 64, 0, q + o * 128, k + o * 128, v + o * 128, g + o,
-                       beta + o, init + (size_t)h * 128 * 128, core + o * 128, S + (size_t)h * 128 * 128);
+        orc_chunk_rule_det(1, (size_t)T, 128, 128, 64, 0, q + o * 128, k + o * 128, v + o * 128, g + o,
+                           beta + o, init + (size_t)h * 128 * 128, core + o * 128, S + (size_t)h * 128 * 128);
       }
     } else {
 #pragma omp parallel for schedule(static)

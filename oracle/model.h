@@ -31,9 +31,10 @@
  *   exp/log: orc_expf/orc_logf.
  * Prefill (HF semantics, modeling_qwen3_5.py:519-530): layer-major over the
  * prompt; every per-token operation is the decode one, except that the
- * DeltaNet recurrence over the prompt is the chunk rule (orc_chunk_rule,
- * C = 64, q/k already L2-normalised in fp16, initial state = the layer's
- * state) and the norm-gate uses its fp32 core output.
+ * DeltaNet recurrence over the prompt is the chunk rule (orc_chunk_rule_det:
+ * run_deltanet_chunk_rule's loops with orc_expf; C = 64, q/k already
+ * L2-normalised in fp16, initial state = the layer's state) and the
+ * norm-gate uses its fp32 core output.
  */
 #ifndef SPOCK_ORACLE_MODEL_H
 #define SPOCK_ORACLE_MODEL_H

@@ -171,8 +171,9 @@ void orc_logf_array(const float* in, float* out, size_t n) {
 
 /* ------------------------------------------------------------------------ */
 /* Chunk rule: deltanet_chunk.cpp:53-284, same loop nests and operation     */
-/* order, std::exp(float) -> expf, so that it matches the compiled          */
-/* reference bit for bit under -ffp-contract=off.                           */
+/* order; std::exp(float) is exp_fn: the C library's expf reproduces the    */
+/* compiled reference bit for bit under -ffp-contract=off, orc_expf gives   */
+/* the variant the GPU evaluates identically.                               */
 /* ------------------------------------------------------------------------ */
 
 static inline size_t qkv_index(size_t head, size_t token, size_t dim, size_t seq, size_t width) {
@@ -191,10 +192,11 @@ static void l2_norm_token(float* values, size_t head, size_t token, size_t seq, 
   for (size_t d = 0; d < width; ++d) values[qkv_index(head, token, d, seq, width)] *= inv_norm;
 }
 
-int orc_chunk_rule(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t chunk,
-                   int use_qk_l2norm, const float* q_in, const float* k_in,
-                   const float* v_in, const float* g_in, const float* beta_in,
-                   const float* init, float* out_core, float* out_state) {
+static int chunk_rule_impl(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t chunk,
+                           int use_qk_l2norm, const float* q_in, const float* k_in,
+                           const float* v_in, const float* g_in, const float* beta_in,
+                           const float* init, float* out_core, float* out_state,
+                           float (*exp_fn)(float)) {
   if (heads == 0 || seq == 0 || k_dim == 0 || v_dim == 0 || chunk == 0) return -1;
 
   float* query = (float*)malloc(heads * seq * k_dim * sizeof(float));
@@ -268,7 +270,7 @@ int orc_chunk_rule(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t 
       memset(decay, 0, chunk * chunk * 4);                    /* :153-159 */
       memset(attn, 0, chunk * chunk * 4);
       for (size_t r = 0; r < chunk; ++r)
-        for (size_t c = 0; c <= r; ++c) decay[r * chunk + c] = expf(gcum[r] - gcum[c]);
+        for (size_t c = 0; c <= r; ++c) decay[r * chunk + c] = exp_fn(gcum[r] - gcum[c]);
       for (size_t r = 0; r < chunk; ++r)                      /* :161-170 */
         for (size_t c = 0; c < r; ++c) {
           float dot = 0.0f;
@@ -292,7 +294,7 @@ int orc_chunk_rule(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t 
           const float coeff = attn[r * chunk + c];
           if (coeff == 0.0f) continue;
           const float bcol = bc[c];
-          const float egc = expf(gcum[c]);
+          const float egc = exp_fn(gcum[c]);
           for (size_t vd = 0; vd < v_dim; ++vd) solved[r * v_dim + vd] += coeff * (vc[c * v_dim + vd] * bcol);
           for (size_t kd = 0; kd < k_dim; ++kd) kcd[r * k_dim + kd] += coeff * (kc[c * k_dim + kd] * bcol * egc);
         }
@@ -304,7 +306,7 @@ int orc_chunk_rule(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t 
           local[r * chunk + c] = dot * decay[r * chunk + c];
         }
       for (size_t r = 0; r < chunk; ++r) {                    /* :215-233 */
-        const float egr = expf(gcum[r]);
+        const float egr = exp_fn(gcum[r]);
         for (size_t vd = 0; vd < v_dim; ++vd) {
           float carry = 0.0f, it = 0.0f;
           for (size_t kd = 0; kd < k_dim; ++kd) {
@@ -321,11 +323,11 @@ int orc_chunk_rule(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t 
           for (size_t c = 0; c <= r; ++c) sum += local[r * chunk + c] * vnew[c * v_dim + vd];
           core[qkv_index(h, base + r, vd, total, v_dim)] = sum;
         }
-      const float eglast = expf(gcum[chunk - 1]);             /* :246-268 */
+      const float eglast = exp_fn(gcum[chunk - 1]);             /* :246-268 */
       for (size_t i = 0; i < k_dim * v_dim; ++i) wstate[i] = S[i] * eglast;
       memset(upd, 0, k_dim * v_dim * 4);
       for (size_t r = 0; r < chunk; ++r) {
-        const float w = expf(gcum[chunk - 1] - gcum[r]);
+        const float w = exp_fn(gcum[chunk - 1] - gcum[r]);
         for (size_t kd = 0; kd < k_dim; ++kd) {
           const float sk = kc[r * k_dim + kd] * w;
           for (size_t vd = 0; vd < v_dim; ++vd) upd[kd * v_dim + vd] += sk * vnew[r * v_dim + vd];
@@ -342,6 +344,23 @@ int orc_chunk_rule(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t 
   free(decay); free(attn); free(solved); free(kcd); free(qc); free(kc); free(vc); free(gcum);
   free(bc); free(wstate); free(local); free(vnew); free(inter); free(upd); free(old_row);
   return 0;
+}
+
+int orc_chunk_rule(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t chunk,
+                   int use_qk_l2norm, const float* q_in, const float* k_in,
+                   const float* v_in, const float* g_in, const float* beta_in,
+                   const float* init, float* out_core, float* out_state) {
+  return chunk_rule_impl(heads, seq, k_dim, v_dim, chunk, use_qk_l2norm, q_in, k_in, v_in, g_in,
+                         beta_in, init, out_core, out_state, expf);
+}
+
+/* The same loops with orc_expf in place of the C library's expf. */
+int orc_chunk_rule_det(size_t heads, size_t seq, size_t k_dim, size_t v_dim, size_t chunk,
+                       int use_qk_l2norm, const float* q_in, const float* k_in,
+                       const float* v_in, const float* g_in, const float* beta_in,
+                       const float* init, float* out_core, float* out_state) {
+  return chunk_rule_impl(heads, seq, k_dim, v_dim, chunk, use_qk_l2norm, q_in, k_in, v_in, g_in,
+                         beta_in, init, out_core, out_state, orc_expf);
 }
 
 int orc_chunk_rule_varlen(size_t H, size_t N, size_t dk, size_t dv, size_t C,

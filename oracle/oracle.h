@@ -64,6 +64,14 @@ int orc_chunk_rule(size_t H, size_t T, size_t dk, size_t dv, size_t C,
                    const float* v, const float* g, const float* beta,
                    const float* init, float* out_core, float* out_state);
 
+/* orc_chunk_rule with every exp evaluated by orc_expf (the deterministic exp
+ * the GPU kernels share) instead of the C library's expf: the chunk rule of the
+ * full-model restatement (model.h) and of spk_chunk_prefill_ordered. */
+int orc_chunk_rule_det(size_t H, size_t T, size_t dk, size_t dv, size_t C,
+                       int use_qk_l2norm, const float* q, const float* k,
+                       const float* v, const float* g, const float* beta,
+                       const float* init, float* out_core, float* out_state);
+
 /* Packed varlen form: q/k/v are [H][N][d] with sequence s on tokens
  * [cu[s], cu[s+1]); each sequence is chunked from its own start.
  * init (nullable) and out_state are [S][H][dk][dv]; out_core is [H][N][dv]. */

@@ -1,0 +1,361 @@
+// exact.hip -- prompt-wide kernels in the operation order of the CPU
+// restatement, so a prompt processed on the GPU gives the same bits as the
+// oracle (and therefore the same greedy tokens downstream):
+//
+//   spk_matvec_f16_rows: the decode matvec (64 contiguous spans fma-chained
+//     from 0, then the s[l] += s[l+stride] tree, one fp16 rounding; the order
+//     of lm_head_tiled.comp) applied to every row of a prompt.  Each output is
+//     bit-identical to spk_matvec_f16 on that row.
+//   spk_chunk_prefill_ordered: run_deltanet_chunk_rule's loop nests
+//     (deltanet_chunk.cpp:53-284) with every reduction in the reference's
+//     sequential order and no contraction, exp = the library's deterministic
+//     exp (numerics.hpp).
+//
+// These are the parity forms of spk_gemm_f16 (matrix cores) and
+// spk_chunk_prefill (MFMA WY/UT kernels); they spend VALU cycles to keep the
+// reference's order and are used where bit-exact prompt results are required.
+#include "capi_common.hpp"
+#include "numerics.hpp"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// spk_matvec_f16_rows
+// ---------------------------------------------------------------------------
+constexpr int kTile = 64;  // 64 W rows x 64 prompt rows per 256-thread block
+
+struct RowsArgs {
+  const uint16_t* W;
+  const uint16_t* X;
+  long long ldx;
+  uint16_t* Y;
+  long long ldy;
+  const uint16_t* R;
+  int rows, out_dim, in_dim, span;
+};
+
+struct Acc16 {
+  float v[16];
+};
+
+// Leaf i (in bit-reversed order: span l = bitrev6(i)) of the 64-span tree for
+// the thread's 4 x 4 outputs.  The tree s[l] += s[l+32], ..., s[l] += s[l+1]
+// pairs spans whose indices differ in bit 5 first; visiting spans in
+// bit-reversed order makes every pair of neighbouring visits a pair of that
+// tree, so a recursive split of the visit order reproduces it exactly.
+__device__ __forceinline__ Acc16 leaf(const RowsArgs& a, int i, float (*Ws)[65], float (*Xs)[65], int r0, int t0) {
+  const int l = (int)(__builtin_bitreverse32((uint32_t)i) >> 26);
+  const int tid = threadIdx.x;
+  const int S = a.span;
+  __syncthreads();
+  for (int idx = tid; idx < kTile * S; idx += 256) {
+    const int row = idx / S, j = idx - (idx / S) * S;
+    const int wr = r0 + row, xr = t0 + row;
+    Ws[row][j] = wr < a.out_dim ? spk::h2f(a.W[(long long)wr * a.in_dim + l * S + j]) : 0.0f;
+    Xs[row][j] = xr < a.rows ? spk::h2f(a.X[(long long)xr * a.ldx + l * S + j]) : 0.0f;
+  }
+  __syncthreads();
+  const int tx = tid & 15, ty = tid >> 4;
+  Acc16 acc;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc.v[k] = 0.0f;
+  for (int j = 0; j < S; ++j) {
+    float w[4], x[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      w[q] = Ws[tx * 4 + q][j];
+      x[q] = Xs[ty * 4 + q][j];
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc.v[p * 4 + q] = __builtin_fmaf(w[p], x[q], acc.v[p * 4 + q]);
+  }
+  return acc;
+}
+
+template <int LEVEL>
+__device__ __forceinline__ Acc16 node(const RowsArgs& a, int j, float (*Ws)[65], float (*Xs)[65], int r0, int t0) {
+  if constexpr (LEVEL == 0) {
+    return leaf(a, j, Ws, Xs, r0, t0);
+  } else {
+    Acc16 lo = node<LEVEL - 1>(a, 2 * j, Ws, Xs, r0, t0);
+    const Acc16 hi = node<LEVEL - 1>(a, 2 * j + 1, Ws, Xs, r0, t0);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) lo.v[k] = lo.v[k] + hi.v[k];
+    return lo;
+  }
+}
+
+__global__ __launch_bounds__(256) void matvec_rows_kernel(RowsArgs a) {
+  __shared__ float Ws[kTile][65];
+  __shared__ float Xs[kTile][65];
+  const int r0 = blockIdx.x * kTile, t0 = blockIdx.y * kTile;
+  const Acc16 s = node<6>(a, 0, Ws, Xs, r0, t0);
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = r0 + tx * 4 + p, t = t0 + ty * 4 + q;
+      if (r < a.out_dim && t < a.rows) {
+        uint16_t o = spk::f2h(s.v[p * 4 + q]);
+        if (a.R) o = spk::f2h(spk::h2f(a.R[(long long)t * a.ldy + r]) + spk::h2f(o));
+        a.Y[(long long)t * a.ldy + r] = o;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// spk_chunk_prefill_ordered
+// ---------------------------------------------------------------------------
+constexpr int kC = 64, kD = 128, kThreads = 512;
+
+struct OrdArgs {
+  int H, T, total;  // total = T rounded up to 64
+  int l2, f16;
+  float q_scale;
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* g;
+  const float* beta;
+  const float* init;
+  float* core;
+  long long core_head_stride;
+  float* state;
+  float* ws;  // per head: qs, ks, vs [total][128]; solved, kcd, vnew, inter [64][128]
+};
+
+__device__ __forceinline__ float ld_in(const void* p, bool f16, long long i) {
+  return f16 ? spk::h2f(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ float* head_ws(const OrdArgs& a, int h) {
+  return a.ws + (size_t)h * ((size_t)3 * a.total * kD + 4 * kC * kD);
+}
+
+// Padded, optionally L2-normalised (deltanet_chunk.cpp:27-39, 78-85) and
+// q-scaled (:87-88) copies of q, k, v; one thread per (head, token).
+__global__ void ordered_prep_kernel(OrdArgs a) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.H * a.total) return;
+  const int h = i / a.total, t = i - (i / a.total) * a.total;
+  float* w = head_ws(a, h);
+  float* qs = w + (size_t)t * kD;
+  float* ks = w + (size_t)a.total * kD + (size_t)t * kD;
+  float* vs = w + (size_t)2 * a.total * kD + (size_t)t * kD;
+  if (t >= a.T) {
+    for (int d = 0; d < kD; ++d) qs[d] = ks[d] = vs[d] = 0.0f;
+    return;
+  }
+  const long long src = ((long long)h * a.T + t) * kD;
+  for (int d = 0; d < kD; ++d) {
+    qs[d] = ld_in(a.q, a.f16, src + d);
+    ks[d] = ld_in(a.k, a.f16, src + d);
+    vs[d] = ld_in(a.v, a.f16, src + d);
+  }
+  if (a.l2) {
+    float sq = 0.0f, sk = 0.0f;
+    for (int d = 0; d < kD; ++d) {
+      sq = sq + qs[d] * qs[d];
+      sk = sk + ks[d] * ks[d];
+    }
+    const float iq = 1.0f / __builtin_sqrtf(sq + 1e-6f), ik = 1.0f / __builtin_sqrtf(sk + 1e-6f);
+    for (int d = 0; d < kD; ++d) {
+      qs[d] = qs[d] * iq;
+      ks[d] = ks[d] * ik;
+    }
+  }
+  for (int d = 0; d < kD; ++d) qs[d] = qs[d] * a.q_scale;
+}
+
+// One workgroup per head; chunks in order; each phase of the reference's
+// chunk body split over independent outputs, every reduction sequential.
+__global__ __launch_bounds__(kThreads) void ordered_chunk_kernel(OrdArgs a) {
+  __shared__ float gcum[kC], bc[kC], eg[kC], wlast[kC], old_row[kC];
+  __shared__ float decay[kC][kC + 1], attn[kC][kC + 1], local[kC][kC + 1];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  float* w = head_ws(a, h);
+  const float* qs = w;
+  const float* ks = w + (size_t)a.total * kD;
+  const float* vs = w + (size_t)2 * a.total * kD;
+  float* solved = w + (size_t)3 * a.total * kD;
+  float* kcd = solved + kC * kD;
+  float* vnew = kcd + kC * kD;
+  float* inter = vnew + kC * kD;
+  float* S = a.state + (size_t)h * kD * kD;
+  for (int i = tid; i < kD * kD; i += kThreads) S[i] = a.init ? a.init[(size_t)h * kD * kD + i] : 0.0f;
+  const int nchunks = a.total / kC;
+  for (int ci = 0; ci < nchunks; ++ci) {
+    const int base = ci * kC;
+    const float* qc = qs + (size_t)base * kD;
+    const float* kc = ks + (size_t)base * kD;
+    const float* vc = vs + (size_t)base * kD;
+    __syncthreads();
+    if (tid == 0) {  // :137-151
+      float running = 0.0f;
+      for (int t = 0; t < kC; ++t) {
+        const int tok = base + t;
+        const float gt = tok < a.T ? a.g[(size_t)h * a.T + tok] : 0.0f;
+        gcum[t] = running + gt;
+        running = gcum[t];
+        bc[t] = tok < a.T ? a.beta[(size_t)h * a.T + tok] : 0.0f;
+      }
+    }
+    __syncthreads();
+    if (tid < kC) {
+      eg[tid] = spk::expf_det(gcum[tid]);
+      wlast[tid] = spk::expf_det(gcum[kC - 1] - gcum[tid]);
+    }
+    for (int i = tid; i < kC * kC; i += kThreads) {  // :153-159
+      const int r = i / kC, c = i % kC;
+      decay[r][c] = c <= r ? spk::expf_det(gcum[r] - gcum[c]) : 0.0f;
+    }
+    __syncthreads();
+    for (int i = tid; i < kC * kC; i += kThreads) {  // :161-170
+      const int r = i / kC, c = i % kC;
+      float val = 0.0f;
+      if (c < r) {
+        float dot = 0.0f;
+        for (int d = 0; d < kD; ++d) dot = dot + (kc[r * kD + d] * bc[r]) * kc[c * kD + d];
+        val = -dot * decay[r][c];
+      }
+      attn[r][c] = val;
+    }
+    __syncthreads();
+    for (int r = 1; r < kC; ++r) {  // :171-181 forward substitution, row by row
+      if (tid < r) old_row[tid] = attn[r][tid];
+      __syncthreads();
+      if (tid < r) {
+        const int c = tid;
+        float sum = old_row[c];
+        for (int in = 0; in < r; ++in) sum = sum + old_row[in] * attn[in][c];
+        attn[r][c] = sum;
+      }
+      __syncthreads();
+    }
+    if (tid < kC) attn[tid][tid] = attn[tid][tid] + 1.0f;  // :182-184
+    __syncthreads();
+    for (int i = tid; i < kC * kD; i += kThreads) {  // :186-202
+      const int r = i / kD, d = i % kD;
+      float sv = 0.0f, sk = 0.0f;
+      for (int c = 0; c < kC; ++c) {
+        const float coeff = attn[r][c];
+        if (coeff == 0.0f) continue;
+        const float bcol = bc[c];
+        sv = sv + coeff * (vc[c * kD + d] * bcol);
+        sk = sk + coeff * ((kc[c * kD + d] * bcol) * eg[c]);
+      }
+      solved[i] = sv;
+      kcd[i] = sk;
+    }
+    for (int i = tid; i < kC * kC; i += kThreads) {  // :204-213
+      const int r = i / kC, c = i % kC;
+      float val = 0.0f;
+      if (c <= r) {
+        float dot = 0.0f;
+        for (int d = 0; d < kD; ++d) dot = dot + qc[r * kD + d] * kc[c * kD + d];
+        val = dot * decay[r][c];
+      }
+      local[r][c] = val;
+    }
+    __syncthreads();
+    for (int i = tid; i < kC * kD; i += kThreads) {  // :215-233
+      const int r = i / kD, vd = i % kD;
+      const float egr = eg[r];
+      float carry = 0.0f, it = 0.0f;
+      for (int kd = 0; kd < kD; ++kd) {
+        const float s = S[kd * kD + vd];
+        carry = carry + kcd[r * kD + kd] * s;
+        it = it + (qc[r * kD + kd] * egr) * s;
+      }
+      vnew[i] = solved[i] - carry;
+      inter[i] = it;
+    }
+    __syncthreads();
+    for (int i = tid; i < kC * kD; i += kThreads) {  // :235-244
+      const int r = i / kD, vd = i % kD;
+      float sum = inter[i];
+      for (int c = 0; c <= r; ++c) sum = sum + local[r][c] * vnew[c * kD + vd];
+      if (base + r < a.T) a.core[((size_t)h * a.core_head_stride + base + r) * kD + vd] = sum;
+    }
+    const float eglast = eg[kC - 1];
+    for (int i = tid; i < kD * kD; i += kThreads) {  // :246-268
+      const int kd = i / kD, vd = i % kD;
+      const float ws = S[i] * eglast;
+      float upd = 0.0f;
+      for (int r = 0; r < kC; ++r) upd = upd + (kc[r * kD + kd] * wlast[r]) * vnew[r * kD + vd];
+      S[i] = ws + upd;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t ldx, uint16_t* Y, int64_t ldy,
+                                   const uint16_t* residual, int32_t rows, int32_t out_dim, int32_t in_dim,
+                                   spk_stream_t stream) {
+  if (!W || !X || !Y) return spk::fail(SPK_ERR_NULL, "spk_matvec_f16_rows: NULL pointer");
+  if (rows <= 0 || out_dim <= 0 || in_dim <= 0 || in_dim % 64 != 0 || in_dim / 64 > 64)
+    return spk::fail(SPK_ERR_SHAPE, "spk_matvec_f16_rows: rows %d out %d in %d (in a multiple of 64, <= 4096)", rows,
+                     out_dim, in_dim);
+  if (ldx < in_dim || ldy < out_dim) return spk::fail(SPK_ERR_SHAPE, "spk_matvec_f16_rows: leading dimensions");
+  if (residual == X || Y == X) return spk::fail(SPK_ERR_ARG, "spk_matvec_f16_rows: output aliases the input");
+  RowsArgs a{W, X, (long long)ldx, Y, (long long)ldy, residual, rows, out_dim, in_dim, in_dim / 64};
+  dim3 grid((out_dim + kTile - 1) / kTile, (rows + kTile - 1) / kTile);
+  hipLaunchKernelGGL(matvec_rows_kernel, grid, dim3(256), 0, spk::to_hip(stream), a);
+  return spk::check_launch("spk_matvec_f16_rows");
+}
+
+extern "C" size_t spk_chunk_prefill_ordered_workspace_size(int32_t num_heads, int32_t total_tokens) {
+  if (num_heads <= 0 || total_tokens <= 0) return 0;
+  const size_t total = ((size_t)total_tokens + kC - 1) / kC * kC;
+  return (size_t)num_heads * (3 * total * kD + 4 * kC * kD) * sizeof(float);
+}
+
+extern "C" int spk_chunk_prefill_ordered(const SpkChunkArgs* p, spk_stream_t stream) {
+  if (!p) return spk::fail(SPK_ERR_NULL, "spk_chunk_prefill_ordered: NULL args");
+  if (p->num_heads <= 0 || p->total_tokens <= 0 || p->key_dim <= 0 || p->value_dim <= 0 || p->chunk_size <= 0)
+    return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill_ordered: DeltaNet chunk config fields must be non-zero");
+  if (p->key_dim != kD || p->value_dim != kD || p->chunk_size != kC)
+    return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill_ordered: key_dim %d value_dim %d chunk %d (need 128/128/64)",
+                     p->key_dim, p->value_dim, p->chunk_size);
+  if (p->cu_seqlens || p->num_seqs > 1)
+    return spk::fail(SPK_ERR_ARG, "spk_chunk_prefill_ordered: one sequence per call");
+  if (!p->q || !p->k || !p->v || !p->g || !p->beta || !p->out_core || !p->out_state || !p->workspace)
+    return spk::fail(SPK_ERR_NULL, "spk_chunk_prefill_ordered: NULL pointer");
+  if (p->input_dtype != SPK_F32 && p->input_dtype != SPK_F16)
+    return spk::fail(SPK_ERR_ARG, "spk_chunk_prefill_ordered: input_dtype %d", p->input_dtype);
+  if (p->workspace_bytes < spk_chunk_prefill_ordered_workspace_size(p->num_heads, p->total_tokens))
+    return spk::fail(SPK_ERR_ARG, "spk_chunk_prefill_ordered: workspace %zu < %zu bytes", p->workspace_bytes,
+                     spk_chunk_prefill_ordered_workspace_size(p->num_heads, p->total_tokens));
+  const long long chs = p->core_head_stride ? p->core_head_stride : p->total_tokens;
+  if (chs < p->total_tokens) return spk::fail(SPK_ERR_SHAPE, "spk_chunk_prefill_ordered: core_head_stride");
+  if (p->initial_state == p->out_state && p->initial_state)
+    return spk::fail(SPK_ERR_ARG, "spk_chunk_prefill_ordered: initial_state must not alias out_state");
+  OrdArgs a;
+  a.H = p->num_heads;
+  a.T = p->total_tokens;
+  a.total = (p->total_tokens + kC - 1) / kC * kC;
+  a.l2 = p->use_qk_l2norm != 0;
+  a.f16 = p->input_dtype == SPK_F16;
+  a.q_scale = p->q_scale != 0.0f ? p->q_scale : 1.0f / sqrtf((float)p->key_dim);
+  a.q = p->q;
+  a.k = p->k;
+  a.v = p->v;
+  a.g = p->g;
+  a.beta = p->beta;
+  a.init = p->initial_state;
+  a.core = p->out_core;
+  a.core_head_stride = chs;
+  a.state = p->out_state;
+  a.ws = static_cast<float*>(p->workspace);
+  hipStream_t s = spk::to_hip(stream);
+  const int n = a.H * a.total;
+  hipLaunchKernelGGL(ordered_prep_kernel, dim3((n + 127) / 128), dim3(128), 0, s, a);
+  int rc = spk::check_launch("spk_chunk_prefill_ordered (prep)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(ordered_chunk_kernel, dim3(a.H), dim3(kThreads), 0, s, a);
+  return spk::check_launch("spk_chunk_prefill_ordered");
+}

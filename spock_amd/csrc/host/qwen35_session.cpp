@@ -91,8 +91,9 @@ std::vector<float> rope_table(std::uint32_t max_seq) {
   return t;
 }
 
-Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::uint32_t max_seq, bool use_graph)
-    : verbose_(verbose), use_graph_(use_graph), max_seq_(max_seq ? max_seq : MAX_SEQ) {
+Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::uint32_t max_seq, bool use_graph,
+                             bool ordered_prefill)
+    : verbose_(verbose), use_graph_(use_graph), ordered_prefill_(ordered_prefill), max_seq_(max_seq ? max_seq : MAX_SEQ) {
   if (max_seq_ > 65536) throw std::runtime_error("max_seq must be <= 65536");
   const auto t0 = std::chrono::steady_clock::now();
   WeightArtifact art = WeightArtifact::load(repack_dir);
@@ -220,7 +221,8 @@ void Qwen35Session::ensure_prefill_capacity(std::uint32_t T) {
   p_beta_ = DeviceBuffer(n * 16 * 4);
   p_core_ = DeviceBuffer(n * VAL * 4);
   p_state_ = DeviceBuffer(std::size_t(16) * 128 * 128 * 4);
-  p_chunk_ws_ = DeviceBuffer(spk_chunk_prefill_workspace_size(16, static_cast<int32_t>(T), 1, 64));
+  p_chunk_ws_ = DeviceBuffer(std::max(spk_chunk_prefill_workspace_size(16, static_cast<int32_t>(T), 1, 64),
+                                      spk_chunk_prefill_ordered_workspace_size(16, static_cast<int32_t>(T))));
   p_gated_ = DeviceBuffer(n * VAL * 2);
   p_qg_ = DeviceBuffer(n * 4096 * 2);
   p_k_ = DeviceBuffer(n * 512 * 2);
@@ -248,6 +250,19 @@ std::uint32_t Qwen35Session::prefill(const std::vector<std::uint32_t>& tokens) {
   hip_check(hipMemcpyAsync(p_tokens_.get(), ids.data(), T * 4, hipMemcpyHostToDevice, stream_), "upload prompt");
   auto* Hs = p_h_.get<std::uint16_t>();
   auto* XN = p_xn_.get<std::uint16_t>();
+  // Prompt projections: the matvec's own order (bit-identical to decode and to
+  // the CPU restatement) or the matrix cores.
+  auto proj = [&](const std::uint16_t* W, const std::uint16_t* X, std::int64_t ldx, std::uint16_t* Y, std::int64_t ldy,
+                  const std::uint16_t* R, std::uint32_t out_dim, std::uint32_t in_dim, const char* what) {
+    if (ordered_prefill_)
+      spk_check(spk_matvec_f16_rows(W, X, ldx, Y, ldy, R, Ti, static_cast<int32_t>(out_dim),
+                                    static_cast<int32_t>(in_dim), S(stream_)),
+                what);
+    else
+      spk_check(spk_gemm_f16(X, ldx, W, in_dim, Y, ldy, R, Ti, static_cast<int32_t>(out_dim),
+                             static_cast<int32_t>(in_dim), S(stream_)),
+                what);
+  };
   spk_check(spk_embedding_f16(embed_, p_tokens_.get<std::int32_t>(), Ti, static_cast<int32_t>(shape_.vocab), Hs, S(stream_)),
             "embedding");
   for (const LayerW& w : layers_) {
@@ -257,10 +272,10 @@ std::uint32_t Qwen35Session::prefill(const std::vector<std::uint32_t>& tokens) {
       auto* Z = p_z_.get<std::uint16_t>();
       auto* A = p_a_.get<std::uint16_t>();
       auto* B = p_b_.get<std::uint16_t>();
-      spk_check(spk_gemm_f16(XN, H, w.dn_qkv, H, QKV, CONV, nullptr, Ti, CONV, H, S(stream_)), "in_proj_qkv");
-      spk_check(spk_gemm_f16(XN, H, w.dn_z, H, Z, VAL, nullptr, Ti, VAL, H, S(stream_)), "in_proj_z");
-      spk_check(spk_gemm_f16(XN, H, w.dn_a, H, A, 16, nullptr, Ti, 16, H, S(stream_)), "in_proj_a");
-      spk_check(spk_gemm_f16(XN, H, w.dn_b, H, B, 16, nullptr, Ti, 16, H, S(stream_)), "in_proj_b");
+      proj(w.dn_qkv, XN, H, QKV, CONV, nullptr, CONV, H, "in_proj_qkv");
+      proj(w.dn_z, XN, H, Z, VAL, nullptr, VAL, H, "in_proj_z");
+      proj(w.dn_a, XN, H, A, 16, nullptr, 16, H, "in_proj_a");
+      proj(w.dn_b, XN, H, B, 16, nullptr, 16, H, "in_proj_b");
       spk_check(spk_deltanet_prefill_conv(QKV, CONV, conv_layer(w.sub), w.dn_conv, Ti, p_qhm_.get<std::uint16_t>(),
                                           p_khm_.get<std::uint16_t>(), p_vhm_.get<std::uint16_t>(), S(stream_)),
                 "prefill conv");
@@ -290,22 +305,21 @@ std::uint32_t Qwen35Session::prefill(const std::vector<std::uint32_t>& tokens) {
       c.num_seqs = 1;
       c.workspace = p_chunk_ws_.get();
       c.workspace_bytes = p_chunk_ws_.bytes();
-      spk_check(spk_chunk_prefill(&c, S(stream_)), "chunk prefill");
+      if (ordered_prefill_)
+        spk_check(spk_chunk_prefill_ordered(&c, S(stream_)), "chunk prefill (reference order)");
+      else
+        spk_check(spk_chunk_prefill(&c, S(stream_)), "chunk prefill");
       hip_check(hipMemcpyAsync(dn_state_layer(w.sub), p_state_.get(), std::size_t(16) * 128 * 128 * 4,
                                hipMemcpyDeviceToDevice, stream_),
                 "final state");
       spk_check(spk_deltanet_norm_gate(p_core_.get<float>(), Ti, Z, VAL, w.dn_norm, 1e-6f, Ti,
                                        p_gated_.get<std::uint16_t>(), VAL, S(stream_)),
                 "norm gate");
-      spk_check(spk_gemm_f16(p_gated_.get<std::uint16_t>(), VAL, w.dn_out, VAL, Hs, H, Hs, Ti, H, VAL, S(stream_)),
-                "out_proj");
+      proj(w.dn_out, p_gated_.get<std::uint16_t>(), VAL, Hs, H, Hs, H, VAL, "out_proj");
     } else {
-      spk_check(spk_gemm_f16(XN, H, w.attn_q, H, p_qg_.get<std::uint16_t>(), 4096, nullptr, Ti, 4096, H, S(stream_)),
-                "q_proj");
-      spk_check(spk_gemm_f16(XN, H, w.attn_k, H, p_k_.get<std::uint16_t>(), 512, nullptr, Ti, 512, H, S(stream_)),
-                "k_proj");
-      spk_check(spk_gemm_f16(XN, H, w.attn_v, H, p_v_.get<std::uint16_t>(), 512, nullptr, Ti, 512, H, S(stream_)),
-                "v_proj");
+      proj(w.attn_q, XN, H, p_qg_.get<std::uint16_t>(), 4096, nullptr, 4096, H, "q_proj");
+      proj(w.attn_k, XN, H, p_k_.get<std::uint16_t>(), 512, nullptr, 512, H, "k_proj");
+      proj(w.attn_v, XN, H, p_v_.get<std::uint16_t>(), 512, nullptr, 512, H, "v_proj");
       SpkAttnArgs aa{};
       aa.qg = p_qg_.get<std::uint16_t>();
       aa.k = p_k_.get<std::uint16_t>();
@@ -320,19 +334,15 @@ std::uint32_t Qwen35Session::prefill(const std::vector<std::uint32_t>& tokens) {
       aa.workspace = p_attn_ws_.get();
       aa.workspace_bytes = p_attn_ws_.bytes();
       spk_check(spk_attention_prefill(&aa, p0, Ti, S(stream_)), "attention prefill");
-      spk_check(spk_gemm_f16(p_gated_.get<std::uint16_t>(), 2048, w.attn_o, 2048, Hs, H, Hs, Ti, H, 2048, S(stream_)),
-                "o_proj");
+      proj(w.attn_o, p_gated_.get<std::uint16_t>(), 2048, Hs, H, Hs, H, 2048, "o_proj");
     }
     spk_check(spk_rmsnorm_f16(Hs, w.post_norm, XN, Ti, H, S(stream_)), "post norm");
-    spk_check(spk_gemm_f16(XN, H, w.mlp_gate, H, p_ga_.get<std::uint16_t>(), INTER, nullptr, Ti, INTER, H, S(stream_)),
-              "gate_proj");
-    spk_check(spk_gemm_f16(XN, H, w.mlp_up, H, p_up_.get<std::uint16_t>(), INTER, nullptr, Ti, INTER, H, S(stream_)),
-              "up_proj");
+    proj(w.mlp_gate, XN, H, p_ga_.get<std::uint16_t>(), INTER, nullptr, INTER, H, "gate_proj");
+    proj(w.mlp_up, XN, H, p_up_.get<std::uint16_t>(), INTER, nullptr, INTER, H, "up_proj");
     spk_check(spk_silu_gate_f16(p_ga_.get<std::uint16_t>(), p_up_.get<std::uint16_t>(), p_ga_.get<std::uint16_t>(),
                                 std::int64_t(T) * INTER, S(stream_)),
               "silu gate");
-    spk_check(spk_gemm_f16(p_ga_.get<std::uint16_t>(), INTER, w.mlp_down, INTER, Hs, H, Hs, Ti, H, INTER, S(stream_)),
-              "down_proj");
+    proj(w.mlp_down, p_ga_.get<std::uint16_t>(), INTER, Hs, H, Hs, H, INTER, "down_proj");
   }
   // Last token: final norm, lm_head + argmax, token bookkeeping on the device.
   const std::uint16_t* last = Hs + std::size_t(T - 1) * H;
@@ -603,13 +613,15 @@ int guarded(F&& f) {
 
 extern "C" const char* spk_model_last_error(void) { return g_model_error.c_str(); }
 
-extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int32_t use_graph) {
+extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int32_t flags) {
   SpkModel* m = nullptr;
   const int rc = guarded([&] {
     if (!repack_dir) throw std::runtime_error("spk_model_open: NULL directory");
+    if (flags & ~(SPK_MODEL_NO_GRAPH | SPK_MODEL_MATRIX_PREFILL)) throw std::runtime_error("spk_model_open: unknown flags");
     auto s = std::make_unique<spock::hip::Qwen35Session>(repack_dir, false,
                                                          max_seq > 0 ? static_cast<std::uint32_t>(max_seq) : 0u,
-                                                         use_graph != 0);
+                                                         (flags & SPK_MODEL_NO_GRAPH) == 0,
+                                                         (flags & SPK_MODEL_MATRIX_PREFILL) == 0);
     m = new SpkModel{std::move(s)};
   });
   return rc == 0 ? m : nullptr;

@@ -10,9 +10,11 @@
 // [layers][16][2], the RoPE table, and the decode activations.
 //
 // Prefill (HF semantics, modeling_qwen3_5.py:519-530): layer-major over the
-// prompt with MFMA projections (spk_gemm_f16), the DeltaNet conv/g/beta of the
-// decode shaders over every token, the chunk rule (spk_chunk_prefill) and the
-// gated norm; full-attention layers attend causally over the prompt.
+// prompt; projections either in the matvec's order (spk_matvec_f16_rows) or on
+// the matrix cores (spk_gemm_f16); the DeltaNet conv/g/beta of the decode
+// shaders over every token; the chunk rule in the reference's order
+// (spk_chunk_prefill_ordered) or on MFMA (spk_chunk_prefill); the gated norm;
+// full-attention layers attend causally over the prompt.
 // Decode: per token one fixed sequence of launches whose token id and
 // position live on the device (spk_gemv_fused with the embedding lookup and
 // input norms fused, spk_deltanet_decode_step, spk_attention_decode,
@@ -49,8 +51,11 @@ class Qwen35Session {
   static constexpr std::uint32_t MAX_SEQ = 2048;  // qwen35_config.hpp: max_sequence_length_v1
   static constexpr std::size_t kStateFloats = 16u * 128u * 128u + 32u;  // + g/beta tail
 
+  // ordered_prefill: prompt projections and chunk rule in the CPU
+  // restatement's operation order (bit-identical prefill, the reference's
+  // default CPU chunk path, vk_session.cpp:4840-4868); false: matrix cores.
   explicit Qwen35Session(const std::string& repack_dir, bool verbose = false, std::uint32_t max_seq = MAX_SEQ,
-                         bool use_graph = true);
+                         bool use_graph = true, bool ordered_prefill = true);
   ~Qwen35Session();
   Qwen35Session(const Qwen35Session&) = delete;
   Qwen35Session& operator=(const Qwen35Session&) = delete;
@@ -104,6 +109,7 @@ class Qwen35Session {
 
   bool verbose_ = false;
   bool use_graph_ = true;
+  bool ordered_prefill_ = true;
   Qwen35Shape shape_;
   std::uint32_t max_seq_ = MAX_SEQ;
   std::uint32_t n_dn_ = 0, n_attn_ = 0;

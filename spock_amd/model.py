@@ -20,6 +20,10 @@ _i32 = C.c_int32
 _sz = C.c_size_t
 
 
+SPK_MODEL_NO_GRAPH = 1
+SPK_MODEL_MATRIX_PREFILL = 2
+
+
 class SpkGenerateStats(C.Structure):
     _fields_ = [("prefill_ms", C.c_double), ("decode_ms", C.c_double), ("gpu_prefill_ms", C.c_double),
                 ("gpu_decode_ms", C.c_double), ("decode_steps", _i32), ("used_graph", _i32)]
@@ -89,10 +93,13 @@ class GenerateResult:
 
 class Session:
     """DecodeSession on one MI355X: construct from a repack directory, then
-    generate(prompt, max_new) (= decode()), reset(), prefill/decode steps."""
+    generate(prompt, max_new) (= decode()), reset(), prefill/decode steps.
+    matrix_prefill=True runs the prompt on the matrix cores; the default runs
+    it in the CPU restatement's order (bit-identical)."""
 
-    def __init__(self, repack_dir, max_seq: int = 2048, use_graph: bool = True):
-        self._h = lib().spk_model_open(str(repack_dir).encode(), max_seq, 1 if use_graph else 0)
+    def __init__(self, repack_dir, max_seq: int = 2048, use_graph: bool = True, matrix_prefill: bool = False):
+        flags = (0 if use_graph else SPK_MODEL_NO_GRAPH) | (SPK_MODEL_MATRIX_PREFILL if matrix_prefill else 0)
+        self._h = lib().spk_model_open(str(repack_dir).encode(), max_seq, flags)
         if not self._h:
             raise ModelError(f"spk_model_open: {lib().spk_model_last_error().decode(errors='replace')}")
         layers, vocab, ms = _i32(), _i32(), _i32()

@@ -373,3 +373,70 @@ def test_gemm_f16_against_fp64(dev, M, N, K, res):
     assert np.all(np.abs(got - (r + dot if res else dot)) <= tol), "outside the accumulation error bound"
     # and the typical element equals the correctly rounded value
     assert np.mean(got == want) > 0.95
+
+
+@pytest.mark.parametrize("rows,out_dim,in_dim,res", [(1, 6144, 1024, False), (70, 1000, 2048, True),
+                                                     (133, 16, 1024, False), (65, 1024, 3584, True)])
+def test_matvec_rows_bitexact(dev, rows, out_dim, in_dim, res):
+    """spk_matvec_f16_rows: each row bit-identical to the decode matvec order."""
+    from spock_amd import _lib
+    print(f"[matvec rows {rows}x{out_dim}x{in_dim}]", flush=True)
+    W = _rand16(90, out_dim * in_dim, 0.02).reshape(out_dim, in_dim)
+    X = _rand16(91, rows * in_dim).reshape(rows, in_dim)
+    R = _rand16(92, rows * out_dim).reshape(rows, out_dim)
+    dW, dX = _h(W, dev), _h(X, dev)
+    Y = _h(R, dev) if res else torch.empty(rows * out_dim, dtype=torch.float16, device=dev)
+    _lib.check(_lib.lib().spk_matvec_f16_rows(dW.data_ptr(), dX.data_ptr(), in_dim, Y.data_ptr(), out_dim,
+                                              Y.data_ptr() if res else None, rows, out_dim, in_dim, _stream()),
+               "spk_matvec_f16_rows")
+    torch.cuda.synchronize()
+    exp = np.zeros((rows, out_dim), np.uint16)
+    _om().orc_matmul_rows(_p(W), _p(X), _p(exp), out_dim, in_dim, rows)
+    if res:
+        e2 = np.zeros_like(exp)
+        _om().orc_residual_add(_p(R), _p(exp), _p(e2), exp.size)
+        exp = e2
+    assert np.array_equal(_u16(Y).reshape(rows, out_dim), exp)
+
+
+@pytest.mark.parametrize("T,f16,l2,init", [(104, False, False, False), (64, True, False, True),
+                                          (1, False, True, True), (200, True, False, True)])
+def test_chunk_prefill_ordered_bitexact(dev, oracle, T, f16, l2, init):
+    """spk_chunk_prefill_ordered: run_deltanet_chunk_rule's loops with the
+    deterministic exp, bit-identical to orc_chunk_rule_det."""
+    import ctypes as C_
+    from spock_amd import _lib, synth
+    print(f"[ordered chunk T={T} f16={f16} l2={l2} init={init}]", flush=True)
+    H = 16
+    inp = synth.chunk_inputs(H, T, seed=T, l2=not l2)
+    if f16:
+        for n in ("q", "k", "v"):
+            inp[n] = inp[n].astype(np.float16).astype(np.float32)
+    st0 = (np.random.default_rng(T).standard_normal((H, 128, 128)) * 0.05).astype(np.float32) if init else None
+    L = oracle.lib()
+    L.orc_chunk_rule_det.restype = C_.c_int
+    L.orc_chunk_rule_det.argtypes = [C_.c_size_t] * 5 + [C_.c_int] + [C_.c_void_p] * 8
+    ec = np.zeros((H, T, 128), np.float32)
+    es = np.zeros((H, 128, 128), np.float32)
+    rc = L.orc_chunk_rule_det(H, T, 128, 128, 64, 1 if l2 else 0, _p(inp["q"]), _p(inp["k"]), _p(inp["v"]),
+                              _p(inp["g"]), _p(inp["beta"]), None if st0 is None else _p(st0), _p(ec), _p(es))
+    assert rc == 0
+    cvt = (lambda a: _h(a.astype(np.float16).view(np.uint16), dev)) if f16 else (lambda a: _f(a, dev))
+    dq, dk, dv = cvt(inp["q"]), cvt(inp["k"]), cvt(inp["v"])
+    dg, db = _f(inp["g"], dev), _f(inp["beta"], dev)
+    dinit = _f(st0, dev) if init else None
+    core = torch.empty(H * T * 128, dtype=torch.float32, device=dev)
+    state = torch.empty(H * 128 * 128, dtype=torch.float32, device=dev)
+    wsb = int(_lib.lib().spk_chunk_prefill_ordered_workspace_size(H, T))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    a = _lib.SpkChunkArgs()
+    a.num_heads, a.total_tokens, a.key_dim, a.value_dim, a.chunk_size = H, T, 128, 128, 64
+    a.use_qk_l2norm, a.q_scale, a.input_dtype = 1 if l2 else 0, 0.0, _lib.SPK_F16 if f16 else _lib.SPK_F32
+    a.q, a.k, a.v, a.g, a.beta = dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), db.data_ptr()
+    a.initial_state = dinit.data_ptr() if init else None
+    a.out_core, a.out_state, a.num_seqs = core.data_ptr(), state.data_ptr(), 1
+    a.workspace, a.workspace_bytes = ws.data_ptr(), wsb
+    _lib.check(_lib.lib().spk_chunk_prefill_ordered(C.byref(a), _stream()), "spk_chunk_prefill_ordered")
+    torch.cuda.synchronize()
+    assert np.array_equal(core.cpu().numpy().view(np.uint32), ec.reshape(-1).view(np.uint32))
+    assert np.array_equal(state.cpu().numpy().view(np.uint32), es.reshape(-1).view(np.uint32))

@@ -5,7 +5,9 @@ against the oracle's full model (oracle/model.h) on seeded synthetic artifacts.
   decode step gives bit-identical greedy tokens, fp16 logits and hidden state
   (the per-token operation order is the oracle's), with and without the
   recorded HIP graph.
-* Prefill with MFMA projections and the MFMA chunk rule: close to the oracle
+* Default (ordered) prefill: bit-identical logits, hidden state, DeltaNet
+  state, conv state and KV cache; greedy generation token-for-token equal.
+* Matrix-core prefill (MFMA projections and chunk rule): close to the oracle
   (fp32 accumulation order differs), same greedy token.
 """
 import numpy as np
@@ -57,14 +59,35 @@ def test_decode_from_oracle_state_bitexact(dev, small_artifact, use_graph):
     assert np.array_equal(st["kv"], om.snapshot()["kv"])
 
 
-def test_prefill_close_to_oracle(dev, small_artifact):
+def test_ordered_prefill_and_generate_bitexact(dev, small_artifact):
     import oracle_model
     from spock_amd import model
-    print("[session prefill]", flush=True)
+    print("[session ordered prefill + generate]", flush=True)
     om = oracle_model.OracleModel(small_artifact, max_seq=MAX_SEQ)
     prompt = _prompt(133, seed=9)
     tok, logits, hidden = om.prefill(prompt, want_logits=True)
+    snap = om.snapshot()
     with model.Session(small_artifact, max_seq=MAX_SEQ) as s:
+        gtok = s.prefill(prompt)
+        glogits, ghidden = s.last_output()
+        st = s.get_state()
+        assert gtok == tok
+        assert np.array_equal(glogits, logits) and np.array_equal(ghidden, hidden)
+        assert np.array_equal(st["dn_state"].view(np.uint32), snap["dn_state"].view(np.uint32))
+        assert np.array_equal(st["conv"], snap["conv"]) and np.array_equal(st["kv"], snap["kv"])
+        r = s.generate(prompt, 24)
+    want = om.generate(prompt, 24)
+    assert r.tokens.tolist() == want.tolist()
+
+
+def test_matrix_prefill_close_to_oracle(dev, small_artifact):
+    import oracle_model
+    from spock_amd import model
+    print("[session matrix prefill]", flush=True)
+    om = oracle_model.OracleModel(small_artifact, max_seq=MAX_SEQ)
+    prompt = _prompt(133, seed=9)
+    tok, logits, hidden = om.prefill(prompt, want_logits=True)
+    with model.Session(small_artifact, max_seq=MAX_SEQ, matrix_prefill=True) as s:
         gtok = s.prefill(prompt)
         glogits, ghidden = s.last_output()
         st = s.get_state()
