@@ -250,6 +250,66 @@ def bench_lm_head(steps, warmup):
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+MODEL_SEED, MODEL_PROMPT, MODEL_NEW = 2026, 512, 128
+
+
+def model_decode_bytes(layers=24, vocab=VOCAB, pos=MODEL_PROMPT + MODEL_NEW // 2):
+    """HBM bytes one batch-1 decode step must move: every weight once (the tied
+    embedding is the lm_head), DeltaNet state read + write, conv state read +
+    write, and the KV rows of the attention layers up to `pos`."""
+    n_attn = layers // 4
+    n_dn = layers - n_attn
+    per_dn = (6144 + 2048 + 16 + 16) * 1024 + 6144 * 4 + 16 + 1024 * 2048 + 16 * 4 + 128 * 4
+    per_attn = (4096 + 512 + 512) * 1024 + 1024 * 2048 + 2 * 256
+    per_layer = 2 * 1024 + 3 * 3584 * 1024  # norms, MLP
+    weights = 2 * (vocab * 1024 + 1024 + layers * per_layer + n_attn * per_attn
+                   + n_dn * (per_dn - 16 * 4 - 128 * 4)) + n_dn * (16 * 4 + 128 * 4)
+    state = n_dn * (2 * 16 * 128 * 128 * 4 + 2 * 6144 * 4 * 2)
+    kv = n_attn * pos * 1024 * 2
+    return weights + state + kv
+
+
+def bench_model(steps, warmup):
+    """Config 4: the full Qwen3.5-0.8B-shaped random-init model, 512-token
+    prompt, 128 greedy tokens at batch 1; decode is HBM-bound."""
+    import tempfile
+    from spock_amd import model, synth
+    work = Path(tempfile.mkdtemp(prefix="spock-config4-"))
+    art = model.write_synthetic_artifact(work / "artifact", layers=24, vocab=VOCAB, seed=MODEL_SEED)
+    prompt = (synth.splitmix64(4, MODEL_PROMPT) % np.uint64(VOCAB)).astype(np.int32)
+    golden = None
+    gp = ROOT / "tests" / "golden" / "config4_tokens.json"
+    if gp.exists():
+        golden = json.loads(gp.read_text())["tokens"]
+    res = {"workload": "config4: 24 layers (18 gated DeltaNet + 6 gated attention), hidden 1024, vocab 248320, "
+                       "fp16 weights N(0,0.02) seed 2026, prompt 512, 128 greedy tokens, batch 1"}
+    for mode, matrix in (("ordered_prefill", False), ("matrix_prefill", True)):
+        with model.Session(art, matrix_prefill=matrix) as s:
+            s.generate(prompt[:64], 4)  # warm-up: kernels loaded, graph recorded
+            runs = [s.generate(prompt, MODEL_NEW) for _ in range(max(1, min(3, steps)))]
+        best = min(runs, key=lambda r: r.gpu_decode_ms)
+        dec_s = best.gpu_decode_ms / 1e3
+        r = {"prefill_ms_gpu": round(min(x.gpu_prefill_ms for x in runs), 3),
+             "prefill_tok_per_s": round(MODEL_PROMPT / (min(x.gpu_prefill_ms for x in runs) / 1e3), 1),
+             "decode_ms_gpu": round(best.gpu_decode_ms, 3), "decode_steps": best.decode_steps,
+             "decode_tok_per_s": round(best.decode_steps / dec_s, 1),
+             "decode_us_per_token": round(dec_s / best.decode_steps * 1e6, 2),
+             "decode_wall_ms": round(best.decode_ms, 3), "graph": best.used_graph}
+        if golden is not None:
+            r["tokens_equal_cpu_oracle"] = best.tokens.tolist() == golden
+            mism = [i for i, (a, b) in enumerate(zip(best.tokens.tolist(), golden)) if a != b]
+            r["first_token_mismatch"] = mism[0] if mism else None
+        res[mode] = r
+    nbytes = model_decode_bytes()
+    per_tok = res["ordered_prefill"]["decode_us_per_token"] / 1e6
+    res["decode_bytes_per_token"] = nbytes
+    res["decode_achieved_gbs"] = round(nbytes / per_tok / 1e9, 1)
+    res["decode_frac_hbm"] = round(nbytes / per_tok / 1e9 / HBM_PEAK_GBS, 4)
+    import shutil
+    shutil.rmtree(work, ignore_errors=True)
+    return res
+
+
 def bench_copy(steps, warmup):
     """A plain device-to-device copy of 512 MiB: the calibration workload for
     the FETCH_SIZE / WRITE_SIZE counters (known bytes read and written)."""
@@ -295,7 +355,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy"],
+    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy", "model"],
                     help="run one workload and print its own JSON (for profiler runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -311,7 +371,7 @@ def main():
     log(f"[bench] device {torch.cuda.get_device_name(0)}")
     if args.only:
         fns = {"prefill": bench_prefill, "config0": bench_config0, "gemv": bench_gemv_chain,
-               "lm_head": bench_lm_head, "copy": bench_copy,
+               "lm_head": bench_lm_head, "copy": bench_copy, "model": bench_model,
                "decode": lambda s, w: [bench_decode(B, s, w) for B in (1, 16, 64, 256)]}
         r = fns[args.only](args.steps, args.warmup)
         print(json.dumps({"only": args.only, "result": r}, default=float), flush=True)
@@ -334,6 +394,8 @@ def main():
         log(f"[bench] gemv chain {secondary['gemv_chain']}")
         secondary["lm_head_argmax"] = bench_lm_head(args.steps, args.warmup)
         log(f"[bench] lm_head {secondary['lm_head_argmax']}")
+        secondary["config4_full_model"] = bench_model(args.steps, args.warmup)
+        log(f"[bench] full model {secondary['config4_full_model']}")
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log(f"[bench] cpu baseline {cpu}")

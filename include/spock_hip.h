@@ -225,12 +225,16 @@ typedef struct SpkGemvInput {
 
 /* y = fp16(W . x), or fp16(residual + fp16(W . x)) (residual_add.comp after
  * the projection) when residual != NULL; y may equal residual (in-place update
- * of the stream) but must not alias the input vectors. */
+ * of the stream) but must not alias the input vectors.  With W_up != NULL the
+ * output is the SiLU-gated pair of the MLP (gate/up matvecs then
+ * silu_gate.comp): y = fp16(silu(fp16(W . x)) * fp16(W_up . x)); a launch
+ * holds either only pairs or only single projections. */
 typedef struct SpkGemvOutput {
   const uint16_t* W;         /* [out_dim][in_dim] fp16, 16-byte aligned */
   uint16_t* y;
   const uint16_t* residual;
   int32_t out_dim;
+  const uint16_t* W_up;      /* nullable, [out_dim][in_dim] */
 } SpkGemvOutput;
 
 /* Up to 8 projections of one input in one launch.  Replaces the

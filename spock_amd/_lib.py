@@ -90,7 +90,7 @@ class SpkGemvInput(C.Structure):
 
 
 class SpkGemvOutput(C.Structure):
-    _fields_ = [("W", _p), ("y", _p), ("residual", _p), ("out_dim", _i32)]
+    _fields_ = [("W", _p), ("y", _p), ("residual", _p), ("out_dim", _i32), ("W_up", _p)]
 
 
 class SpkAttnArgs(C.Structure):

@@ -383,10 +383,11 @@ void Qwen35Session::enqueue_decode_step() {
     in.token_rows = static_cast<int32_t>(shape_.vocab);
     in.h_out = L == 0 ? h : nullptr;
     if (!w.attn) {
-      const SpkGemvOutput outs[4] = {{w.dn_qkv, qkv_.get<std::uint16_t>(), nullptr, static_cast<int32_t>(CONV)},
-                                     {w.dn_z, z_.get<std::uint16_t>(), nullptr, static_cast<int32_t>(VAL)},
-                                     {w.dn_a, a_.get<std::uint16_t>(), nullptr, 16},
-                                     {w.dn_b, b_.get<std::uint16_t>(), nullptr, 16}};
+      const SpkGemvOutput outs[4] = {
+          {w.dn_qkv, qkv_.get<std::uint16_t>(), nullptr, static_cast<int32_t>(CONV), nullptr},
+          {w.dn_z, z_.get<std::uint16_t>(), nullptr, static_cast<int32_t>(VAL), nullptr},
+          {w.dn_a, a_.get<std::uint16_t>(), nullptr, 16, nullptr},
+          {w.dn_b, b_.get<std::uint16_t>(), nullptr, 16, nullptr}};
       spk_check(spk_gemv_fused(&in, outs, 4, S(stream_)), "deltanet projections");
       SpkDecodeArgs d{};
       d.batch = 1;
@@ -411,12 +412,12 @@ void Qwen35Session::enqueue_decode_step() {
       oi.kind = SPK_GEMV_IN_PLAIN;
       oi.in_dim = VAL;
       oi.x = qkv_.get<std::uint16_t>() + 4096;
-      const SpkGemvOutput oo{w.dn_out, h, h, static_cast<int32_t>(H)};
+      const SpkGemvOutput oo{w.dn_out, h, h, static_cast<int32_t>(H), nullptr};
       spk_check(spk_gemv_fused(&oi, &oo, 1, S(stream_)), "out_proj");
     } else {
-      const SpkGemvOutput outs[3] = {{w.attn_q, qg_.get<std::uint16_t>(), nullptr, 4096},
-                                     {w.attn_k, k_.get<std::uint16_t>(), nullptr, 512},
-                                     {w.attn_v, v_.get<std::uint16_t>(), nullptr, 512}};
+      const SpkGemvOutput outs[3] = {{w.attn_q, qg_.get<std::uint16_t>(), nullptr, 4096, nullptr},
+                                     {w.attn_k, k_.get<std::uint16_t>(), nullptr, 512, nullptr},
+                                     {w.attn_v, v_.get<std::uint16_t>(), nullptr, 512, nullptr}};
       spk_check(spk_gemv_fused(&in, outs, 3, S(stream_)), "attention projections");
       SpkAttnArgs aa{};
       aa.qg = qg_.get<std::uint16_t>();
@@ -436,7 +437,7 @@ void Qwen35Session::enqueue_decode_step() {
       oi.kind = SPK_GEMV_IN_PLAIN;
       oi.in_dim = 2048;
       oi.x = attn_out_.get<std::uint16_t>();
-      const SpkGemvOutput oo{w.attn_o, h, h, static_cast<int32_t>(H)};
+      const SpkGemvOutput oo{w.attn_o, h, h, static_cast<int32_t>(H), nullptr};
       spk_check(spk_gemv_fused(&oi, &oo, 1, S(stream_)), "o_proj");
     }
     SpkGemvInput mi{};
@@ -444,15 +445,14 @@ void Qwen35Session::enqueue_decode_step() {
     mi.in_dim = H;
     mi.x = h;
     mi.x2 = w.post_norm;
-    const SpkGemvOutput mo[2] = {{w.mlp_gate, gate_.get<std::uint16_t>(), nullptr, static_cast<int32_t>(INTER)},
-                                 {w.mlp_up, up_.get<std::uint16_t>(), nullptr, static_cast<int32_t>(INTER)}};
-    spk_check(spk_gemv_fused(&mi, mo, 2, S(stream_)), "gate/up");
+    // gate/up matvecs with silu_gate.comp fused: m = fp16(silu(gate) * up)
+    const SpkGemvOutput mo{w.mlp_gate, gate_.get<std::uint16_t>(), nullptr, static_cast<int32_t>(INTER), w.mlp_up};
+    spk_check(spk_gemv_fused(&mi, &mo, 1, S(stream_)), "gate/up");
     SpkGemvInput di{};
-    di.kind = SPK_GEMV_IN_SILU_GATE;
+    di.kind = SPK_GEMV_IN_PLAIN;
     di.in_dim = INTER;
     di.x = gate_.get<std::uint16_t>();
-    di.x2 = up_.get<std::uint16_t>();
-    const SpkGemvOutput dout{w.mlp_down, h, h, static_cast<int32_t>(H)};
+    const SpkGemvOutput dout{w.mlp_down, h, h, static_cast<int32_t>(H), nullptr};
     spk_check(spk_gemv_fused(&di, &dout, 1, S(stream_)), "down_proj");
   }
   spk_check(spk_rmsnorm_f16(h, final_norm_, hn_.get<std::uint16_t>(), 1, H, S(stream_)), "final norm");

@@ -71,6 +71,9 @@ __device__ __forceinline__ float block_tree256(float p, float* red) {
 //   RMSNORM    fp16(RMSNorm(h) * (1 + w)),  h = x (or row token[0] of x)
 //   SILU_GATE  fp16(silu(gate) * up)
 // computed once per workgroup into LDS (fp16-rounded values as floats).
+// An output with a second matrix (W2) is the SiLU-gated pair of
+// silu_gate.comp: y = fp16(silu(fp16(W . x)) * fp16(W2 . x)), both rows of a
+// pair computed by the same wave.
 // ---------------------------------------------------------------------------
 constexpr int kMaxOut = 8;
 constexpr int kMaxIn = 4096;
@@ -85,6 +88,7 @@ struct FusedGemv {
   uint16_t* h_out;
   int count;
   const uint16_t* W[kMaxOut];
+  const uint16_t* W2[kMaxOut];
   uint16_t* y[kMaxOut];
   const uint16_t* res[kMaxOut];
   int out_dim[kMaxOut];
@@ -92,6 +96,31 @@ struct FusedGemv {
 };
 
 template <int N8, int R>
+__device__ __forceinline__ void load_rows(const uint16_t* __restrict__ W, int row0, int out_dim, int lane,
+                                          uint4 (&wv)[R][N8]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r < out_dim ? row0 + r : out_dim - 1;
+    const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * (512 * N8) + lane * (8 * N8));
+#pragma unroll
+    for (int k = 0; k < N8; ++k) wv[r][k] = ld_stream(src + k);
+  }
+}
+
+template <int N8>
+__device__ __forceinline__ float row_dot(const uint4 (&wr)[N8], const float* xf) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < N8; ++k) {
+    float wf[8];
+    unpack8(wr[k], wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
+  }
+  return spk::tree64_to_lane0(acc);
+}
+
+template <int N8, int R, bool PAIR>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   __shared__ float xs[kMaxIn];
   __shared__ float red[257];
@@ -107,16 +136,9 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   const int row0 = (((int)blockIdx.x - a.first_block[d]) * 4 + wave) * R;
   // Weight rows first: they do not depend on x, so their latency overlaps the prologue.
   uint4 wv[R][N8];
-  {
-    const uint16_t* __restrict__ W = a.W[d];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = row0 + r < out_dim ? row0 + r : out_dim - 1;
-      const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
-#pragma unroll
-      for (int k = 0; k < N8; ++k) wv[r][k] = ld_stream(src + k);
-    }
-  }
+  uint4 wv2[PAIR ? R : 1][N8];
+  load_rows<N8, R>(a.W[d], row0, out_dim, lane, wv);
+  if (PAIR) load_rows<N8, PAIR ? R : 1>(a.W2[d], row0, out_dim, lane, wv2);
   if (a.kind == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
     const uint16_t* h = a.x;
     if (a.token) {  // ids outside [0, token_rows) select row 0 instead of reading out of bounds
@@ -124,11 +146,11 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
       h += (size_t)((id >= 0 && id < a.token_rows) ? id : 0) * kHidden;
     }
     const uint2 hv = *reinterpret_cast<const uint2*>(h + 4 * tid);
-    const uint2 wv2 = *reinterpret_cast<const uint2*>(a.x2 + 4 * tid);
+    const uint2 wv2n = *reinterpret_cast<const uint2*>(a.x2 + 4 * tid);
     const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
                         spk::h2f(hv.y >> 16)};
-    const float w[4] = {spk::h2f(wv2.x & 0xffffu), spk::h2f(wv2.x >> 16), spk::h2f(wv2.y & 0xffffu),
-                        spk::h2f(wv2.y >> 16)};
+    const float w[4] = {spk::h2f(wv2n.x & 0xffffu), spk::h2f(wv2n.x >> 16), spk::h2f(wv2n.y & 0xffffu),
+                        spk::h2f(wv2n.y >> 16)};
     float p = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) p = __builtin_fmaf(v[i], v[i], p);
@@ -137,13 +159,36 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) xs[4 * tid + i] = round16((v[i] * nf) * (1.0f + w[i]));
     if (a.h_out && blockIdx.x == 0) *reinterpret_cast<uint2*>(a.h_out + 4 * tid) = hv;
-  } else if (a.kind == SPK_GEMV_IN_SILU_GATE) {
-    for (int i = tid; i < in_dim; i += 256) {
-      const float g = spk::h2f(a.x[i]);
-      xs[i] = round16(spk::silu_det(g) * spk::h2f(a.x2[i]));
-    }
   } else {
-    for (int i = tid; i < in_dim; i += 256) xs[i] = spk::h2f(a.x[i]);
+    // 16-byte pieces, all loads issued before any use
+    constexpr int NV = in_dim / 8;
+    constexpr int PER = (NV + 255) / 256;
+    uint4 xv[PER], uv[PER];
+    const bool silu = a.kind == SPK_GEMV_IN_SILU_GATE;
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = tid + 256 * c;
+      if (idx < NV) {
+        xv[c] = *reinterpret_cast<const uint4*>(a.x + 8 * idx);
+        if (silu) uv[c] = *reinterpret_cast<const uint4*>(a.x2 + 8 * idx);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = tid + 256 * c;
+      if (idx < NV) {
+        float f[8];
+        unpack8(xv[c], f);
+        if (silu) {
+          float u[8];
+          unpack8(uv[c], u);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = round16(spk::silu_det(f[e]) * u[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xs[8 * idx + e] = f[e];
+      }
+    }
   }
   __syncthreads();
   float xf[8 * N8];
@@ -159,18 +204,13 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   const uint16_t* __restrict__ res = a.res[d];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < N8; ++k) {
-      float wf[8];
-      unpack8(wv[r][k], wf);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
-    }
-    acc = spk::tree64_to_lane0(acc);
+    const float acc = row_dot<N8>(wv[r], xf);
+    float acc2 = 0.0f;
+    if (PAIR) acc2 = row_dot<N8>(wv2[PAIR ? r : 0], xf);
     const int row = row0 + r;
     if (lane == 0 && row < out_dim) {
       uint16_t o = spk::f2h(acc);
+      if (PAIR) o = spk::f2h(spk::silu_det(spk::h2f(o)) * spk::h2f(spk::f2h(acc2)));
       if (res) o = spk::f2h(spk::h2f(res[row]) + spk::h2f(o));
       y[row] = o;
     }
@@ -261,23 +301,17 @@ struct AttnArgs {
 };
 
 // One query-head wave over one block of positions [64b, 64b+64) of npos valid
-// ones: writes m_b, S_b, O_b.  q (fp16-rounded floats) is in qs[256] (LDS);
-// cur_k/cur_v (LDS, fp16 bits) stand in for the cache row of position `cur`.
-__device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t* kv, int kvh, int b, int npos,
-                                                int cur, const uint16_t* cur_k, const uint16_t* cur_v, int lane,
+// ones, operands staged in LDS (K transposed, Kt[d][p]; V as Vs[p][d]; q as
+// fp16-rounded floats): writes m_b, S_b, O_b.
+__device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t (*Kt)[kAttnBlock],
+                                                const uint16_t (*Vs)[kHeadDim], int b, int npos, int lane,
                                                 float* part) {
   const int p = kAttnBlock * b + lane;
   float sc = -INFINITY;
   if (p < npos) {
-    const uint16_t* kp = (p == cur) ? cur_k : kv + (size_t)p * kKvRow + kvh * kHeadDim;
     float dot = 0.0f;
-    for (int d8 = 0; d8 < kHeadDim; d8 += 8) {
-      const uint4 u = *reinterpret_cast<const uint4*>(kp + d8);
-      float kf[8];
-      unpack8(u, kf);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(qs[d8 + e], kf[e], dot);
-    }
+#pragma unroll 8
+    for (int d = 0; d < kHeadDim; ++d) dot = __builtin_fmaf(qs[d], spk::h2f(Kt[d][lane]), dot);
     sc = dot * 0.0625f;
   }
   float m = sc;
@@ -288,11 +322,9 @@ __device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t*
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int nvalid = min(kAttnBlock, npos - kAttnBlock * b);
   for (int j = 0; j < nvalid; ++j) {
-    const int pj = kAttnBlock * b + j;
     const float wj = __shfl(w, j, 64);
-    const uint16_t* vp = (pj == cur) ? cur_v : kv + (size_t)pj * kKvRow + 512 + kvh * kHeadDim;
     float vf[4];
-    load4h(vp + 4 * lane, vf);
+    load4h(&Vs[j][4 * lane], vf);
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(wj, vf[i], acc[i]);
   }
@@ -306,16 +338,47 @@ __device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t*
 // grid (max_blocks, kv_heads, T); block 256.
 __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
   __shared__ float qs[4][kHeadDim];
-  __shared__ __align__(16) uint16_t cur_k[kHeadDim];
-  __shared__ __align__(16) uint16_t cur_v[kHeadDim];
+  __shared__ __align__(16) uint16_t Kt[kHeadDim][kAttnBlock];
+  __shared__ __align__(16) uint16_t Vs[kAttnBlock][kHeadDim];
   const int b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = a.pos_dev ? a.pos_dev[0] : a.pos0 + t;
   if (pos < 0 || pos >= a.max_seq) return;
   const int npos = pos + 1;
   if (kAttnBlock * b >= npos) return;
   const float* cs = a.rope + (size_t)pos * 64;
-  const bool has_cur = a.store_kv && (pos / kAttnBlock) == b;
+  const int cur = (a.store_kv && (pos / kAttnBlock) == b) ? pos - kAttnBlock * b : -1;
+  // Stage the block's K (transposed) and V rows: thread (p = tid/4, quarter tid%4)
+  // moves 64 dims of K and of V of position 64b + p; all loads first.
+  {
+    const int p = tid >> 2, q4 = tid & 3;
+    const int gp = kAttnBlock * b + p;
+    uint4 kv4[8], vv4[8];
+    const bool live = gp < npos && p != cur;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (live) {
+        const uint16_t* row = a.kv + (size_t)gp * kKvRow + kvh * kHeadDim + q4 * 64;
+        kv4[i] = *reinterpret_cast<const uint4*>(row + 8 * i);
+        vv4[i] = *reinterpret_cast<const uint4*>(row + 512 + 8 * i);
+      } else {
+        kv4[i] = make_uint4(0, 0, 0, 0);
+        vv4[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    if (p != cur) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t w4[4] = {kv4[i].x, kv4[i].y, kv4[i].z, kv4[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          Kt[q4 * 64 + 8 * i + 2 * e][p] = (uint16_t)(w4[e] & 0xffffu);
+          Kt[q4 * 64 + 8 * i + 2 * e + 1][p] = (uint16_t)(w4[e] >> 16);
+        }
+        *reinterpret_cast<uint4*>(&Vs[p][q4 * 64 + 8 * i]) = vv4[i];
+      }
+    }
+  }
   const int qh = kvh * 4 + wave;
   {
     float v[4];
@@ -325,22 +388,25 @@ __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = v[i];
   }
-  if (has_cur && wave == 0) {  // new K row: norm + rope; V row as projected
+  if (cur >= 0 && wave == 0) {  // new K row: norm + rope; V row as projected
     float v[4];
     load4h(a.k + (size_t)t * 512 + kvh * kHeadDim + 4 * lane, v);
     head_norm_wave(v, a.k_norm_w, lane);
     rope_wave(v, cs, lane);
     const uint2 kb = pack4h(v);
     const uint2 vb = *reinterpret_cast<const uint2*>(a.v + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
-    *reinterpret_cast<uint2*>(cur_k + 4 * lane) = kb;
-    *reinterpret_cast<uint2*>(cur_v + 4 * lane) = vb;
+    const uint16_t k16[4] = {(uint16_t)(kb.x & 0xffffu), (uint16_t)(kb.x >> 16), (uint16_t)(kb.y & 0xffffu),
+                             (uint16_t)(kb.y >> 16)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Kt[4 * lane + i][cur] = k16[i];
+    *reinterpret_cast<uint2*>(&Vs[cur][4 * lane]) = vb;
     uint16_t* row = a.kv + (size_t)pos * kKvRow;  // kv_cache_store.comp:27-48
     *reinterpret_cast<uint2*>(row + kvh * kHeadDim + 4 * lane) = kb;
     *reinterpret_cast<uint2*>(row + 512 + kvh * kHeadDim + 4 * lane) = vb;
   }
   __syncthreads();
   float* part = a.part + (((size_t)t * kQHeads + qh) * a.max_blocks + b) * kPartFloats;
-  attn_block_wave(qs[wave], a.kv, kvh, b, npos, has_cur ? pos : -1, cur_k, cur_v, lane, part);
+  attn_block_wave(qs[wave], Kt, Vs, b, npos, lane, part);
 }
 
 // Prefill: K/V rows of positions pos0..pos0+T-1, before any block pass reads
@@ -359,21 +425,49 @@ __global__ __launch_bounds__(64) void attn_store_kv_kernel(AttnArgs a) {
       *reinterpret_cast<const uint2*>(a.v + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
 }
 
-// grid (8 query heads, T); block 256 (thread = output dim).
+// grid (8 query heads, T); block 256 (thread = output dim).  Blocks are
+// combined in order; their partials are loaded 8 at a time so the loads are
+// in flight together.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  __shared__ float cfac[1024], sfac[1024];
+  __shared__ float red[257];
   const int qh = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
   const int pos = a.pos_dev ? a.pos_dev[0] : a.pos0 + t;
   if (pos < 0 || pos >= a.max_seq) return;
-  const int nb = (pos + kAttnBlock) / kAttnBlock;
+  const int nb = (pos + kAttnBlock) / kAttnBlock;  // <= max_blocks <= 1024
   const float* part = a.part + ((size_t)t * kQHeads + qh) * a.max_blocks * kPartFloats;
   float M = -INFINITY;
-  for (int b = 0; b < nb; ++b) M = fmaxf(M, part[(size_t)b * kPartFloats]);
+  for (int b = d; b < nb; b += 256) {
+    const float m = part[(size_t)b * kPartFloats];
+    cfac[b] = m;
+    sfac[b] = part[(size_t)b * kPartFloats + 1];
+    M = fmaxf(M, m);
+  }
+  red[d] = M;
+  __syncthreads();
+  if (d < 64) {
+    float m = fmaxf(fmaxf(red[d], red[d + 64]), fmaxf(red[d + 128], red[d + 192]));
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh, 64));
+    if (d == 0) red[256] = m;
+  }
+  __syncthreads();
+  M = red[256];
+  for (int b = d; b < nb; b += 256) cfac[b] = spk::expf_det(cfac[b] - M);
+  __syncthreads();
   float tot = 0.0f, o = 0.0f;
-  for (int b = 0; b < nb; ++b) {
-    const float* pb = part + (size_t)b * kPartFloats;
-    const float c = spk::expf_det(pb[0] - M);
-    tot = tot + pb[1] * c;
-    o = o + pb[2 + d] * c;
+  for (int b0 = 0; b0 < nb; b0 += 8) {
+    float ov[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ov[i] = b0 + i < nb ? part[(size_t)(b0 + i) * kPartFloats + 2 + d] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (b0 + i < nb) {
+        const float c = cfac[b0 + i];
+        tot = tot + sfac[b0 + i] * c;
+        o = o + ov[i] * c;
+      }
+    }
   }
   const float att = round16(o * (1.0f / (tot + 1e-30f)));
   const float g = spk::h2f(a.qg[(size_t)t * 4096 + qh * 512 + 256 + d]);
@@ -506,7 +600,12 @@ extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs,
     // y may be the residual (in-place update of the stream) but never an input of this launch.
     if (o.y == in->x || o.y == in->x2)
       return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: output %d aliases the input vector", i);
+    if ((o.W_up != nullptr) != (outs[0].W_up != nullptr))
+      return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: SiLU-gated pairs and plain outputs in one launch");
+    if (o.W_up && !spk::aligned(o.W_up, 16))
+      return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: W_up %d must be 16-byte aligned", i);
     a.W[i] = o.W;
+    a.W2[i] = o.W_up;
     a.y[i] = o.y;
     a.res[i] = o.residual;
     a.out_dim[i] = o.out_dim;
@@ -514,21 +613,31 @@ extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs,
     blocks += (o.out_dim + 4 * R - 1) / (4 * R);
   }
   for (int i = count; i < kMaxOut; ++i) {
-    a.W[i] = nullptr; a.y[i] = nullptr; a.res[i] = nullptr; a.out_dim[i] = 0; a.first_block[i] = blocks;
+    a.W[i] = nullptr; a.W2[i] = nullptr; a.y[i] = nullptr; a.res[i] = nullptr; a.out_dim[i] = 0;
+    a.first_block[i] = blocks;
   }
   a.first_block[kMaxOut] = blocks;
   hipStream_t s = spk::to_hip(stream);
+  const bool pair = outs[0].W_up != nullptr;
+#define SPK_FG(n8, r)                                                                                   \
+  case n8:                                                                                              \
+    if (pair)                                                                                           \
+      hipLaunchKernelGGL((fused_gemv_kernel<n8, r, true>), dim3(blocks), dim3(256), 0, s, a);           \
+    else                                                                                                \
+      hipLaunchKernelGGL((fused_gemv_kernel<n8, r, false>), dim3(blocks), dim3(256), 0, s, a);          \
+    break;
   switch (n8) {
-    case 1: hipLaunchKernelGGL((fused_gemv_kernel<1, 2>), dim3(blocks), dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((fused_gemv_kernel<2, 2>), dim3(blocks), dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((fused_gemv_kernel<3, 1>), dim3(blocks), dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((fused_gemv_kernel<4, 1>), dim3(blocks), dim3(256), 0, s, a); break;
-    case 5: hipLaunchKernelGGL((fused_gemv_kernel<5, 1>), dim3(blocks), dim3(256), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((fused_gemv_kernel<6, 1>), dim3(blocks), dim3(256), 0, s, a); break;
-    case 7: hipLaunchKernelGGL((fused_gemv_kernel<7, 1>), dim3(blocks), dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((fused_gemv_kernel<8, 1>), dim3(blocks), dim3(256), 0, s, a); break;
+    SPK_FG(1, 2)
+    SPK_FG(2, 2)
+    SPK_FG(3, 1)
+    SPK_FG(4, 1)
+    SPK_FG(5, 1)
+    SPK_FG(6, 1)
+    SPK_FG(7, 1)
+    SPK_FG(8, 1)
     default: return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: in_dim %d", in_dim);
   }
+#undef SPK_FG
   return spk::check_launch("spk_gemv_fused");
 }
 
@@ -543,7 +652,8 @@ static int attention_common(const SpkAttnArgs* p, int T, int positions, const ch
   if (!p->qg || !p->k || !p->v || !p->q_norm_w || !p->k_norm_w || !p->rope || !p->kv_cache || !p->out ||
       !p->workspace)
     return spk::fail(SPK_ERR_NULL, "%s: NULL pointer", who);
-  if (p->max_seq <= 0 || T <= 0) return spk::fail(SPK_ERR_SHAPE, "%s: max_seq %d tokens %d", who, p->max_seq, T);
+  if (p->max_seq <= 0 || p->max_seq > 65536 || T <= 0 || positions > 65536)
+    return spk::fail(SPK_ERR_SHAPE, "%s: max_seq %d (at most 65536) tokens %d", who, p->max_seq, T);
   if (p->workspace_bytes < spk_attention_workspace_size(positions, T))
     return spk::fail(SPK_ERR_ARG, "%s: workspace %zu < %zu bytes", who, p->workspace_bytes,
                      spk_attention_workspace_size(positions, T));

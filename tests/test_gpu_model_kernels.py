@@ -440,3 +440,27 @@ def test_chunk_prefill_ordered_bitexact(dev, oracle, T, f16, l2, init):
     torch.cuda.synchronize()
     assert np.array_equal(core.cpu().numpy().view(np.uint32), ec.reshape(-1).view(np.uint32))
     assert np.array_equal(state.cpu().numpy().view(np.uint32), es.reshape(-1).view(np.uint32))
+
+
+def test_gemv_silu_pair_bitexact(dev):
+    """gate/up projections with silu_gate.comp fused: fp16(silu(fp16(Wg.x)) * fp16(Wu.x))."""
+    from spock_amd import _lib
+    n = 3584
+    h = _rand16(95, 1024)
+    w = _rand16(96, 1024, 0.02)
+    Wg = _rand16(97, n * 1024, 0.02).reshape(n, 1024)
+    Wu = _rand16(98, n * 1024, 0.02).reshape(n, 1024)
+    dh, dw, dWg, dWu = _h(h, dev), _h(w, dev), _h(Wg, dev), _h(Wu, dev)
+    y = torch.empty(n, dtype=torch.float16, device=dev)
+    inp = _lib.SpkGemvInput()
+    inp.kind, inp.in_dim, inp.x, inp.x2 = _lib.SPK_GEMV_IN_RMSNORM, 1024, dh.data_ptr(), dw.data_ptr()
+    arr = (_lib.SpkGemvOutput * 1)()
+    arr[0].W, arr[0].y, arr[0].out_dim, arr[0].W_up = dWg.data_ptr(), y.data_ptr(), n, dWu.data_ptr()
+    _lib.check(_lib.lib().spk_gemv_fused(C.byref(inp), arr, 1, _stream()), "spk_gemv_fused pair")
+    torch.cuda.synchronize()
+    xn = np.zeros(1024, np.uint16)
+    _om().orc_rmsnorm1024(_p(h), _p(w), _p(xn))
+    g, u = _orc_matvec(Wg, xn), _orc_matvec(Wu, xn)
+    exp = np.zeros(n, np.uint16)
+    _om().orc_silu_gate(_p(g), _p(u), _p(exp), n)
+    assert np.array_equal(_u16(y), exp)
