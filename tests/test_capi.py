@@ -9,8 +9,8 @@ import pytest
 from conftest import ROOT
 
 
-def _declared():
-    hdr = (ROOT / "include" / "spock_hip.h").read_text()
+def _declared(header="spock_hip.h"):
+    hdr = (ROOT / "include" / header).read_text()
     hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
     return sorted(set(re.findall(r"\b(spk_[a-z0-9_]+)\s*\(", hdr)))
 
@@ -63,3 +63,22 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(_lib.SpockError, match="no CPU fallback"):
         _lib.lib()
+
+
+def test_model_header_binding_and_exports():
+    """include/spock_model.h (the session surface) against spock_amd/model.py
+    and libspock_hip_host.so's exports."""
+    from spock_amd import model
+    assert set(_declared("spock_model.h")) == set(model.SIGNATURES)
+    lib = model.lib()
+    for name in _declared("spock_model.h"):
+        assert hasattr(lib, name), name
+    assert C.sizeof(model.SpkGenerateStats) == 40
+
+
+def test_model_session_errors_without_device(tmp_path):
+    from spock_amd import model
+    with pytest.raises(model.ModelError, match="text_repack_manifest.json|cannot open|No such"):
+        model.Session(tmp_path / "absent")
+    assert model.lib().spk_model_info(None, None, None, None) == -1
+    assert model.lib().spk_artifact_write_synthetic(str(tmp_path / "x").encode(), 0, 10, 1) == -1
