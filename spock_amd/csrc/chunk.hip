@@ -48,6 +48,9 @@ constexpr int kWsKdT = 20480;
 constexpr int kWsQs = 28672;
 constexpr int kWsMisc = 28736;
 constexpr int kWsStride = 28800;  // 115200 bytes, a multiple of 256
+// Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
+// which untyped loads/stores need for the num_records range check to apply.
+constexpr int kBufDword3 = 0x00020000;
 
 __device__ __forceinline__ f4v mfma4(float a, float b, f4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -486,9 +489,12 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
       for (int u = 0; u < 8; ++u)
         g.a[u] = R::ld4(q, ((size_t)h * p.N + tok0 + row) * kD + 16 * u + 4 * lg);
       g.qs = ws[kWsQs + tok];
+      // all four blocks, the zero upper ones included: no load sits under a
+      // branch, so the compiler's vmcnt bookkeeping stays exact and the
+      // prefetch of the next chunk is never waited for early
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        if (u <= M) g.at[u] = *reinterpret_cast<const float4*>(ws + kWsA + tok * 64 + 16 * u + 4 * lg);
+        g.at[u] = *reinterpret_cast<const float4*>(ws + kWsA + tok * 64 + 16 * u + 4 * lg);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -521,6 +527,16 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
         acc1 = mfma4(elem(av, e), elem(b1, e), acc1);
       }
     }
+    // The next chunk's loads (issued just before this stage, same scheduling
+    // region) are spread over the MFMA stream, two after every eight MFMAs:
+    // issued as one burst by all eight wavefronts they queue in the CU's
+    // vector-memory pipe and stall the issuing wavefront for thousands of
+    // cycles.  (sched_group_barrier masks: 0x020 VMEM read, 0x008 MFMA.)
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    }
 
     // ---- stage B: v_new = U - W S
     if (WROLE) {
@@ -532,28 +548,30 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
     }
     __syncthreads();
 
-    // ---- stage C: o = Q*qs S + A v_new
+    // ---- stage C: o = Q*qs S + A v_new (the blocks above the diagonal of A
+    // are zero, so all four are taken: the SIMD's critical path is the
+    // M = 3 wave's either way)
     if (!WROLE) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (u <= M) {
-          const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
-          const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
+        const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
+        const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc0 = mfma4(elem(cur.at[u], e), elem(b0, e), acc0);
-            acc1 = mfma4(elem(cur.at[u], e), elem(b1, e), acc1);
-          }
+        for (int e = 0; e < 4; ++e) {
+          acc0 = mfma4(elem(cur.at[u], e), elem(b0, e), acc0);
+          acc1 = mfma4(elem(cur.at[u], e), elem(b1, e), acc1);
         }
       }
+      // rows tok0 .. tok0+len-1 of this head through a buffer resource of
+      // len rows: the hardware drops the padding rows' stores (offset past
+      // num_records), with no branch around the stores
+      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+          p.core + ((size_t)h * p.core_hs + tok0) * kD, 0, len * kD * (int)sizeof(float), kBufDword3);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tok = 16 * M + 4 * lg + r;
-        if (tok < len) {
-          float* o = p.core + ((size_t)h * p.core_hs + tok0 + tok) * kD + n0 + li;
-          o[0] = acc0[r];
-          o[16] = acc1[r];
-        }
+        const int off = ((16 * M + 4 * lg + r) * kD + n0 + li) * (int)sizeof(float);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc0[r]), out, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc1[r]), out, off + 64, 0, 0);
       }
     }
 
@@ -582,15 +600,16 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
   };
 
   // Two register sets used alternately: the loads of chunk c+1 are in flight
-  // while chunk c computes.
+  // while chunk c computes.  The prefetch index is clamped (the last chunk is
+  // fetched twice) rather than guarded, for the same reason as above.
   StateRegs ra, rb;
   if (nchunks > 0) load(ra, 0);
   __syncthreads();
   for (int c = 0; c < nchunks; c += 2) {
-    if (c + 1 < nchunks) load(rb, c + 1);
+    load(rb, min(c + 1, nchunks - 1));
     step(ra, c);
     if (c + 1 >= nchunks) break;
-    if (c + 2 < nchunks) load(ra, c + 2);
+    load(ra, min(c + 2, nchunks - 1));
     step(rb, c + 1);
   }
 }
