@@ -11,17 +11,21 @@
 //
 // Two launches:
 //  1. chunk_intra_kernel -- one workgroup per (chunk, head), all chunks of all
-//     sequences in parallel.  K/Q/V of the chunk are staged in LDS; K K^T and
-//     Q K^T are 16x16x4 fp32 MFMA tiles; T is inverted blockwise (4 diagonal
-//     16x16 blocks by per-lane forward substitution in registers, off-diagonal
-//     blocks T_IJ = -T_II sum_M L_IM T_MJ as MFMA products); U and W are MFMA
-//     products skipping the zero upper blocks of T.  U, W, A and per-token
-//     scales go to the workspace.
+//     sequences in parallel.  Every global load is issued up front; K and V
+//     rows are staged in LDS in the input type (50 KB for fp16, so three
+//     workgroups share a CU).  K K^T and Q K^T are 16x16x4 fp32 MFMA tiles,
+//     five independent accumulators per wavefront; T is inverted blockwise (4
+//     diagonal 16x16 blocks by per-lane forward substitution, written over L's,
+//     off-diagonal blocks T_IJ = -T_II sum_M L_IM T_MJ as MFMA products); U
+//     and W are MFMA products over the nonzero blocks of T with beta and the
+//     decays applied to the B operand as it is read.  U^T, W, A, raw K^T and
+//     per-token scales go to the workspace.
 //  2. chunk_state_kernel -- one workgroup per (sequence, head, 32-column tile
 //     of the value dim): columns of S evolve independently, so the sequential
 //     chunk scan runs on 4*H*num_seqs workgroups.  The 128x32 state tile lives
-//     in LDS; each wavefront owns 32 rows of [W; Q e^g] S, of the output and of
-//     the state update, all 16x16x4 MFMA.
+//     in LDS; each wavefront owns 16 rows of [W; Q e^g] S, of the output and
+//     of the state update (S += K^T diag(Ks) v_new), all 16x16x4 MFMA, with the
+//     next chunk's operands prefetched into registers during the current one.
 // MFMA operand trick: the contraction index of a 16x16x4 step is a free
 // permutation, so lane (m = l%16, g = l/16) reads a float4 at k = 16u + 4g and
 // feeds its elements to 4 consecutive steps; the B operand uses the same map.
@@ -34,20 +38,23 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int kC = 64;
 constexpr int kD = 128;
-constexpr int kLDK = 132;  // LDS row stride (floats) of [64][128] tiles
 constexpr int kLdST = 132;  // LDS row stride of the transposed 32-column state tile
 constexpr int kLdVT = 68;   // LDS row stride of the transposed v_new tile
 // workspace record per (chunk, head), in floats.  Layouts are the ones the
-// state scan reads with 16-byte loads along its contraction index:
-//   U^T  [128 value cols][64 tokens]      W  [64 tokens][128 key dims]
-//   A    [64 tokens][64 tokens]           KdT [128 key dims][64 tokens], K*ks
+// state scan reads along its contraction index:
+//   U^T [128 value cols][64 tokens] fp32   W   [64 tokens][128 key dims] fp32
+//   A   [64 tokens][64 tokens] fp32        K^T [128 key dims][64 tokens], raw
+//                                              input type (fp16 or fp32)
+//   Qs  [64] Q scale (q_scale iq e^gcum)   Ks  [64] e^{gL - gcum} ik
+//   Misc[0] e^{gL}
 constexpr int kWsUT = 0;
 constexpr int kWsW = 8192;
 constexpr int kWsA = 16384;
-constexpr int kWsKdT = 20480;
+constexpr int kWsKT = 20480;
 constexpr int kWsQs = 28672;
-constexpr int kWsMisc = 28736;
-constexpr int kWsStride = 28800;  // 115200 bytes, a multiple of 256
+constexpr int kWsKs = 28736;
+constexpr int kWsMisc = 28800;
+constexpr int kWsStride = 28864;  // 115456 bytes, a multiple of 256
 // Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
 // which untyped loads/stores need for the num_records range check to apply.
 constexpr int kBufDword3 = 0x00020000;
@@ -137,49 +144,138 @@ template <> struct RawOf<uint16_t> {
   }
 };
 
-// V staged transposed in LDS: [128 value cols][64 tokens (+pad)], fp16 for
-// fp16 inputs (4 tokens = one 8-byte read) and fp32 otherwise.
-template <typename TIn> struct VStage;
-template <> struct VStage<uint16_t> {
-  static constexpr int kLd = 72;  // halves per row (144 B)
+// K and V rows staged in LDS in the input type (fp16 rows stay fp16) with a
+// row stride of 132 elements: the 16 rows of one 16-lane group of an 8-byte
+// operand read (fp16), or the 8 rows of an 8-lane group of a 16-byte read
+// (fp32), start on distinct bank groups.
+template <typename TIn> struct RowStage;
+template <> struct RowStage<uint16_t> {
+  static constexpr int kLd = 132;  // halves (264 B)
   typedef uint16_t T;
-  static __device__ __forceinline__ void put(T* s, int col, int tok, const float4& raw, int e) {
-    const uint32_t w = __float_as_uint(e < 2 ? raw.x : raw.y);
-    s[col * kLd + tok] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
+  // raw: 4 halves as loaded by RawOf<uint16_t>::ld4
+  static __device__ __forceinline__ void put4(T* s, int r, int c, const float4& raw) {
+    *reinterpret_cast<uint2*>(s + r * kLd + c) = make_uint2(__float_as_uint(raw.x), __float_as_uint(raw.y));
   }
-  static __device__ __forceinline__ float4 get4(const T* s, int col, int tok) {
-    const uint2 u = *reinterpret_cast<const uint2*>(s + col * kLd + tok);
+  static __device__ __forceinline__ float4 get4(const T* s, int r, int c) {
+    const uint2 u = *reinterpret_cast<const uint2*>(s + r * kLd + c);
     return make_float4(spk::h2f((uint16_t)(u.x & 0xffffu)), spk::h2f((uint16_t)(u.x >> 16)),
                        spk::h2f((uint16_t)(u.y & 0xffffu)), spk::h2f((uint16_t)(u.y >> 16)));
   }
-};
-template <> struct VStage<float> {
-  static constexpr int kLd = 68;
-  typedef float T;
-  static __device__ __forceinline__ void put(T* s, int col, int tok, const float4& raw, int e) {
-    s[col * kLd + tok] = elem(raw, e);
+  static __device__ __forceinline__ float get1(const T* s, int r, int c) { return spk::h2f(s[r * kLd + c]); }
+  // rows r..r+3 of column c, stored as 4 consecutive elements at dst
+  static __device__ __forceinline__ void col4_to(const T* s, int r, int c, T* dst) {
+    const uint32_t a = s[r * kLd + c], b = s[(r + 1) * kLd + c];
+    const uint32_t x = s[(r + 2) * kLd + c], y = s[(r + 3) * kLd + c];
+    *reinterpret_cast<uint2*>(dst) = make_uint2(a | (b << 16), x | (y << 16));
   }
-  static __device__ __forceinline__ float4 get4(const T* s, int col, int tok) {
-    return *reinterpret_cast<const float4*>(s + col * kLd + tok);
+};
+template <> struct RowStage<float> {
+  static constexpr int kLd = 132;  // floats (528 B)
+  typedef float T;
+  static __device__ __forceinline__ void put4(T* s, int r, int c, const float4& raw) {
+    *reinterpret_cast<float4*>(s + r * kLd + c) = raw;
+  }
+  static __device__ __forceinline__ float4 get4(const T* s, int r, int c) {
+    return *reinterpret_cast<const float4*>(s + r * kLd + c);
+  }
+  static __device__ __forceinline__ float get1(const T* s, int r, int c) { return s[r * kLd + c]; }
+  static __device__ __forceinline__ void col4_to(const T* s, int r, int c, T* dst) {
+    *reinterpret_cast<float4*>(dst) =
+        make_float4(s[r * kLd + c], s[(r + 1) * kLd + c], s[(r + 2) * kLd + c], s[(r + 3) * kLd + c]);
   }
 };
 
-// L and T are block lower triangular: the 10 blocks (I >= J) of 16x16 are
-// stored packed, block (I,J) at (I(I+1)/2 + J) * 256, row-major with stride 16.
+// L is block lower triangular: its 10 blocks (I >= J) of 16x16 are stored
+// packed, block (I,J) at (I(I+1)/2 + J) * 256, row-major with stride 16.  T =
+// (I + L)^{-1} has the same shape; its diagonal blocks overwrite L's once those
+// are solved (nothing reads them afterwards) and its 6 off-diagonal blocks
+// (I > J) have a buffer of their own.
 __device__ __forceinline__ int blk(int I, int J) { return (I * (I + 1) / 2 + J) * 256; }
+__device__ __forceinline__ int offblk(int I, int J) { return ((I - 1) * I / 2 + J) * 256; }
 
 constexpr float kLog2e = 1.44269504f;
 
-template <typename TIn>
-__global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
+// The five Gram tiles of wavefront W: K K^T row block 3-W (tiles J = 0..3-W)
+// and Q K^T row block W (tiles J = 0..W), accumulated together so that the
+// MFMA stream carries five independent chains.  The K rows of block J are the
+// B operand of both products and are read once.
+template <typename TIn, int W>
+__device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, const float4 (&qa)[8],
+                                           int li, int lg, f4v (&acc)[5]) {
+  typedef RowStage<TIn> RS;
   typedef RawOf<TIn> R;
-  typedef VStage<TIn> VS;
-  __shared__ float sK[64 * kLDK];                       // K rows (normalised if requested)
-  __shared__ typename VS::T sVT[128 * VS::kLd];         // V^T
-  __shared__ float sL[10 * 256];                        // L blocks
-  __shared__ float sT[10 * 256];                        // T blocks, later T diag(beta [e^g])
-  __shared__ float sX[4 * 256];                         // per-wave product scratch
-  __shared__ float sG[64], sB[64], sE[64], sKS[64], sIQ[64], sIK[64];
+  constexpr int Ik = 3 - W;
+  constexpr int nJ = (Ik > W ? Ik : W) + 1;
+#pragma unroll
+  for (int t = 0; t < 5; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    float4 kb[nJ];
+#pragma unroll
+    for (int J = 0; J < nJ; ++J) kb[J] = RS::get4(sK, 16 * J + li, 16 * u + 4 * lg);
+    const float4 qf = R::cvt4(qa[u]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int t = 0; t < 5; ++t) {
+        const bool isq = t > Ik;
+        const int J = isq ? t - Ik - 1 : t;
+        float4 a;
+        if (isq) a = qf;
+        else a = kb[Ik];
+        acc[t] = mfma4(elem(a, e), elem(kb[J], e), acc[t]);
+      }
+    }
+  }
+}
+
+// Epilogue of the Gram tiles: L = strict_lower(beta_i k_i.k_j Gamma_ij) into
+// LDS, A = lower(q_i.k_j scale Gamma_ij) into the workspace (with the inverse
+// L2 norms when requested; 1 otherwise).
+template <int W>
+__device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG, const float* sB,
+                                           const float* sIK, float iq_scale, float* sL, float* ws,
+                                           int li, int lg, int lane) {
+  constexpr int Ik = 3 - W;
+#pragma unroll
+  for (int t = 0; t < 5; ++t) {
+    const bool isq = t > Ik;
+    const int I = isq ? W : Ik;
+    const int J = isq ? t - Ik - 1 : t;
+    const int j = 16 * J + li;
+    const float ikj = sIK[j];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * I + 4 * lg + r;
+      const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
+      if (!isq) {
+        sL[blk(I, J) + (4 * lg + r) * 16 + li] = (j < i) ? sB[i] * (acc[t][r] * (sIK[i] * ikj)) * dec : 0.0f;
+      } else {
+        // iq of row i lives in lane (i - 16W) of this wavefront
+        const float iq = __shfl(iq_scale, 4 * lg + r);
+        ws[kWsA + i * 64 + j] = (j <= i) ? (acc[t][r] * (iq * ikj)) * dec : 0.0f;
+      }
+    }
+  }
+  // strictly-upper blocks of this wavefront's A row block are zero
+  for (int e = lane; e < (3 - W) * 256; e += 64)
+    ws[kWsA + (16 * W + (e >> 4) % 16) * 64 + 16 * (W + 1) + (e >> 8) * 16 + (e & 15)] = 0.0f;
+}
+
+// fp16 inputs: 3 workgroups per CU (50 KB of LDS each), so at most 168 VGPRs;
+// fp32 inputs stage 83 KB and run one workgroup per CU.
+template <typename TIn>
+__global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_kernel(ChunkParams p) {
+  typedef RawOf<TIn> R;
+  typedef RowStage<TIn> RS;
+  __shared__ __align__(16) typename RS::T sK[64 * RS::kLd];  // K rows, raw
+  __shared__ __align__(16) typename RS::T sV[64 * RS::kLd];  // V rows, raw
+  __shared__ __align__(16) float sL[10 * 256];  // L blocks; diagonal blocks become T's
+  __shared__ __align__(16) float sT[6 * 256];   // off-diagonal T blocks
+  __shared__ __align__(16) float sG[64];   // gcum
+  __shared__ __align__(16) float sB[64];   // beta
+  __shared__ __align__(16) float sBE[64];  // beta e^gcum ik
+  __shared__ __align__(16) float sIK[64];  // inverse K norms (1 without L2 normalisation)
 
   const int gchunk = blockIdx.x;
   const int h = blockIdx.y;
@@ -196,7 +292,16 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
   const TIn* v = static_cast<const TIn*>(p.v);
   float* ws = p.ws + ((size_t)gchunk * p.H + h) * kWsStride;
 
-  // ---- Q row block `wave` straight into MFMA A-operand registers (raw)
+  // ---- every global load first: g/beta (wave 0), Q row block `wave` as MFMA
+  // A-operand registers, 8 K and 8 V row segments per thread.  Padding rows
+  // read row 0 and are zeroed when staged.
+  float gv = 0.0f, bv = 0.0f;
+  if (wave == 0) {
+    const int tt = lane < len ? lane : 0;
+    gv = p.g[(size_t)h * p.N + t0 + tt];
+    bv = p.beta[(size_t)h * p.N + t0 + tt];
+    if (lane >= len) gv = bv = 0.0f;
+  }
   float4 qa[8];
   {
     const int row = 16 * wave + li;
@@ -204,137 +309,97 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) qa[u] = R::ld4(q, ((size_t)h * p.N + t0 + rr) * kD + 16 * u + 4 * lg);
   }
-  // ---- stage K rows (fp32) and V^T; padding rows are zero, g = beta = 0
-  for (int i = tid; i < 64 * 32; i += 256) {
-    const int r = i >> 5;
-    const int c = (i & 31) * 4;
-    float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 vr = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (r < len) {
-      const size_t off = ((size_t)h * p.N + t0 + r) * kD + c;
-      kv = R::cvt4(R::ld4(k, off));
-      vr = R::ld4(v, off);
-    }
-    *reinterpret_cast<float4*>(&sK[r * kLDK + c]) = kv;
+  float4 kr[8], vr[8];
+  const int c4 = (tid & 31) * 4;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) VS::put(sVT, c + e, r, vr, e);
+  for (int it = 0; it < 8; ++it) {
+    const int r = (tid >> 5) + 8 * it;
+    const size_t off = ((size_t)h * p.N + t0 + (r < len ? r : 0)) * kD + c4;
+    kr[it] = R::ld4(k, off);
+    vr[it] = R::ld4(v, off);
   }
-  if (tid < 64) {
-    const bool valid = tid < len;
-    sG[tid] = valid ? p.g[(size_t)h * p.N + t0 + tid] : 0.0f;
-    sB[tid] = valid ? p.beta[(size_t)h * p.N + t0 + tid] : 0.0f;
+  // gcum (running sum in token order, deltanet_chunk.cpp:137-142): lane t adds
+  // g_0 .. g_t left to right (adding +0 past t), so every lane's sum is
+  // rounded exactly as the reference's running sum
+  if (wave == 0) {
+    float run = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      const float gj = __shfl(gv, j);
+      run = run + (j <= lane ? gj : 0.0f);
+    }
+    sG[lane] = run;
+    sB[lane] = bv;
+  }
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = (tid >> 5) + 8 * it;
+    float4 kx = kr[it], vx = vr[it];
+    if (r >= len) kx = vx = make_float4(0.f, 0.f, 0.f, 0.f);
+    RS::put4(sK, r, c4, kx);
+    RS::put4(sV, r, c4, vx);
   }
   __syncthreads();
 
-  // ---- gcum (running sum in token order, deltanet_chunk.cpp:137-142) and,
-  // if requested, inverse L2 norms (eps inside the sqrt, :27-39)
-  if (tid == 0) {
-    float gv[64];
+  // ---- inverse L2 norms (eps inside the sqrt, deltanet_chunk.cpp:27-39):
+  // K rows from LDS, 4 threads per row; Q rows from this lane's registers
+  float iq = 1.0f;
+  if (p.l2) {
+    float ssq = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 64; r += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(&sG[r]);
-      gv[r] = x.x; gv[r + 1] = x.y; gv[r + 2] = x.z; gv[r + 3] = x.w;
+    for (int u = 0; u < 8; ++u) {
+      const float4 x = R::cvt4(qa[u]);
+      ssq = ssq + x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
     }
-    float run = 0.0f;
+    ssq = ssq + __shfl_xor(ssq, 16);
+    ssq = ssq + __shfl_xor(ssq, 32);
+    iq = 1.0f / sqrtf(ssq + 1e-6f);
+    const int r = tid >> 2, part = tid & 3;
+    float sk = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 64; ++r) {
-      run = run + gv[r];
-      gv[r] = run;
+    for (int c = 0; c < 32; c += 4) {
+      const float4 x = RS::get4(sK, r, 32 * part + c);
+      sk = sk + x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
     }
-#pragma unroll
-    for (int r = 0; r < 64; r += 4)
-      *reinterpret_cast<float4*>(&sG[r]) = make_float4(gv[r], gv[r + 1], gv[r + 2], gv[r + 3]);
+    sk = sk + __shfl_xor(sk, 1);
+    sk = sk + __shfl_xor(sk, 2);
+    if (part == 0) sIK[r] = 1.0f / sqrtf(sk + 1e-6f);
+  } else if (tid < 64) {
+    sIK[tid] = 1.0f;
   }
-  if (p.l2 && tid >= 64 && tid < 192) {
-    // rows of Q come from global (this block owns them only as MFMA operands),
-    // so their norms are taken from global too
-    const int r = (tid - 64) & 63;
-    float ss = 0.0f;
-    if (tid < 128) {
-      const int rr = r < len ? r : 0;
-      for (int c = 0; c < kD; c += 4) {
-        const float4 x = R::cvt4(R::ld4(q, ((size_t)h * p.N + t0 + rr) * kD + c));
-        ss = ss + x.x * x.x; ss = ss + x.y * x.y; ss = ss + x.z * x.z; ss = ss + x.w * x.w;
-      }
-      sIQ[r] = 1.0f / sqrtf(ss + 1e-6f);
-    } else {
-      for (int c = 0; c < kD; ++c) ss = ss + sK[r * kLDK + c] * sK[r * kLDK + c];
-      sIK[r] = 1.0f / sqrtf(ss + 1e-6f);
-    }
+
+  // ---- Gram tiles (raw dot products; decays and scales in the epilogue)
+  f4v acc[5];
+  switch (wave) {
+    case 0: gram_tiles<TIn, 0>(sK, qa, li, lg, acc); break;
+    case 1: gram_tiles<TIn, 1>(sK, qa, li, lg, acc); break;
+    case 2: gram_tiles<TIn, 2>(sK, qa, li, lg, acc); break;
+    default: gram_tiles<TIn, 3>(sK, qa, li, lg, acc); break;
   }
   __syncthreads();
-  if (p.l2) {
-    for (int i = tid; i < 64 * kD; i += 256) {
-      const int r = i >> 7;
-      sK[r * kLDK + (i & 127)] *= sIK[r];
-    }
+
+  // ---- epilogue: L into LDS, A into the workspace; per-token scales
+  const float iq_scale = iq * p.q_scale;  // lane li of any group: row 16*wave + li
+  switch (wave) {
+    case 0: gram_store<0>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane); break;
+    case 1: gram_store<1>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane); break;
+    case 2: gram_store<2>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane); break;
+    default: gram_store<3>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane); break;
   }
   const float gL = sG[63];
+  if (lg == 0) ws[kWsQs + 16 * wave + li] = iq_scale * expf(sG[16 * wave + li]);  // the scan re-reads Q raw
   if (tid < 64) {
-    const float iq = p.l2 ? sIQ[tid] : 1.0f;
     const float eg = expf(sG[tid]);
-    sE[tid] = eg;
-    sKS[tid] = expf(gL - sG[tid]);
-    ws[kWsQs + tid] = (iq * p.q_scale) * eg;  // the scan re-reads Q raw
-    if (!p.l2) sIQ[tid] = 1.0f;
+    sBE[tid] = sB[tid] * eg * sIK[tid];
+    ws[kWsKs + tid] = expf(gL - sG[tid]) * sIK[tid];
   }
   if (tid == 0) ws[kWsMisc] = expf(gL);
   __syncthreads();
 
-  // ---- (K e^{gL-g})^T, 16 lanes per 256-byte row
-  for (int i = tid; i < 128 * 16; i += 256) {
-    const int kd = i >> 4;
-    const int t = (i & 15) * 4;
-    *reinterpret_cast<float4*>(ws + kWsKdT + kd * 64 + t) =
-        make_float4(sK[t * kLDK + kd] * sKS[t], sK[(t + 1) * kLDK + kd] * sKS[t + 1],
-                    sK[(t + 2) * kLDK + kd] * sKS[t + 2], sK[(t + 3) * kLDK + kd] * sKS[t + 3]);
-  }
-
-  // ---- K K^T row block 3-w -> L, Q K^T row block w -> A: 5 tiles per wave
-  {
-    const int Ik = 3 - wave;
-    const float iq = sIQ[16 * wave + li];
-    float4 qf[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float4 x = R::cvt4(qa[u]);
-      qf[u] = make_float4(x.x * iq, x.y * iq, x.z * iq, x.w * iq);
-    }
-    for (int tt = 0; tt < 5; ++tt) {
-      const bool isq = tt > 3 - wave;
-      const int I = isq ? wave : Ik;
-      const int J = isq ? tt - (4 - wave) : tt;
-      f4v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float4 b4 = *reinterpret_cast<const float4*>(&sK[(16 * J + li) * kLDK + 16 * u + 4 * lg]);
-        const float4 a4 = isq ? qf[u] : *reinterpret_cast<const float4*>(&sK[(16 * I + li) * kLDK + 16 * u + 4 * lg]);
-        acc = mfma4(a4.x, b4.x, acc);
-        acc = mfma4(a4.y, b4.y, acc);
-        acc = mfma4(a4.z, b4.z, acc);
-        acc = mfma4(a4.w, b4.w, acc);
-      }
-      const int j = 16 * J + li;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * lg + r;
-        const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
-        if (!isq) {
-          sL[blk(I, J) + (4 * lg + r) * 16 + li] = (j < i) ? sB[i] * acc[r] * dec : 0.0f;
-        } else {
-          ws[kWsA + i * 64 + j] = (j <= i) ? acc[r] * p.q_scale * dec : 0.0f;
-        }
-      }
-    }
-    // strictly-upper blocks of this wave's A row block are zero
-    for (int e = lane; e < (3 - wave) * 256; e += 64)
-      ws[kWsA + (16 * wave + (e >> 4) % 16) * 64 + 16 * (wave + 1) + (e >> 8) * 16 + (e & 15)] = 0.0f;
-  }
-  __syncthreads();
-
-  // ---- diagonal blocks of T: lane j < 16 of wave w solves column j of block w
+  // ---- diagonal blocks of T by forward substitution, lane j < 16 of wave w
+  // solving column j of block w; written over L's block once it is read
   if (li == lane) {
-    const float* Lb = sL + blk(wave, wave);
+    float* Lb = sL + blk(wave, wave);
     const int j = lane;
     float tc[16];
 #pragma unroll
@@ -344,88 +409,81 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
       for (int m = 0; m < i; ++m) s = __builtin_fmaf(Lb[i * 16 + m], tc[m], s);
       tc[i] = (i == j) ? 1.0f : (i < j ? 0.0f : -s);
     }
-    float* Tb = sT + blk(wave, wave);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) Tb[i * 16 + j] = tc[i];
+    for (int i = 0; i < 16; ++i) Lb[i * 16 + j] = tc[i];
   }
   __syncthreads();
 
-  // ---- off-diagonal blocks by distance d = I - J: T_IJ = -T_II sum_M L_IM T_MJ
+  // ---- off-diagonal blocks by distance d = I - J: T_IJ = -T_II sum_M L_IM T_MJ.
+  // With contraction index k = 4*lg + s, the product's C fragment is already
+  // the B operand of the second product: no LDS round trip.
   for (int d = 1; d < 4; ++d) {
-    const bool active = wave < 4 - d;
-    const int J = wave;
-    const int I = J + d;
-    if (active) {
-      f4v acc = {0.f, 0.f, 0.f, 0.f};
+    if (wave < 4 - d) {
+      const int J = wave;
+      const int I = J + d;
+      f4v x = {0.f, 0.f, 0.f, 0.f};
       for (int M = J; M < I; ++M) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&sL[blk(I, M) + li * 16 + 4 * lg]);
+        const float* tmj = (M == J) ? sL + blk(J, J) : sT + offblk(M, J);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          acc = mfma4(sL[blk(I, M) + li * 16 + 4 * s + lg], sT[blk(M, J) + (4 * s + lg) * 16 + li], acc);
+        for (int s = 0; s < 4; ++s) x = mfma4(elem(a4, s), tmj[(4 * lg + s) * 16 + li], x);
       }
+      const float4 a4 = *reinterpret_cast<const float4*>(&sL[blk(I, I) + li * 16 + 4 * lg]);
+      f4v y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sX[wave * 256 + (4 * lg + r) * 16 + li] = acc[r];
-    }
-    __syncthreads();
-    if (active) {
-      f4v acc = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < 4; ++s) y = mfma4(elem(a4, s), x[s], y);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        acc = mfma4(sT[blk(I, I) + li * 16 + 4 * s + lg], sX[wave * 256 + (4 * s + lg) * 16 + li], acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sT[blk(I, J) + (4 * lg + r) * 16 + li] = -acc[r];
+      for (int r = 0; r < 4; ++r) sT[offblk(I, J) + (4 * lg + r) * 16 + li] = -y[r];
     }
     __syncthreads();
   }
 
-  // ---- columns of T scaled by beta, then U = (T diag(beta)) V, stored as U^T
-  for (int e = tid; e < 10 * 256; e += 256) {
-    const int b = e >> 8;
-    const int I = b >= 6 ? 3 : b >= 3 ? 2 : b >= 1 ? 1 : 0;
-    const int J = b - I * (I + 1) / 2;
-    sT[e] *= sB[16 * J + (e & 15)];
-  }
-  __syncthreads();
+  // ---- U = T diag(beta) V (stored as U^T) and W = T diag(beta e^g ik) K, row
+  // blocks I = 0..3 of two 16-column tiles per wavefront accumulated together;
+  // the per-token factors are applied to the B operand as it is read
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
     const int n = 16 * (2 * wave + jj) + li;
-    for (int I = 0; I < 4; ++I) {
-      f4v acc = {0.f, 0.f, 0.f, 0.f};
-      for (int u = 0; u <= I; ++u) {
-        const float4 a4 = *reinterpret_cast<const float4*>(&sT[blk(I, u) + li * 16 + 4 * lg]);
-        const float4 b4 = VS::get4(sVT, n, 16 * u + 4 * lg);
-        acc = mfma4(a4.x, b4.x, acc);
-        acc = mfma4(a4.y, b4.y, acc);
-        acc = mfma4(a4.z, b4.z, acc);
-        acc = mfma4(a4.w, b4.w, acc);
-      }
-      *reinterpret_cast<float4*>(ws + kWsUT + n * 64 + 16 * I + 4 * lg) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    }
-  }
-  __syncthreads();
-  // ---- columns scaled by e^gcum, then W = (T diag(beta e^g)) K
-  for (int e = tid; e < 10 * 256; e += 256) {
-    const int b = e >> 8;
-    const int I = b >= 6 ? 3 : b >= 3 ? 2 : b >= 1 ? 1 : 0;
-    const int J = b - I * (I + 1) / 2;
-    sT[e] *= sE[16 * J + (e & 15)];
-  }
-  __syncthreads();
+    f4v au[4], aw[4];
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    const int n = 16 * (2 * wave + jj) + li;
-    for (int I = 0; I < 4; ++I) {
-      f4v acc = {0.f, 0.f, 0.f, 0.f};
-      for (int u = 0; u <= I; ++u) {
-        const float4 a4 = *reinterpret_cast<const float4*>(&sT[blk(I, u) + li * 16 + 4 * lg]);
-        const int t = 16 * u + 4 * lg;
-        acc = mfma4(a4.x, sK[t * kLDK + n], acc);
-        acc = mfma4(a4.y, sK[(t + 1) * kLDK + n], acc);
-        acc = mfma4(a4.z, sK[(t + 2) * kLDK + n], acc);
-        acc = mfma4(a4.w, sK[(t + 3) * kLDK + n], acc);
+    for (int I = 0; I < 4; ++I) au[I] = aw[I] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = 16 * u + 4 * lg;
+      const float4 bb = *reinterpret_cast<const float4*>(&sB[t]);
+      const float4 be = *reinterpret_cast<const float4*>(&sBE[t]);
+      float vb[4], kb[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        vb[s] = RS::get1(sV, t + s, n) * elem(bb, s);
+        kb[s] = RS::get1(sK, t + s, n) * elem(be, s);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ws[kWsW + (16 * I + 4 * lg + r) * kD + n] = acc[r];
+      for (int I = u; I < 4; ++I) {
+        const float* tp = (I == u) ? sL + blk(I, I) : sT + offblk(I, u);
+        const float4 a4 = *reinterpret_cast<const float4*>(&tp[li * 16 + 4 * lg]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          au[I] = mfma4(elem(a4, s), vb[s], au[I]);
+          aw[I] = mfma4(elem(a4, s), kb[s], aw[I]);
+        }
+      }
     }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      *reinterpret_cast<float4*>(ws + kWsUT + n * 64 + 16 * I + 4 * lg) = make_float4(au[I][0], au[I][1], au[I][2], au[I][3]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ws[kWsW + (16 * I + 4 * lg + r) * kD + n] = aw[I][r];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // one column tile's operands live at a time
+  }
+
+  // ---- K^T [128 key dims][64 tokens], raw input type, 16 lanes per row
+  typename RS::T* kt = reinterpret_cast<typename RS::T*>(ws + kWsKT);
+  for (int i = tid; i < 128 * 16; i += 256) {
+    const int kd = i >> 4;
+    const int t = (i & 15) * 4;
+    RS::col4_to(sK, t, kd, kt + kd * 64 + t);
   }
 }
 
@@ -433,7 +491,8 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(ChunkParams p) {
 struct StateRegs {
   float4 a[8];      // stage A row block: W (v_new waves) or raw Q (output waves)
   float4 at[4];     // stage C: A rows (output waves)
-  float4 kd[4];     // stage D: (K*ks)^T rows, 4 tokens each
+  float4 kd[4];     // stage D: K^T rows (raw input type), 4 tokens each
+  float4 ks;        // stage B: Ks of this lane's 4 tokens (v_new waves)
   float4 u[2];      // stage B: U^T, 4 tokens each (v_new waves)
   float qs;         // stage A: Q scale of this lane's row (output waves)
   float gle;        // e^{gcum_last}
@@ -460,7 +519,7 @@ __device__ __forceinline__ int lpt_sequence(const ChunkParams& p, int slot) {
 // wave also updates state rows 16w..16w+15.  A SIMD holds waves s and s+4, one
 // of each role.  Both roles execute the same barriers.
 template <typename TIn, bool WROLE>
-__device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, float* sVT, int h,
+__device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, float* sVT, float* sVS, int h,
                                            int n0, int t_begin, int L, int co, int wave, int lane) {
   typedef RawOf<TIn> R;
   const int li = lane & 15;
@@ -496,9 +555,10 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
       for (int u = 0; u < 4; ++u)
         g.at[u] = *reinterpret_cast<const float4*>(ws + kWsA + tok * 64 + 16 * u + 4 * lg);
     }
+    const TIn* kt = reinterpret_cast<const TIn*>(ws + kWsKT);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      g.kd[u] = *reinterpret_cast<const float4*>(ws + kWsKdT + (16 * wave + li) * 64 + 16 * u + 4 * lg);
+    for (int u = 0; u < 4; ++u) g.kd[u] = R::ld4(kt, (16 * wave + li) * 64 + 16 * u + 4 * lg);
+    if (WROLE) g.ks = *reinterpret_cast<const float4*>(ws + kWsKs + 16 * M + 4 * lg);
     g.gle = ws[kWsMisc];
   };
 
@@ -538,13 +598,17 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     }
 
-    // ---- stage B: v_new = U - W S
+    // ---- stage B: v_new = U - W S, and v_new scaled by Ks for the state
+    // update (S += K^T diag(Ks) v_new)
     if (WROLE) {
       const int tok = 16 * M + 4 * lg;
-      *reinterpret_cast<float4*>(&sVT[li * kLdVT + tok]) =
-          make_float4(cur.u[0].x - acc0[0], cur.u[0].y - acc0[1], cur.u[0].z - acc0[2], cur.u[0].w - acc0[3]);
-      *reinterpret_cast<float4*>(&sVT[(16 + li) * kLdVT + tok]) =
-          make_float4(cur.u[1].x - acc1[0], cur.u[1].y - acc1[1], cur.u[1].z - acc1[2], cur.u[1].w - acc1[3]);
+      const float4 v0 = make_float4(cur.u[0].x - acc0[0], cur.u[0].y - acc0[1], cur.u[0].z - acc0[2], cur.u[0].w - acc0[3]);
+      const float4 v1 = make_float4(cur.u[1].x - acc1[0], cur.u[1].y - acc1[1], cur.u[1].z - acc1[2], cur.u[1].w - acc1[3]);
+      const float4 ks = cur.ks;
+      *reinterpret_cast<float4*>(&sVT[li * kLdVT + tok]) = v0;
+      *reinterpret_cast<float4*>(&sVT[(16 + li) * kLdVT + tok]) = v1;
+      *reinterpret_cast<float4*>(&sVS[li * kLdVT + tok]) = make_float4(v0.x * ks.x, v0.y * ks.y, v0.z * ks.z, v0.w * ks.w);
+      *reinterpret_cast<float4*>(&sVS[(16 + li) * kLdVT + tok]) = make_float4(v1.x * ks.x, v1.y * ks.y, v1.z * ks.z, v1.w * ks.w);
     }
     __syncthreads();
 
@@ -575,19 +639,20 @@ __device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, flo
       }
     }
 
-    // ---- stage D: S <- e^{gL} S + (K*ks)^T v_new, rows 16w..16w+15
+    // ---- stage D: S <- e^{gL} S + K^T (Ks v_new), rows 16w..16w+15
     const float4 s0 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * wave + 4 * lg]);
     const float4 s1 = *reinterpret_cast<const float4*>(&sST[(16 + li) * kLdST + 16 * wave + 4 * lg]);
     f4v sacc0 = {s0.x * cur.gle, s0.y * cur.gle, s0.z * cur.gle, s0.w * cur.gle};
     f4v sacc1 = {s1.x * cur.gle, s1.y * cur.gle, s1.z * cur.gle, s1.w * cur.gle};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
-      const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
+      const float4 b0 = *reinterpret_cast<const float4*>(&sVS[li * kLdVT + 16 * u + 4 * lg]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&sVS[(16 + li) * kLdVT + 16 * u + 4 * lg]);
+      const float4 a4 = R::cvt4(cur.kd[u]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        sacc0 = mfma4(elem(cur.kd[u], e), elem(b0, e), sacc0);
-        sacc1 = mfma4(elem(cur.kd[u], e), elem(b1, e), sacc1);
+        sacc0 = mfma4(elem(a4, e), elem(b0, e), sacc0);
+        sacc1 = mfma4(elem(a4, e), elem(b1, e), sacc1);
       }
     }
     // every wave has read sST (stage A) before the barrier above and only its
@@ -619,8 +684,9 @@ __global__ __launch_bounds__(512, 1) void chunk_state_kernel(ChunkParams p) {
   // S tile and v_new stored transposed ([column][contraction index]) so one
   // ds_read_b128 feeds four consecutive MFMA steps; strides 132 and 68 keep
   // the 8-lane groups of a b128 access on distinct banks.
-  __shared__ float sST[32 * kLdST];
-  __shared__ float sVT[32 * kLdVT];
+  __shared__ __align__(16) float sST[32 * kLdST];
+  __shared__ __align__(16) float sVT[32 * kLdVT];  // v_new
+  __shared__ __align__(16) float sVS[32 * kLdVT];  // v_new scaled by Ks
 
   // Workgroup -> (column tile, head, sequence).  Groups (sequence, head) are
   // dealt longest sequence first so the longest chunk scans start earliest,
@@ -659,9 +725,9 @@ __global__ __launch_bounds__(512, 1) void chunk_state_kernel(ChunkParams p) {
   }
 
   if (wave < 4)
-    state_scan<TIn, true>(p, sST, sVT, h, n0, t_begin, L, co, wave, lane);
+    state_scan<TIn, true>(p, sST, sVT, sVS, h, n0, t_begin, L, co, wave, lane);
   else
-    state_scan<TIn, false>(p, sST, sVT, h, n0, t_begin, L, co, wave, lane);
+    state_scan<TIn, false>(p, sST, sVT, sVS, h, n0, t_begin, L, co, wave, lane);
   __syncthreads();
 
   float* out = p.state + ((size_t)seq * p.H + h) * kD * kD;

@@ -80,7 +80,7 @@ def test_reference_unit_case_with_init_and_l2(dev, oracle):
 
 @pytest.mark.parametrize("T", [1, 63, 64, 65, 104, 257])
 @pytest.mark.parametrize("l2,init,half", [(False, False, False), (True, True, False),
-                                          (False, True, True)])
+                                          (False, True, True), (True, False, True)])
 def test_single_sequence(dev, oracle, T, l2, init, half):
     from spock_amd import synth
     inp = synth.chunk_inputs(16, T, seed=T, l2=not l2)
