@@ -38,23 +38,28 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int kC = 64;
 constexpr int kD = 128;
-constexpr int kLdST = 132;  // LDS row stride of the transposed 32-column state tile
-constexpr int kLdVT = 68;   // LDS row stride of the transposed v_new tile
-// workspace record per (chunk, head), in floats.  Layouts are the ones the
-// state scan reads along its contraction index:
-//   U^T [128 value cols][64 tokens] fp32   W   [64 tokens][128 key dims] fp32
-//   A   [64 tokens][64 tokens] fp32        K^T [128 key dims][64 tokens], raw
-//                                              input type (fp16 or fp32)
-//   Qs  [64] Q scale (q_scale iq e^gcum)   Ks  [64] e^{gL - gcum} ik
+// Workspace record per (chunk, head), in floats.  The matrices are stored in
+// the state scan's MFMA fragment order: fragment f of wavefront M is 64 lanes
+// x 4 consecutive contraction-index elements, so every load of the scan reads
+// one contiguous 1 KB (fp32) or 512 B (fp16) block.  Loads whose 64 lanes
+// touch 16 separate rows (the row-major alternative) cost the vector-memory
+// pipe several times more per byte.  Lane l = 16*lg + li.
+//   W   [M 4][u 8][lane][4]   W[16M+li][16u+4lg+e]                 fp32
+//   U   [tile 8][M 4][lane][4] U[16M+4lg+e][16 tile+li]             fp32
+//   A   [M 4][J 4][lane][4]   A[16M+li][16J+4lg+e] (0 above diag)  fp32
+//   KT  [M 4][v 8][lane][4]   K[16(v%4)+4lg+e][32M+16(v/4)+li]     input type
+//   Q   [M 4][u 8][lane][4]   Q[16M+li][16u+4lg+e] (raw)            input type
+//   Qs  [64] Q scale (q_scale iq e^gcum)   Ks [64] e^{gL - gcum} ik
 //   Misc[0] e^{gL}
-constexpr int kWsUT = 0;
-constexpr int kWsW = 8192;
+constexpr int kWsW = 0;
+constexpr int kWsU = 8192;
 constexpr int kWsA = 16384;
 constexpr int kWsKT = 20480;
-constexpr int kWsQs = 28672;
-constexpr int kWsKs = 28736;
-constexpr int kWsMisc = 28800;
-constexpr int kWsStride = 28864;  // 115456 bytes, a multiple of 256
+constexpr int kWsQ = 28672;
+constexpr int kWsQs = 36864;
+constexpr int kWsKs = 36928;
+constexpr int kWsMisc = 36992;
+constexpr int kWsStride = 37056;  // 148224 bytes, a multiple of 256
 // Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
 // which untyped loads/stores need for the num_records range check to apply.
 constexpr int kBufDword3 = 0x00020000;
@@ -162,6 +167,9 @@ template <> struct RowStage<uint16_t> {
                        spk::h2f((uint16_t)(u.y & 0xffffu)), spk::h2f((uint16_t)(u.y >> 16)));
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return spk::h2f(s[r * kLd + c]); }
+  static __device__ __forceinline__ void store_raw4(T* dst, const float4& raw) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(__float_as_uint(raw.x), __float_as_uint(raw.y));
+  }
   // rows r..r+3 of column c, stored as 4 consecutive elements at dst
   static __device__ __forceinline__ void col4_to(const T* s, int r, int c, T* dst) {
     const uint32_t a = s[r * kLd + c], b = s[(r + 1) * kLd + c];
@@ -179,6 +187,9 @@ template <> struct RowStage<float> {
     return *reinterpret_cast<const float4*>(s + r * kLd + c);
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return s[r * kLd + c]; }
+  static __device__ __forceinline__ void store_raw4(T* dst, const float4& raw) {
+    *reinterpret_cast<float4*>(dst) = raw;
+  }
   static __device__ __forceinline__ void col4_to(const T* s, int r, int c, T* dst) {
     *reinterpret_cast<float4*>(dst) =
         make_float4(s[r * kLd + c], s[(r + 1) * kLd + c], s[(r + 2) * kLd + c], s[(r + 3) * kLd + c]);
@@ -196,9 +207,11 @@ __device__ __forceinline__ int offblk(int I, int J) { return ((I - 1) * I / 2 + 
 constexpr float kLog2e = 1.44269504f;
 
 // The five Gram tiles of wavefront W: K K^T row block 3-W (tiles J = 0..3-W)
-// and Q K^T row block W (tiles J = 0..W), accumulated together so that the
-// MFMA stream carries five independent chains.  The K rows of block J are the
-// B operand of both products and are read once.
+// and (Q K^T)^T = K Q^T for query block W (tiles J = 0..W), accumulated
+// together so that the MFMA stream carries five independent chains.  The K
+// rows of block J are read once for both products.  A is produced transposed
+// so that each lane holds four consecutive key positions of one query row:
+// the A-operand fragment of the state scan.
 template <typename TIn, int W>
 __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, const float4 (&qa)[8],
                                            int li, int lg, f4v (&acc)[5]) {
@@ -220,18 +233,19 @@ __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, 
       for (int t = 0; t < 5; ++t) {
         const bool isq = t > Ik;
         const int J = isq ? t - Ik - 1 : t;
-        float4 a;
-        if (isq) a = qf;
-        else a = kb[Ik];
-        acc[t] = mfma4(elem(a, e), elem(kb[J], e), acc[t]);
+        if (isq)
+          acc[t] = mfma4(elem(kb[J], e), elem(qf, e), acc[t]);
+        else
+          acc[t] = mfma4(elem(kb[Ik], e), elem(kb[J], e), acc[t]);
       }
     }
   }
 }
 
 // Epilogue of the Gram tiles: L = strict_lower(beta_i k_i.k_j Gamma_ij) into
-// LDS, A = lower(q_i.k_j scale Gamma_ij) into the workspace (with the inverse
-// L2 norms when requested; 1 otherwise).
+// LDS, A = lower(q_i.k_j scale Gamma_ij) into the workspace in fragment order
+// (with the inverse L2 norms when requested; 1 otherwise).  iq_scale is the
+// scale of query row 16W + li.
 template <int W>
 __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG, const float* sB,
                                            const float* sIK, float iq_scale, float* sL, float* ws,
@@ -240,26 +254,33 @@ __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG,
 #pragma unroll
   for (int t = 0; t < 5; ++t) {
     const bool isq = t > Ik;
-    const int I = isq ? W : Ik;
     const int J = isq ? t - Ik - 1 : t;
-    const int j = 16 * J + li;
-    const float ikj = sIK[j];
+    if (!isq) {
+      const int j = 16 * J + li;
+      const float ikj = sIK[j];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * I + 4 * lg + r;
-      const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
-      if (!isq) {
-        sL[blk(I, J) + (4 * lg + r) * 16 + li] = (j < i) ? sB[i] * (acc[t][r] * (sIK[i] * ikj)) * dec : 0.0f;
-      } else {
-        // iq of row i lives in lane (i - 16W) of this wavefront
-        const float iq = __shfl(iq_scale, 4 * lg + r);
-        ws[kWsA + i * 64 + j] = (j <= i) ? (acc[t][r] * (iq * ikj)) * dec : 0.0f;
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * Ik + 4 * lg + r;
+        const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
+        sL[blk(Ik, J) + (4 * lg + r) * 16 + li] = (j < i) ? sB[i] * (acc[t][r] * (sIK[i] * ikj)) * dec : 0.0f;
       }
+    } else {
+      // lane (li, lg) holds A[i][j], i = 16W + li, j = 16J + 4lg + r
+      const int i = 16 * W + li;
+      float o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * J + 4 * lg + r;
+        const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
+        o[r] = (j <= i) ? (acc[t][r] * (iq_scale * sIK[j])) * dec : 0.0f;
+      }
+      *reinterpret_cast<float4*>(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4) = make_float4(o[0], o[1], o[2], o[3]);
     }
   }
-  // strictly-upper blocks of this wavefront's A row block are zero
-  for (int e = lane; e < (3 - W) * 256; e += 64)
-    ws[kWsA + (16 * W + (e >> 4) % 16) * 64 + 16 * (W + 1) + (e >> 8) * 16 + (e & 15)] = 0.0f;
+  // blocks above the diagonal of this query block are zero
+#pragma unroll
+  for (int J = W + 1; J < 4; ++J)
+    *reinterpret_cast<float4*>(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 // fp16 inputs: 3 workgroups per CU (50 KB of LDS each), so at most 168 VGPRs;
@@ -340,6 +361,13 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
     RS::put4(sV, r, c4, vx);
   }
   __syncthreads();
+
+  // ---- raw Q rows of block `wave` in the scan's fragment order
+  {
+    typename RS::T* qf = reinterpret_cast<typename RS::T*>(ws + kWsQ);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) RS::store_raw4(qf + ((wave * 8 + u) * 64 + lane) * 4, qa[u]);
+  }
 
   // ---- inverse L2 norms (eps inside the sqrt, deltanet_chunk.cpp:27-39):
   // K rows from LDS, 4 threads per row; Q rows from this lane's registers
@@ -438,9 +466,11 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
     __syncthreads();
   }
 
-  // ---- U = T diag(beta) V (stored as U^T) and W = T diag(beta e^g ik) K, row
-  // blocks I = 0..3 of two 16-column tiles per wavefront accumulated together;
-  // the per-token factors are applied to the B operand as it is read
+  // ---- U = T diag(beta) V and W^T = K^T diag(beta e^g ik) T^T, row blocks
+  // I = 0..3 of two 16-column tiles per wavefront accumulated together; the
+  // per-token factors are applied to the V / K operand as it is read.  W is
+  // produced transposed so that each lane holds four consecutive key dims of
+  // one token: the A-operand fragment of the state scan.
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
     const int n = 16 * (2 * wave + jj) + li;
@@ -465,38 +495,32 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           au[I] = mfma4(elem(a4, s), vb[s], au[I]);
-          aw[I] = mfma4(elem(a4, s), kb[s], aw[I]);
+          aw[I] = mfma4(kb[s], elem(a4, s), aw[I]);
         }
       }
     }
+    // U: lane (li, lg) holds U[16I+4lg+r][n]; W^T: W[16I+li][16(2w+jj)+4lg+r]
+    const int ct = 2 * wave + jj;
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      *reinterpret_cast<float4*>(ws + kWsUT + n * 64 + 16 * I + 4 * lg) = make_float4(au[I][0], au[I][1], au[I][2], au[I][3]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ws[kWsW + (16 * I + 4 * lg + r) * kD + n] = aw[I][r];
+      *reinterpret_cast<float4*>(ws + kWsU + ((ct * 4 + I) * 64 + lane) * 4) = make_float4(au[I][0], au[I][1], au[I][2], au[I][3]);
+      *reinterpret_cast<float4*>(ws + kWsW + ((I * 8 + ct) * 64 + lane) * 4) = make_float4(aw[I][0], aw[I][1], aw[I][2], aw[I][3]);
     }
     __builtin_amdgcn_sched_barrier(0);  // one column tile's operands live at a time
   }
 
-  // ---- K^T [128 key dims][64 tokens], raw input type, 16 lanes per row
+  // ---- K^T fragments of the state update, raw input type: fragment
+  // f = 64 v + l of wavefront M holds K[16(v%4)+4lg .. +3][32M+16(v/4)+li]
   typename RS::T* kt = reinterpret_cast<typename RS::T*>(ws + kWsKT);
-  for (int i = tid; i < 128 * 16; i += 256) {
-    const int kd = i >> 4;
-    const int t = (i & 15) * 4;
-    RS::col4_to(sK, t, kd, kt + kd * 64 + t);
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int f = tid + 256 * it;  // [M][v][lane]
+    const int l = f & 63;
+    const int v8 = (f >> 6) & 7;
+    const int Mw = f >> 9;
+    RS::col4_to(sK, 16 * (v8 & 3) + 4 * (l >> 4), 32 * Mw + 16 * (v8 >> 2) + (l & 15), kt + f * 4);
   }
 }
-
-// One wavefront's operands of one chunk, loaded a chunk ahead.
-struct StateRegs {
-  float4 a[8];      // stage A row block: W (v_new waves) or raw Q (output waves)
-  float4 at[4];     // stage C: A rows (output waves)
-  float4 kd[4];     // stage D: K^T rows (raw input type), 4 tokens each
-  float4 ks;        // stage B: Ks of this lane's 4 tokens (v_new waves)
-  float4 u[2];      // stage B: U^T, 4 tokens each (v_new waves)
-  float qs;         // stage A: Q scale of this lane's row (output waves)
-  float gle;        // e^{gcum_last}
-};
 
 // Sequence with rank `slot` by decreasing length (ties: lower index first).
 __device__ __forceinline__ int lpt_sequence(const ChunkParams& p, int slot) {
@@ -513,202 +537,67 @@ __device__ __forceinline__ int lpt_sequence(const ChunkParams& p, int slot) {
   return slot;
 }
 
-// Sequential chunk scan of one workgroup (8 wavefronts, two per SIMD) for one
-// wavefront role.  WROLE (waves 0-3): v_new = U - W S for token block w.
-// Output role (waves 4-7): o = Q*qs S + A v_new for token block w-4.  Every
-// wave also updates state rows 16w..16w+15.  A SIMD holds waves s and s+4, one
-// of each role.  Both roles execute the same barriers.
-template <typename TIn, bool WROLE>
-__device__ __forceinline__ void state_scan(const ChunkParams& p, float* sST, float* sVT, float* sVS, int h,
-                                           int n0, int t_begin, int L, int co, int wave, int lane) {
-  typedef RawOf<TIn> R;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const int M = WROLE ? wave : wave - 4;  // token block of stages A-C
-  const TIn* q = static_cast<const TIn*>(p.q);
-  const int nchunks = (L + kC - 1) / kC;
+constexpr int kTiles = 8;   // 16-column tiles of the value dim per (sequence, head)
+constexpr int kLdST = 132;  // LDS row stride of the transposed state tile (floats)
+constexpr int kLdVT = 68;   // LDS row stride of the transposed v_new tile (floats)
 
-  // Issue every global load of chunk c for this lane; padding rows are read
-  // from row 0 (always valid) and zeroed at use, so there is no branch.
-  auto load = [&](StateRegs& g, int c) {
-    const int tok0 = t_begin + c * kC;
-    const int len = min(kC, L - c * kC);
-    const float* ws = p.ws + ((size_t)(co + c) * p.H + h) * kWsStride;
-    const int tok = 16 * M + li;
-    if (WROLE) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        g.a[u] = *reinterpret_cast<const float4*>(ws + kWsW + tok * kD + 16 * u + 4 * lg);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-        g.u[nt] = *reinterpret_cast<const float4*>(ws + kWsUT + (n0 + 16 * nt + li) * 64 + 16 * M + 4 * lg);
-    } else {
-      const int row = tok < len ? tok : 0;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        g.a[u] = R::ld4(q, ((size_t)h * p.N + tok0 + row) * kD + 16 * u + 4 * lg);
-      g.qs = ws[kWsQs + tok];
-      // all four blocks, the zero upper ones included: no load sits under a
-      // branch, so the compiler's vmcnt bookkeeping stays exact and the
-      // prefetch of the next chunk is never waited for early
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        g.at[u] = *reinterpret_cast<const float4*>(ws + kWsA + tok * 64 + 16 * u + 4 * lg);
-    }
-    const TIn* kt = reinterpret_cast<const TIn*>(ws + kWsKT);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) g.kd[u] = R::ld4(kt, (16 * wave + li) * 64 + 16 * u + 4 * lg);
-    if (WROLE) g.ks = *reinterpret_cast<const float4*>(ws + kWsKs + 16 * M + 4 * lg);
-    g.gle = ws[kWsMisc];
-  };
+// Operands of one chunk for stage A and for stages B-D (both prefetched a
+// chunk ahead).
+struct ScanEarly {
+  float4 w[8];  // W rows: token 16M+li, key dims 16u+4lg..+3
+  float4 q[8];  // raw Q rows, same map
+  float qs;     // Q scale of this lane's row
+};
+struct ScanLate {
+  float4 a[4];   // A rows: token 16M+li, tokens 16u+4lg..+3
+  float4 kt[8];  // raw K^T rows 32M+16(v/4)+li, tokens 16(v%4)+4lg..+3
+  float4 u;      // U^T: column n0+li, tokens 16M+4lg..+3
+  float4 ks;     // Ks of tokens 16M+4lg..+3
+  float gle;     // e^{gL}
+};
 
-  // One chunk step from the operands in `cur`.
-  auto step = [&](const StateRegs& cur, int c) {
-    const int tok0 = t_begin + c * kC;
-    const int len = min(kC, L - c * kC);
-
-    // ---- stage A: row block M of [W ; Q*qs] times S
-    f4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    const float qsc = (16 * M + li) < len ? cur.qs : 0.0f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      float4 av;
-      if (WROLE) {
-        av = cur.a[u];
-      } else {
-        const float4 x = R::cvt4(cur.a[u]);
-        av = make_float4(x.x * qsc, x.y * qsc, x.z * qsc, x.w * qsc);
-      }
-      const float4 b0 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * u + 4 * lg]);
-      const float4 b1 = *reinterpret_cast<const float4*>(&sST[(16 + li) * kLdST + 16 * u + 4 * lg]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc0 = mfma4(elem(av, e), elem(b0, e), acc0);
-        acc1 = mfma4(elem(av, e), elem(b1, e), acc1);
-      }
-    }
-    // The next chunk's loads (issued just before this stage, same scheduling
-    // region) are spread over the MFMA stream, two after every eight MFMAs:
-    // issued as one burst by all eight wavefronts they queue in the CU's
-    // vector-memory pipe and stall the issuing wavefront for thousands of
-    // cycles.  (sched_group_barrier masks: 0x020 VMEM read, 0x008 MFMA.)
-#pragma unroll
-    for (int i = 0; i < 9; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    }
-
-    // ---- stage B: v_new = U - W S, and v_new scaled by Ks for the state
-    // update (S += K^T diag(Ks) v_new)
-    if (WROLE) {
-      const int tok = 16 * M + 4 * lg;
-      const float4 v0 = make_float4(cur.u[0].x - acc0[0], cur.u[0].y - acc0[1], cur.u[0].z - acc0[2], cur.u[0].w - acc0[3]);
-      const float4 v1 = make_float4(cur.u[1].x - acc1[0], cur.u[1].y - acc1[1], cur.u[1].z - acc1[2], cur.u[1].w - acc1[3]);
-      const float4 ks = cur.ks;
-      *reinterpret_cast<float4*>(&sVT[li * kLdVT + tok]) = v0;
-      *reinterpret_cast<float4*>(&sVT[(16 + li) * kLdVT + tok]) = v1;
-      *reinterpret_cast<float4*>(&sVS[li * kLdVT + tok]) = make_float4(v0.x * ks.x, v0.y * ks.y, v0.z * ks.z, v0.w * ks.w);
-      *reinterpret_cast<float4*>(&sVS[(16 + li) * kLdVT + tok]) = make_float4(v1.x * ks.x, v1.y * ks.y, v1.z * ks.z, v1.w * ks.w);
-    }
-    __syncthreads();
-
-    // ---- stage C: o = Q*qs S + A v_new (the blocks above the diagonal of A
-    // are zero, so all four are taken: the SIMD's critical path is the
-    // M = 3 wave's either way)
-    if (!WROLE) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float4 b0 = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
-        const float4 b1 = *reinterpret_cast<const float4*>(&sVT[(16 + li) * kLdVT + 16 * u + 4 * lg]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc0 = mfma4(elem(cur.at[u], e), elem(b0, e), acc0);
-          acc1 = mfma4(elem(cur.at[u], e), elem(b1, e), acc1);
-        }
-      }
-      // rows tok0 .. tok0+len-1 of this head through a buffer resource of
-      // len rows: the hardware drops the padding rows' stores (offset past
-      // num_records), with no branch around the stores
-      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
-          p.core + ((size_t)h * p.core_hs + tok0) * kD, 0, len * kD * (int)sizeof(float), kBufDword3);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int off = ((16 * M + 4 * lg + r) * kD + n0 + li) * (int)sizeof(float);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc0[r]), out, off, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc1[r]), out, off + 64, 0, 0);
-      }
-    }
-
-    // ---- stage D: S <- e^{gL} S + K^T (Ks v_new), rows 16w..16w+15
-    const float4 s0 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * wave + 4 * lg]);
-    const float4 s1 = *reinterpret_cast<const float4*>(&sST[(16 + li) * kLdST + 16 * wave + 4 * lg]);
-    f4v sacc0 = {s0.x * cur.gle, s0.y * cur.gle, s0.z * cur.gle, s0.w * cur.gle};
-    f4v sacc1 = {s1.x * cur.gle, s1.y * cur.gle, s1.z * cur.gle, s1.w * cur.gle};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float4 b0 = *reinterpret_cast<const float4*>(&sVS[li * kLdVT + 16 * u + 4 * lg]);
-      const float4 b1 = *reinterpret_cast<const float4*>(&sVS[(16 + li) * kLdVT + 16 * u + 4 * lg]);
-      const float4 a4 = R::cvt4(cur.kd[u]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sacc0 = mfma4(elem(a4, e), elem(b0, e), sacc0);
-        sacc1 = mfma4(elem(a4, e), elem(b1, e), sacc1);
-      }
-    }
-    // every wave has read sST (stage A) before the barrier above and only its
-    // own rows here, so the rows can be replaced in place
-    *reinterpret_cast<float4*>(&sST[li * kLdST + 16 * wave + 4 * lg]) =
-        make_float4(sacc0[0], sacc0[1], sacc0[2], sacc0[3]);
-    *reinterpret_cast<float4*>(&sST[(16 + li) * kLdST + 16 * wave + 4 * lg]) =
-        make_float4(sacc1[0], sacc1[1], sacc1[2], sacc1[3]);
-    __syncthreads();
-  };
-
-  // Two register sets used alternately: the loads of chunk c+1 are in flight
-  // while chunk c computes.  The prefetch index is clamped (the last chunk is
-  // fetched twice) rather than guarded, for the same reason as above.
-  StateRegs ra, rb;
-  if (nchunks > 0) load(ra, 0);
-  __syncthreads();
-  for (int c = 0; c < nchunks; c += 2) {
-    load(rb, min(c + 1, nchunks - 1));
-    step(ra, c);
-    if (c + 1 >= nchunks) break;
-    load(ra, min(c + 2, nchunks - 1));
-    step(rb, c + 1);
-  }
-}
-
+// Sequential chunk scan over one 128x16 state tile: one workgroup of 4
+// wavefronts per (sequence, head, 16-column tile), so a 16-head batch of 8
+// sequences gives 1024 workgroups and two run on each CU (independent
+// barriers: one workgroup's waits are the other's issue slots).  Wavefront M:
+//   A  v_new rows and output rows of token block M: W_M S and (Q_M qs) S
+//   B  v_new = U - W S  -> LDS, also scaled by Ks
+//   C  o = (Q qs) S + A v_new -> core
+//   D  S rows 32M..32M+31 <- e^{gL} S + K^T diag(Ks) v_new
+// 112 MFMA per wavefront per chunk.
 template <typename TIn>
-__global__ __launch_bounds__(512, 1) void chunk_state_kernel(ChunkParams p) {
+__global__ __launch_bounds__(256, 2) void chunk_state_kernel(ChunkParams p) {
+  typedef RawOf<TIn> R;
   // S tile and v_new stored transposed ([column][contraction index]) so one
   // ds_read_b128 feeds four consecutive MFMA steps; strides 132 and 68 keep
   // the 8-lane groups of a b128 access on distinct banks.
-  __shared__ __align__(16) float sST[32 * kLdST];
-  __shared__ __align__(16) float sVT[32 * kLdVT];  // v_new
-  __shared__ __align__(16) float sVS[32 * kLdVT];  // v_new scaled by Ks
+  __shared__ __align__(16) float sST[16 * kLdST];
+  __shared__ __align__(16) float sVT[16 * kLdVT];  // v_new
+  __shared__ __align__(16) float sVS[16 * kLdVT];  // v_new scaled by Ks
 
-  // Workgroup -> (column tile, head, sequence).  Groups (sequence, head) are
-  // dealt longest sequence first so the longest chunk scans start earliest,
-  // and the four column tiles of a group get workgroup ids congruent mod 8 --
-  // the same XCD (ids are dealt to the 8 XCDs round-robin) -- so they share
-  // one L2 for W, Q, K and A.
+  // Workgroup -> (tile, head, sequence).  Groups (sequence, head) are dealt
+  // longest sequence first so the longest chunk scans start earliest, and the
+  // eight tiles of a group get workgroup ids congruent mod 8 -- the same XCD
+  // (ids are dealt to the 8 XCDs round-robin) -- so they share one L2 for W,
+  // Q, A and K^T.
   const int b = blockIdx.x;
   const int groups = p.S * p.H;
   int gi, tile;
   if ((groups & 7) == 0) {
-    gi = (b >> 5) * 8 + (b & 7);
-    tile = (b >> 3) & 3;
+    gi = (b >> 6) * 8 + (b & 7);
+    tile = (b >> 3) & 7;
   } else {
-    gi = b >> 2;
-    tile = b & 3;
+    gi = b >> 3;
+    tile = b & 7;
   }
   const int h = gi % p.H;
   const int seq = lpt_sequence(p, gi / p.H);
-  const int n0 = tile * 32;
+  const int n0 = tile * 16;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int M = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int li = lane & 15;
+  const int lg = lane >> 4;
 
   int t_begin = 0, L = p.N, co = 0;
   if (p.cu) {
@@ -716,25 +605,152 @@ __global__ __launch_bounds__(512, 1) void chunk_state_kernel(ChunkParams p) {
     L = p.cu[seq + 1] - t_begin;
     for (int s = 0; s < seq; ++s) co += (p.cu[s + 1] - p.cu[s] + kC - 1) / kC;
   }
+  const int nchunks = (L + kC - 1) / kC;
 
   const float* init = p.init ? p.init + ((size_t)seq * p.H + h) * kD * kD : nullptr;
-  for (int i = tid; i < 128 * 32; i += 512) {
-    const int r = i >> 5;
-    const int c = i & 31;
+  for (int i = tid; i < 128 * 16; i += 256) {
+    const int r = i >> 4;
+    const int c = i & 15;
     sST[c * kLdST + r] = init ? init[r * kD + n0 + c] : 0.0f;
   }
 
-  if (wave < 4)
-    state_scan<TIn, true>(p, sST, sVT, sVS, h, n0, t_begin, L, co, wave, lane);
-  else
-    state_scan<TIn, false>(p, sST, sVT, sVS, h, n0, t_begin, L, co, wave, lane);
-  __syncthreads();
+  // Every load is unconditional (the intra kernel's padding Q rows are row 0
+  // of the chunk, zeroed here through qs; the last chunk is prefetched again
+  // rather than guarded), so the compiler's vmcnt bookkeeping stays exact.
+  // Each load instruction reads one contiguous fragment.
+  auto record = [&](int c) { return p.ws + ((size_t)(co + c) * p.H + h) * kWsStride; };
+  auto load_early = [&](ScanEarly& e, int c) {
+    const float* ws = record(c);
+    const TIn* qf = reinterpret_cast<const TIn*>(ws + kWsQ);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      e.w[u] = *reinterpret_cast<const float4*>(ws + kWsW + ((M * 8 + u) * 64 + lane) * 4);
+      e.q[u] = R::ld4(qf, ((M * 8 + u) * 64 + lane) * 4);
+    }
+    e.qs = ws[kWsQs + 16 * M + li];
+  };
+  auto load_late = [&](ScanLate& l, int c) {
+    const float* ws = record(c);
+    const TIn* kt = reinterpret_cast<const TIn*>(ws + kWsKT);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      l.a[u] = *reinterpret_cast<const float4*>(ws + kWsA + ((M * 4 + u) * 64 + lane) * 4);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) l.kt[u] = R::ld4(kt, ((M * 8 + u) * 64 + lane) * 4);
+    l.u = *reinterpret_cast<const float4*>(ws + kWsU + ((tile * 4 + M) * 64 + lane) * 4);
+    l.ks = *reinterpret_cast<const float4*>(ws + kWsKs + 16 * M + 4 * lg);
+    l.gle = ws[kWsMisc];
+  };
 
-  float* out = p.state + ((size_t)seq * p.H + h) * kD * kD;
-  for (int i = tid; i < 128 * 32; i += 512) {
-    const int r = i >> 5;
-    const int c = i & 31;
-    out[r * kD + n0 + c] = sST[c * kLdST + r];
+  auto step = [&](const ScanEarly& e, const ScanLate& l, int c) {
+    const int tok0 = t_begin + c * kC;
+    const int len = min(kC, L - c * kC);
+
+    // ---- stage A: W_M S and (Q_M qs) S share the B operand (S)
+    f4v aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+    const float qsc = (16 * M + li) < len ? e.qs : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float4 x = R::cvt4(e.q[u]);
+      const float4 qv = make_float4(x.x * qsc, x.y * qsc, x.z * qsc, x.w * qsc);
+      const float4 sb = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * u + 4 * lg]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        aw = mfma4(elem(e.w[u], k), elem(sb, k), aw);
+        aq = mfma4(elem(qv, k), elem(sb, k), aq);
+      }
+    }
+    // The loads issued just before this stage (same scheduling region) are
+    // spread over the MFMA stream rather than issued as one burst, which
+    // would queue in the CU's vector-memory pipe behind the other
+    // wavefronts' bursts.  (sched_group_barrier masks: 0x020 VMEM read,
+    // 0x008 MFMA.)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+
+    // ---- stage B: v_new = U - W S, and v_new scaled by Ks for the update
+    {
+      const float4 v = make_float4(l.u.x - aw[0], l.u.y - aw[1], l.u.z - aw[2], l.u.w - aw[3]);
+      const int tok = 16 * M + 4 * lg;
+      *reinterpret_cast<float4*>(&sVT[li * kLdVT + tok]) = v;
+      *reinterpret_cast<float4*>(&sVS[li * kLdVT + tok]) =
+          make_float4(v.x * l.ks.x, v.y * l.ks.y, v.z * l.ks.z, v.w * l.ks.w);
+    }
+    __syncthreads();
+
+    // ---- stage C: o = (Q qs) S + A v_new (all four blocks of A's row block;
+    // the ones above the diagonal are zero)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float4 vb = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) aq = mfma4(elem(l.a[u], k), elem(vb, k), aq);
+    }
+    // rows tok0 .. tok0+len-1 of this head through a buffer resource of len
+    // rows: the hardware drops the padding rows' stores (offset past
+    // num_records), with no branch around the stores
+    const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+        p.core + ((size_t)h * p.core_hs + tok0) * kD, 0, len * kD * (int)sizeof(float), kBufDword3);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(aq[r]), out,
+                                            ((16 * M + 4 * lg + r) * kD + n0 + li) * (int)sizeof(float), 0, 0);
+
+    // ---- stage D: S rows 32M+16j.. <- e^{gL} S + K^T (Ks v_new), j = 0, 1
+    f4v s0, s1;
+    {
+      const float4 x0 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 32 * M + 4 * lg]);
+      const float4 x1 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 32 * M + 16 + 4 * lg]);
+      s0 = f4v{x0.x * l.gle, x0.y * l.gle, x0.z * l.gle, x0.w * l.gle};
+      s1 = f4v{x1.x * l.gle, x1.y * l.gle, x1.z * l.gle, x1.w * l.gle};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float4 vb = *reinterpret_cast<const float4*>(&sVS[li * kLdVT + 16 * u + 4 * lg]);
+      const float4 k0 = R::cvt4(l.kt[u]);
+      const float4 k1 = R::cvt4(l.kt[4 + u]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        s0 = mfma4(elem(k0, k), elem(vb, k), s0);
+        s1 = mfma4(elem(k1, k), elem(vb, k), s1);
+      }
+    }
+    // every wave read sST (stage A) before the barrier above and only its own
+    // rows here, so the rows are replaced in place
+    *reinterpret_cast<float4*>(&sST[li * kLdST + 32 * M + 4 * lg]) = make_float4(s0[0], s0[1], s0[2], s0[3]);
+    *reinterpret_cast<float4*>(&sST[li * kLdST + 32 * M + 16 + 4 * lg]) = make_float4(s1[0], s1[1], s1[2], s1[3]);
+    __syncthreads();
+  };
+
+  // Two operand sets used alternately: the loads of chunk c+1 are in flight
+  // while chunk c computes.
+  ScanEarly ea, eb;
+  ScanLate la, lb;
+  if (nchunks > 0) {
+    load_early(ea, 0);
+    load_late(la, 0);
+  }
+  __syncthreads();
+  for (int c = 0; c < nchunks; c += 2) {
+    const int c1 = min(c + 1, nchunks - 1);
+    load_late(lb, c1);
+    load_early(eb, c1);
+    step(ea, la, c);
+    if (c + 1 >= nchunks) break;
+    const int c2 = min(c + 2, nchunks - 1);
+    load_late(la, c2);
+    load_early(ea, c2);
+    step(eb, lb, c + 1);
+  }
+
+  float* outs = p.state + ((size_t)seq * p.H + h) * kD * kD;
+  for (int i = tid; i < 128 * 16; i += 256) {
+    const int r = i >> 4;
+    const int c = i & 15;
+    outs[r * kD + n0 + c] = sST[c * kLdST + r];
   }
 }
 
@@ -838,11 +854,11 @@ extern "C" int spk_chunk_prefill(const SpkChunkArgs* a, spk_stream_t stream) {
     const int rc = spk::check_launch("spk_chunk_prefill (intra)");
     if (rc) return rc;
   }
-  dim3 g2((unsigned)(4 * p.H * S));
+  dim3 g2((unsigned)(kTiles * p.H * S));
   if (a->input_dtype == SPK_F32)
-    hipLaunchKernelGGL(chunk_state_kernel<float>, g2, dim3(512), 0, s, p);
+    hipLaunchKernelGGL(chunk_state_kernel<float>, g2, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(chunk_state_kernel<uint16_t>, g2, dim3(512), 0, s, p);
+    hipLaunchKernelGGL(chunk_state_kernel<uint16_t>, g2, dim3(256), 0, s, p);
   return spk::check_launch("spk_chunk_prefill (state)");
 }
 
