@@ -24,6 +24,10 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Decode-sized matrices (a few MB) are read with plain (cached) 16-byte
+// loads: non-temporal loads measured up to 2x slower there on MI355X.  The
+// 0.5 GB lm_head stream is the opposite case and keeps non-temporal loads.
+__device__ __forceinline__ uint4 ld_w(const uint4* p) { return *p; }
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -92,7 +96,7 @@ __device__ __forceinline__ void unpack8(const uint4& u, float* f) {
 
 // Dot products of R rows (row0..row0+R-1, clipped to out_dim) with x; lane 0
 // of the wave returns the fp32 sums.
-template <int N8, int R>
+template <int N8, int R, bool STREAM = false>
 __device__ __forceinline__ void rows_dot(const uint16_t* __restrict__ W, int in_dim, int row0,
                                          int out_dim, const float* xf, int lane, float* sums) {
   uint4 wv[R][N8];
@@ -102,7 +106,7 @@ __device__ __forceinline__ void rows_dot(const uint16_t* __restrict__ W, int in_
     if (row < out_dim) {
       const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
 #pragma unroll
-      for (int k = 0; k < N8; ++k) wv[r][k] = ld_stream(src + k);
+      for (int k = 0; k < N8; ++k) wv[r][k] = STREAM ? ld_stream(src + k) : ld_w(src + k);
     } else {
 #pragma unroll
       for (int k = 0; k < N8; ++k) wv[r][k] = make_uint4(0, 0, 0, 0);
@@ -177,7 +181,7 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const uint16_t* __restrict
   load_x<N8>(x, lane, xf);
   const int row0 = (blockIdx.x * 4 + wave) * R;
   float sums[R];
-  rows_dot<N8, R>(W, 512 * N8, row0, vocab, xf, lane, sums);
+  rows_dot<N8, R, true>(W, 512 * N8, row0, vocab, xf, lane, sums);
   unsigned long long key = 0ull;
   if (lane == 0) {
 #pragma unroll
@@ -213,12 +217,13 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
 }
 
 // Several GEMVs in one launch: workgroup ranges are assigned to descriptors by
-// prefix sums; each workgroup runs 4 wavefronts x kBatchRows rows of one
+// prefix sums; each workgroup runs 4 wavefronts x batch_rows(n8) rows of one
 // descriptor with the same per-row order as gemv_kernel (bit-identical
-// results), the row span per lane (in_dim / 64, a multiple of 8 halves) being
-// a runtime count of 16-byte loads.
+// results).  A wavefront issues all of its weight loads (batch_rows rows x
+// n8 16-byte loads per lane) before it reads x; one or two rows per
+// wavefront (many workgroups) measured fastest for decode-sized projections.
 constexpr int kMaxBatch = 8;
-constexpr int kBatchRows = 2;
+__host__ __device__ constexpr int batch_rows(int n8) { return n8 <= 2 ? 2 : 1; }
 struct GemvBatch {
   const uint16_t* W[kMaxBatch];
   const uint16_t* x[kMaxBatch];
@@ -229,6 +234,38 @@ struct GemvBatch {
   int count;
 };
 
+template <int N8>
+__device__ __forceinline__ void batched_rows(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
+                                             uint16_t* __restrict__ y, int out_dim, int blk, int wave,
+                                             int lane) {
+  constexpr int R = batch_rows(N8);
+  constexpr int in_dim = 512 * N8;
+  const int row0 = (blk * 4 + wave) * R;
+  uint4 wv[R][N8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r < out_dim ? row0 + r : out_dim - 1;
+    const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
+#pragma unroll
+    for (int k = 0; k < N8; ++k) wv[r][k] = ld_w(src + k);
+  }
+  float xf[8 * N8];
+  load_x<N8>(x, lane, xf);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N8; ++k) {
+      float wf[8];
+      unpack8(wv[r][k], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
+    }
+    acc = spk::tree64_to_lane0(acc);
+    if (lane == 0 && row0 + r < out_dim) y[row0 + r] = spk::f2h(acc);
+  }
+}
+
 __global__ __launch_bounds__(256) void gemv_batched_kernel(GemvBatch b) {
   int d = 0;
 #pragma unroll
@@ -236,41 +273,19 @@ __global__ __launch_bounds__(256) void gemv_batched_kernel(GemvBatch b) {
     if (i < b.count && (int)blockIdx.x >= b.first_block[i]) d = i;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int n8 = b.n8[d];
-  const int in_dim = 512 * n8;
-  const int out_dim = b.out_dim[d];
-  const uint16_t* __restrict__ W = b.W[d];
-  float xf[64];
-  {
-    const uint4* src = reinterpret_cast<const uint4*>(b.x[d] + lane * (8 * n8));
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k < n8) unpack8(src[k], xf + 8 * k);
-  }
-  const int row0 = (((int)blockIdx.x - b.first_block[d]) * 4 + wave) * kBatchRows;
-  uint4 wv[kBatchRows][8];
-#pragma unroll
-  for (int r = 0; r < kBatchRows; ++r) {
-    const int row = row0 + r < out_dim ? row0 + r : out_dim - 1;
-    const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * n8));
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k < n8) wv[r][k] = ld_stream(src + k);
-  }
-#pragma unroll
-  for (int r = 0; r < kBatchRows; ++r) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (k < n8) {
-        float wf[8];
-        unpack8(wv[r][k], wf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
-      }
-    }
-    acc = spk::tree64_to_lane0(acc);
-    if (lane == 0 && row0 + r < out_dim) b.y[d][row0 + r] = spk::f2h(acc);
+  const int blk = (int)blockIdx.x - b.first_block[d];
+  switch (b.n8[d]) {
+#define SPK_BATCH_CASE(n8) \
+  case n8: batched_rows<n8>(b.W[d], b.x[d], b.y[d], b.out_dim[d], blk, wave, lane); break;
+    SPK_BATCH_CASE(1)
+    SPK_BATCH_CASE(2)
+    SPK_BATCH_CASE(3)
+    SPK_BATCH_CASE(4)
+    SPK_BATCH_CASE(5)
+    SPK_BATCH_CASE(6)
+    SPK_BATCH_CASE(7)
+    default: batched_rows<8>(b.W[d], b.x[d], b.y[d], b.out_dim[d], blk, wave, lane); break;
+#undef SPK_BATCH_CASE
   }
 }
 
@@ -365,7 +380,8 @@ extern "C" int spk_matvec_f16_batched(const SpkMatvecDesc* d, int32_t count, spk
     b.out_dim[b.count] = d[i].out_dim;
     b.n8[b.count] = d[i].in_dim / 512;
     b.first_block[b.count] = blocks;
-    blocks += (d[i].out_dim + 4 * kBatchRows - 1) / (4 * kBatchRows);
+    const int rows_per_block = 4 * batch_rows(d[i].in_dim / 512);
+    blocks += (d[i].out_dim + rows_per_block - 1) / rows_per_block;
     if (++b.count == kMaxBatch) {
       const int rc = flush();
       if (rc) return rc;
