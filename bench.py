@@ -352,7 +352,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 30 untimed calls (~30 ms of prefill work) bring the GPU to its steady
+    # clocks; with 3 the timed region still includes the ramp (~10% slower)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy", "model"],

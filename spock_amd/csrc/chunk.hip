@@ -541,32 +541,35 @@ constexpr int kTiles = 8;   // 16-column tiles of the value dim per (sequence, h
 constexpr int kLdST = 132;  // LDS row stride of the transposed state tile (floats)
 constexpr int kLdVT = 68;   // LDS row stride of the transposed v_new tile (floats)
 
-// Operands of one chunk for stage A and for stages B-D (both prefetched a
-// chunk ahead).
+// Operands of one chunk for stage A (prefetched a chunk ahead) and for stages
+// B-D (loaded at the start of the chunk's own step, in flight during stage A).
 struct ScanEarly {
   float4 w[8];  // W rows: token 16M+li, key dims 16u+4lg..+3
   float4 q[8];  // raw Q rows, same map
-  float qs;     // Q scale of this lane's row
 };
 struct ScanLate {
   float4 a[4];   // A rows: token 16M+li, tokens 16u+4lg..+3
   float4 kt[8];  // raw K^T rows 32M+16(v/4)+li, tokens 16(v%4)+4lg..+3
   float4 u;      // U^T: column n0+li, tokens 16M+4lg..+3
   float4 ks;     // Ks of tokens 16M+4lg..+3
+  float4 qs;     // Qs of tokens 16M+4lg..+3
   float gle;     // e^{gL}
 };
 
 // Sequential chunk scan over one 128x16 state tile: one workgroup of 4
 // wavefronts per (sequence, head, 16-column tile), so a 16-head batch of 8
-// sequences gives 1024 workgroups and two run on each CU (independent
-// barriers: one workgroup's waits are the other's issue slots).  Wavefront M:
-//   A  v_new rows and output rows of token block M: W_M S and (Q_M qs) S
+// sequences gives 1024 workgroups and three run on each CU (independent
+// barriers: one workgroup's waits are the others' issue slots).  Wavefront M:
+//   A  v_new rows and output rows of token block M: W_M S and Q_M S
 //   B  v_new = U - W S  -> LDS, also scaled by Ks
-//   C  o = (Q qs) S + A v_new -> core
+//   C  o = qs (Q S) + A v_new -> core
 //   D  S rows 32M..32M+31 <- e^{gL} S + K^T diag(Ks) v_new
 // 112 MFMA per wavefront per chunk.
+// Three workgroups per CU (168 VGPRs; the fp16 instance spills a few): more
+// resident wavefronts measured faster than two workgroups holding both operand
+// sets double-buffered.
 template <typename TIn>
-__global__ __launch_bounds__(256, 2) void chunk_state_kernel(ChunkParams p) {
+__global__ __launch_bounds__(256, 3) void chunk_state_kernel(ChunkParams p) {
   typedef RawOf<TIn> R;
   // S tile and v_new stored transposed ([column][contraction index]) so one
   // ds_read_b128 feeds four consecutive MFMA steps; strides 132 and 68 keep
@@ -627,7 +630,6 @@ __global__ __launch_bounds__(256, 2) void chunk_state_kernel(ChunkParams p) {
       e.w[u] = *reinterpret_cast<const float4*>(ws + kWsW + ((M * 8 + u) * 64 + lane) * 4);
       e.q[u] = R::ld4(qf, ((M * 8 + u) * 64 + lane) * 4);
     }
-    e.qs = ws[kWsQs + 16 * M + li];
   };
   auto load_late = [&](ScanLate& l, int c) {
     const float* ws = record(c);
@@ -639,6 +641,7 @@ __global__ __launch_bounds__(256, 2) void chunk_state_kernel(ChunkParams p) {
     for (int u = 0; u < 8; ++u) l.kt[u] = R::ld4(kt, ((M * 8 + u) * 64 + lane) * 4);
     l.u = *reinterpret_cast<const float4*>(ws + kWsU + ((tile * 4 + M) * 64 + lane) * 4);
     l.ks = *reinterpret_cast<const float4*>(ws + kWsKs + 16 * M + 4 * lg);
+    l.qs = *reinterpret_cast<const float4*>(ws + kWsQs + 16 * M + 4 * lg);
     l.gle = ws[kWsMisc];
   };
 
@@ -646,18 +649,17 @@ __global__ __launch_bounds__(256, 2) void chunk_state_kernel(ChunkParams p) {
     const int tok0 = t_begin + c * kC;
     const int len = min(kC, L - c * kC);
 
-    // ---- stage A: W_M S and (Q_M qs) S share the B operand (S)
+    // ---- stage A: W_M S and Q_M S share the B operand (S); the per-row Q
+    // scale is applied to the product
     f4v aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
-    const float qsc = (16 * M + li) < len ? e.qs : 0.0f;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const float4 x = R::cvt4(e.q[u]);
-      const float4 qv = make_float4(x.x * qsc, x.y * qsc, x.z * qsc, x.w * qsc);
       const float4 sb = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * u + 4 * lg]);
+      const float4 x = R::cvt4(e.q[u]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         aw = mfma4(elem(e.w[u], k), elem(sb, k), aw);
-        aq = mfma4(elem(qv, k), elem(sb, k), aq);
+        aq = mfma4(elem(x, k), elem(sb, k), aq);
       }
     }
     // The loads issued just before this stage (same scheduling region) are
@@ -681,13 +683,23 @@ __global__ __launch_bounds__(256, 2) void chunk_state_kernel(ChunkParams p) {
     }
     __syncthreads();
 
-    // ---- stage C: o = (Q qs) S + A v_new (all four blocks of A's row block;
-    // the ones above the diagonal are zero)
+    // ---- stage C: o = qs (Q S) + A v_new (all four blocks of A's row
+    // block, the ones above the diagonal being zero; two accumulator chains)
+    {
+      float4 vb[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float4 vb = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
+      for (int u = 0; u < 4; ++u) vb[u] = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
+      f4v ac = {aq[0] * l.qs.x, aq[1] * l.qs.y, aq[2] * l.qs.z, aq[3] * l.qs.w};
+      f4v ad = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) aq = mfma4(elem(l.a[u], k), elem(vb, k), aq);
+      for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          ac = mfma4(elem(l.a[u], k), elem(vb[u], k), ac);
+          ad = mfma4(elem(l.a[u + 2], k), elem(vb[u + 2], k), ad);
+        }
+      }
+      aq = ac + ad;
     }
     // rows tok0 .. tok0+len-1 of this head through a buffer resource of len
     // rows: the hardware drops the padding rows' stores (offset past
@@ -707,15 +719,17 @@ __global__ __launch_bounds__(256, 2) void chunk_state_kernel(ChunkParams p) {
       s0 = f4v{x0.x * l.gle, x0.y * l.gle, x0.z * l.gle, x0.w * l.gle};
       s1 = f4v{x1.x * l.gle, x1.y * l.gle, x1.z * l.gle, x1.w * l.gle};
     }
+    float4 vs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vs[u] = *reinterpret_cast<const float4*>(&sVS[li * kLdVT + 16 * u + 4 * lg]);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const float4 vb = *reinterpret_cast<const float4*>(&sVS[li * kLdVT + 16 * u + 4 * lg]);
       const float4 k0 = R::cvt4(l.kt[u]);
       const float4 k1 = R::cvt4(l.kt[4 + u]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        s0 = mfma4(elem(k0, k), elem(vb, k), s0);
-        s1 = mfma4(elem(k1, k), elem(vb, k), s1);
+        s0 = mfma4(elem(k0, k), elem(vs[u], k), s0);
+        s1 = mfma4(elem(k1, k), elem(vs[u], k), s1);
       }
     }
     // every wave read sST (stage A) before the barrier above and only its own
@@ -725,25 +739,21 @@ __global__ __launch_bounds__(256, 2) void chunk_state_kernel(ChunkParams p) {
     __syncthreads();
   };
 
-  // Two operand sets used alternately: the loads of chunk c+1 are in flight
-  // while chunk c computes.
+  // Stage-A operands double-buffered (the loads of chunk c+1 are in flight
+  // while chunk c computes); stage B-D operands of chunk c are loaded at the
+  // start of its own step and arrive during stage A.
   ScanEarly ea, eb;
-  ScanLate la, lb;
-  if (nchunks > 0) {
-    load_early(ea, 0);
-    load_late(la, 0);
-  }
+  ScanLate lt;
+  if (nchunks > 0) load_early(ea, 0);
   __syncthreads();
   for (int c = 0; c < nchunks; c += 2) {
-    const int c1 = min(c + 1, nchunks - 1);
-    load_late(lb, c1);
-    load_early(eb, c1);
-    step(ea, la, c);
+    load_late(lt, c);
+    load_early(eb, min(c + 1, nchunks - 1));
+    step(ea, lt, c);
     if (c + 1 >= nchunks) break;
-    const int c2 = min(c + 2, nchunks - 1);
-    load_late(la, c2);
-    load_early(ea, c2);
-    step(eb, lb, c + 1);
+    load_late(lt, c + 1);
+    load_early(ea, min(c + 2, nchunks - 1));
+    step(eb, lt, c + 1);
   }
 
   float* outs = p.state + ((size_t)seq * p.H + h) * kD * kD;
