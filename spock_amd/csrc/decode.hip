@@ -9,7 +9,8 @@
 //       delta, rank-1 update, o=S^T q, RMSNorm, fp16(w*n)*SiLU(z).
 // The state stream is the cost (2 x 64 KiB per head): each lane owns a 16-row
 // x 4-column slice loaded as 16 float4 (global_load_dwordx4, row segments of
-// 512 B per 32 lanes), issued before the conv work so the HBM latency overlaps.
+// 512 B per 32 lanes).  Every global load is issued at the start, so no phase
+// after the conv waits on a memory round trip of its own.
 //
 // Reduction orders (fixed, and restated by the CPU oracle):
 //   conv taps summed i = 0..3; L2 / RMS sums use the shaders' 128-wide tree
@@ -73,11 +74,37 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
 
   const int c4 = tid & 31;  // owns columns 4*c4 .. 4*c4+3
   const int rq = tid >> 5;  // owns row groups 4*rq .. 4*rq+3, i.e. rows 16*rq .. 16*rq+15
+  // The small g/beta and norm-gate operands are loaded first and without a
+  // branch (a branch around a load makes the compiler wait for the loads
+  // before it), then the state; the conv operands follow inside the conv
+  // branch.  No later phase waits on a memory round trip of its own.
+  uint16_t a16 = 0, b16 = 0;
+  float a_log = 0.0f, dt_bias = 0.0f, g_tail = 0.0f, beta_tail = 0.0f;
+  uint16_t z16[2] = {0, 0};
+  float nw[2] = {0.0f, 0.0f};
+  if (REC) {
+    if (GB_TAIL) {
+      const float* tail = p.state + (long long)seq * p.state_stride + (long long)nh * 128 * 128;
+      g_tail = tail[h];
+      beta_tail = tail[nh + h];
+    } else {
+      a16 = p.a[(long long)seq * p.ab_stride + h];
+      b16 = p.b[(long long)seq * p.ab_stride + h];
+      a_log = p.alb[(p.layer * nh + h) * 2];
+      dt_bias = p.alb[(p.layer * nh + h) * 2 + 1];
+    }
+    if (NORM_GATE) {  // used by wave 0
+      const uint16_t* zr = p.z + (long long)seq * p.z_stride + h * 128;
+      z16[0] = zr[lane];
+      z16[1] = zr[lane + 64];
+      nw[0] = p.norm_w[lane];
+      nw[1] = p.norm_w[lane + 64];
+    }
+  }
   float4 S[16];
   float* st_head = nullptr;
   if (REC) {
-    float* st_seq = p.state + (long long)seq * p.state_stride;
-    st_head = st_seq + (long long)h * 128 * 128;
+    st_head = p.state + (long long)seq * p.state_stride + (long long)h * 128 * 128;
 #pragma unroll
     for (int m = 0; m < 16; ++m)
       S[m] = *reinterpret_cast<const float4*>(st_head + (rq * 16 + m) * 128 + c4 * 4);
@@ -88,14 +115,24 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
       // wave 0: Q block of head h, wave 1: K block, wave 2: V block.
       const int ch0 = wave * nh * 128 + h * 128;
       uint16_t* cs_seq = p.conv_state + (long long)seq * p.conv_stride;
+      // both halves' operands are loaded before the first conv-state store
+      uint2 olds[2], wvs[2];
+      uint16_t xs[2];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int ch = ch0 + lane + 64 * half;
+        olds[half] = *reinterpret_cast<const uint2*>(cs_seq + ch * 4);
+        wvs[half] = *reinterpret_cast<const uint2*>(p.conv_w + ch * 4);
+        xs[half] = qkv[ch];
+      }
       uint16_t y[2];
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int ch = ch0 + lane + 64 * half;
         uint2* csp = reinterpret_cast<uint2*>(cs_seq + ch * 4);
-        const uint2 old = *csp;
-        const uint2 wv = *reinterpret_cast<const uint2*>(p.conv_w + ch * 4);
-        const uint16_t x = qkv[ch];
+        const uint2 old = olds[half];
+        const uint2 wv = wvs[half];
+        const uint16_t x = xs[half];
         // shifted window (conv_l2_qk.comp:48-58): [old1, old2, old3, x]
         const uint16_t s0 = (uint16_t)(old.x >> 16);
         const uint16_t s1 = (uint16_t)(old.y & 0xffffu);
@@ -145,14 +182,11 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
 
   float g, beta;
   if (GB_TAIL) {
-    const float* tail = p.state + (long long)seq * p.state_stride + (long long)nh * 128 * 128;
-    g = tail[h];
-    beta = tail[nh + h];
+    g = g_tail;
+    beta = beta_tail;
   } else {
-    const float av = spk::h2f(p.a[(long long)seq * p.ab_stride + h]);
-    const float bv = spk::h2f(p.b[(long long)seq * p.ab_stride + h]);
-    const float a_log = p.alb[(p.layer * nh + h) * 2];
-    const float dt_bias = p.alb[(p.layer * nh + h) * 2 + 1];
+    const float av = spk::h2f(a16);
+    const float bv = spk::h2f(b16);
     const float sp = spk::logf_det(1.0f + spk::expf_det(av + dt_bias));
     g = -spk::expf_det(a_log) * sp;
     beta = 1.0f / (1.0f + spk::expf_det(-bv));
@@ -217,14 +251,13 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
       v = spk::tree64_to_lane0(v);
       const float tot = __shfl(v, 0, 64);
       const float r = spk::rsqrt_det(tot / 128.0f + p.eps);
-      const uint16_t* zr = p.z + (long long)seq * p.z_stride + h * 128;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int j = lane + 64 * half;
         const float o = half ? ob : oa;
         const float normed = o * r;
-        const float weighted = spk::h2f(spk::f2h(p.norm_w[j] * normed));
-        out[j] = spk::f2h(weighted * spk::silu_det(spk::h2f(zr[j])));
+        const float weighted = spk::h2f(spk::f2h(nw[half] * normed));
+        out[j] = spk::f2h(weighted * spk::silu_det(spk::h2f(z16[half])));
       }
     } else {
       out[lane] = spk::f2h(oa);

@@ -106,8 +106,9 @@ __device__ __forceinline__ void load_rows(const uint16_t* __restrict__ W, int ro
   }
 }
 
+// Sequential fma chain over the lane's 8*N8 contiguous elements (from 0).
 template <int N8>
-__device__ __forceinline__ float row_dot(const uint4 (&wr)[N8], const float* xf) {
+__device__ __forceinline__ float lane_dot(const uint4 (&wr)[N8], const float* xf) {
   float acc = 0.0f;
 #pragma unroll
   for (int k = 0; k < N8; ++k) {
@@ -116,10 +117,45 @@ __device__ __forceinline__ float row_dot(const uint4 (&wr)[N8], const float* xf)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
   }
-  return spk::tree64_to_lane0(acc);
+  return acc;
 }
 
-template <int N8, int R, bool PAIR>
+// v <- v + (v of lane l + S), for lanes whose partner lies in the same row of
+// 16 lanes (DPP row_shl:S); other lanes receive values no later level reads.
+template <int S>
+__device__ __forceinline__ float add_row_shl(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + S, 0xF, 0xF, true));
+}
+
+// N independent 64-lane trees s[l] += s[l+stride], stride 32..1 (the order of
+// spk::tree64_to_lane0), interleaved so each level's cross-lane moves are in
+// flight together: strides 32 and 16 through the LDS permute, 8..1 as DPP
+// row shifts.  Sums end in lane 0.
+template <int N>
+__device__ __forceinline__ void tree64_rows(float (&v)[N]) {
+  float t[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = __shfl_down(v[i], 32, 64);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = __shfl_down(v[i], 16, 64);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = add_row_shl<8>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = add_row_shl<4>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = add_row_shl<2>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = add_row_shl<1>(v[i]);
+}
+
+// KIND is the input kind (compile time, so the input and weight loads sit in
+// one straight-line block: the input operands are issued first and the
+// prologue waits for them alone while the weight rows are in flight).
+template <int N8, int R, bool PAIR, int KIND>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   __shared__ float xs[kMaxIn];
   __shared__ float red[257];
@@ -133,23 +169,43 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   constexpr int in_dim = 512 * N8;
   const int out_dim = a.out_dim[d];
   const int row0 = (((int)blockIdx.x - a.first_block[d]) * 4 + wave) * R;
-  // Weight rows first: they do not depend on x, so their latency overlaps the prologue.
-  uint4 wv[R][N8];
-  uint4 wv2[PAIR ? R : 1][N8];
-  load_rows<N8, R>(a.W[d], row0, out_dim, lane, wv);
-  if (PAIR) load_rows<N8, PAIR ? R : 1>(a.W2[d], row0, out_dim, lane, wv2);
-  if (a.kind == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
+  constexpr int NV = in_dim / 8;  // 16-byte pieces of x
+  constexpr int PER = (NV + 255) / 256;
+  static_assert(256 * PER * 8 <= kMaxIn, "x staging overruns xs");
+  uint2 hv = make_uint2(0, 0), nwv = make_uint2(0, 0);
+  uint4 xv[PER], uv[PER];
+  if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
     const uint16_t* h = a.x;
     if (a.token) {  // ids outside [0, token_rows) select row 0 instead of reading out of bounds
       const int id = a.token[0];
       h += (size_t)((id >= 0 && id < a.token_rows) ? id : 0) * kHidden;
     }
-    const uint2 hv = *reinterpret_cast<const uint2*>(h + 4 * tid);
-    const uint2 wv2n = *reinterpret_cast<const uint2*>(a.x2 + 4 * tid);
+    hv = *reinterpret_cast<const uint2*>(h + 4 * tid);
+    nwv = *reinterpret_cast<const uint2*>(a.x2 + 4 * tid);
+  } else {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = min(tid + 256 * c, NV - 1);
+      xv[c] = *reinterpret_cast<const uint4*>(a.x + 8 * idx);
+      if constexpr (KIND == SPK_GEMV_IN_SILU_GATE) uv[c] = *reinterpret_cast<const uint4*>(a.x2 + 8 * idx);
+    }
+  }
+  // residual rows (or, without a residual, any in-bounds halves) ahead of
+  // the weights, so the epilogue waits on no load of its own
+  const uint16_t* __restrict__ res = a.res[d];
+  const uint16_t* rsrc = res ? res : a.W[d];
+  uint16_t rv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rv[r] = rsrc[min(row0 + r, out_dim - 1)];
+  uint4 wv[R][N8];
+  uint4 wv2[PAIR ? R : 1][N8];
+  load_rows<N8, R>(a.W[d], row0, out_dim, lane, wv);
+  if (PAIR) load_rows<N8, PAIR ? R : 1>(a.W2[d], row0, out_dim, lane, wv2);
+  if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {
     const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
                         spk::h2f(hv.y >> 16)};
-    const float w[4] = {spk::h2f(wv2n.x & 0xffffu), spk::h2f(wv2n.x >> 16), spk::h2f(wv2n.y & 0xffffu),
-                        spk::h2f(wv2n.y >> 16)};
+    const float w[4] = {spk::h2f(nwv.x & 0xffffu), spk::h2f(nwv.x >> 16), spk::h2f(nwv.y & 0xffffu),
+                        spk::h2f(nwv.y >> 16)};
     float p = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) p = __builtin_fmaf(v[i], v[i], p);
@@ -157,36 +213,22 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
     const float nf = 1.0f / __builtin_sqrtf(sum / 1024.0f + 1e-6f);
 #pragma unroll
     for (int i = 0; i < 4; ++i) xs[4 * tid + i] = round16((v[i] * nf) * (1.0f + w[i]));
-    if (a.h_out && blockIdx.x == 0) *reinterpret_cast<uint2*>(a.h_out + 4 * tid) = hv;
   } else {
-    // 16-byte pieces, all loads issued before any use
-    constexpr int NV = in_dim / 8;
-    constexpr int PER = (NV + 255) / 256;
-    uint4 xv[PER], uv[PER];
-    const bool silu = a.kind == SPK_GEMV_IN_SILU_GATE;
+    // unconditional (pieces past NV repeat the last one into xs slots no lane
+    // reads; 256 * PER * 8 <= kMaxIn), so no load is sunk under a branch
 #pragma unroll
     for (int c = 0; c < PER; ++c) {
       const int idx = tid + 256 * c;
-      if (idx < NV) {
-        xv[c] = *reinterpret_cast<const uint4*>(a.x + 8 * idx);
-        if (silu) uv[c] = *reinterpret_cast<const uint4*>(a.x2 + 8 * idx);
+      float f[8];
+      unpack8(xv[c], f);
+      if constexpr (KIND == SPK_GEMV_IN_SILU_GATE) {
+        float u[8];
+        unpack8(uv[c], u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = round16(spk::silu_det(f[e]) * u[e]);
       }
-    }
 #pragma unroll
-    for (int c = 0; c < PER; ++c) {
-      const int idx = tid + 256 * c;
-      if (idx < NV) {
-        float f[8];
-        unpack8(xv[c], f);
-        if (silu) {
-          float u[8];
-          unpack8(uv[c], u);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = round16(spk::silu_det(f[e]) * u[e]);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xs[8 * idx + e] = f[e];
-      }
+      for (int e = 0; e < 8; e += 4) *reinterpret_cast<float4*>(&xs[8 * idx + e]) = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
     }
   }
   __syncthreads();
@@ -199,21 +241,28 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
     xf[k + 2] = t.z;
     xf[k + 3] = t.w;
   }
-  uint16_t* __restrict__ y = a.y[d];
-  const uint16_t* __restrict__ res = a.res[d];
+  constexpr int NT = PAIR ? 2 * R : R;
+  float acc[NT];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float acc = row_dot<N8>(wv[r], xf);
-    float acc2 = 0.0f;
-    if (PAIR) acc2 = row_dot<N8>(wv2[PAIR ? r : 0], xf);
+    acc[r] = lane_dot<N8>(wv[r], xf);
+    if (PAIR) acc[R + r] = lane_dot<N8>(wv2[PAIR ? r : 0], xf);
+  }
+  tree64_rows<NT>(acc);
+  uint16_t* __restrict__ y = a.y[d];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
     const int row = row0 + r;
     if (lane == 0 && row < out_dim) {
-      uint16_t o = spk::f2h(acc);
-      if (PAIR) o = spk::f2h(spk::silu_det(spk::h2f(o)) * spk::h2f(spk::f2h(acc2)));
-      if (res) o = spk::f2h(spk::h2f(res[row]) + spk::h2f(o));
+      uint16_t o = spk::f2h(acc[r]);
+      if (PAIR) o = spk::f2h(spk::silu_det(spk::h2f(o)) * spk::h2f(spk::f2h(acc[PAIR ? R + r : 0])));
+      if (res) o = spk::f2h(spk::h2f(rv[r]) + spk::h2f(o));
       y[row] = o;
     }
   }
+  // the first layer's input row (token embedding) becomes the residual stream
+  if constexpr (KIND == SPK_GEMV_IN_RMSNORM)
+    if (a.h_out && blockIdx.x == 0) *reinterpret_cast<uint2*>(a.h_out + 4 * tid) = hv;
 }
 
 // ---------------------------------------------------------------------------
@@ -229,7 +278,8 @@ constexpr int kPartFloats = 2 + kHeadDim;  // m, S, O[256]
 
 // Per-head RMSNorm(1+w) of the 256 values a wave holds (lane l: d = 4l..4l+3),
 // in the s[t] += s[t+stride] (stride 128..1) order; returns fp16-rounded values.
-__device__ __forceinline__ void head_norm_wave(float (&v)[4], const uint16_t* w, int lane) {
+// wf: the lane's 4 norm weights.
+__device__ __forceinline__ void head_norm_wave(float (&v)[4], const float (&wf)[4]) {
   float s[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) s[i] = v[i] * v[i];
@@ -241,30 +291,45 @@ __device__ __forceinline__ void head_norm_wave(float (&v)[4], const uint16_t* w,
   float sum = (s[0] + s[2]) + (s[1] + s[3]);  // strides 2 then 1 inside lane 0
   sum = __shfl(sum, 0, 64);
   const float nf = 1.0f / __builtin_sqrtf(sum / 256.0f + 1e-6f);
-  const uint2 wv = *reinterpret_cast<const uint2*>(w + 4 * lane);
-  const float wf[4] = {spk::h2f(wv.x & 0xffffu), spk::h2f(wv.x >> 16), spk::h2f(wv.y & 0xffffu),
-                       spk::h2f(wv.y >> 16)};
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = round16((v[i] * nf) * (1.0f + wf[i]));
 }
 
+__device__ __forceinline__ void head_norm_wave(float (&v)[4], const uint16_t* w, int lane) {
+  const uint2 wv = *reinterpret_cast<const uint2*>(w + 4 * lane);
+  const float wf[4] = {spk::h2f(wv.x & 0xffffu), spk::h2f(wv.x >> 16), spk::h2f(wv.y & 0xffffu),
+                       spk::h2f(wv.y >> 16)};
+  head_norm_wave(v, wf);
+}
+
+// The (cos, sin) pairs of the lane's 4 dims d = 4l..4l+3 (pair index d & 31).
+__device__ __forceinline__ void load_rope(const float* cs, int lane, float (&c)[8]) {
+  const int p0 = (4 * lane) & 31;
+  const float4 lo = *reinterpret_cast<const float4*>(cs + 2 * p0);
+  const float4 hi = *reinterpret_cast<const float4*>(cs + 2 * p0 + 4);
+  c[0] = lo.x; c[1] = lo.y; c[2] = lo.z; c[3] = lo.w;
+  c[4] = hi.x; c[5] = hi.y; c[6] = hi.z; c[7] = hi.w;
+}
+
 // rope_apply.comp pairs (i, i+32), i < 32: lanes 0..7 hold d < 32, lanes 8..15 d in [32, 64).
-__device__ __forceinline__ void rope_wave(float (&v)[4], const float* cs, int lane) {
+__device__ __forceinline__ void rope_wave(float (&v)[4], const float (&c8)[8], int lane) {
   float o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = __shfl_xor(v[i], 8, 64);
   if (lane < 16) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int d = 4 * lane + i;
-      const int p = d & 31;
-      const float c = cs[2 * p], s = cs[2 * p + 1];
-      if (d < 32)
-        v[i] = round16(v[i] * c - o[i] * s);
-      else
-        v[i] = round16(v[i] * c + o[i] * s);
+      // d < 32: v*c - o*s; else v*c + o*s (negating o first gives the same bits)
+      const float os = (4 * lane + i < 32) ? -o[i] : o[i];
+      v[i] = round16(v[i] * c8[2 * i] + os * c8[2 * i + 1]);
     }
   }
+}
+
+__device__ __forceinline__ void rope_wave(float (&v)[4], const float* cs, int lane) {
+  float c8[8];
+  load_rope(cs, lane, c8);
+  rope_wave(v, c8, lane);
 }
 
 __device__ __forceinline__ void load4h(const uint16_t* p, float (&v)[4]) {
@@ -299,18 +364,40 @@ struct AttnArgs {
   int store_kv;        // decode: the current position's block stores its K/V row
 };
 
+// K rows in LDS are padded to 264 halves (528 B): lane p reading 16 B of row p
+// and lane p+1 reading row p+1 land 4 banks apart, so a ds_read_b128 over 64
+// rows is conflict-free.
+constexpr int kKLd = kHeadDim + 8;
+
 // One query-head wave over one block of positions [64b, 64b+64) of npos valid
-// ones, operands staged in LDS (K transposed, Kt[d][p]; V as Vs[p][d]; q as
-// fp16-rounded floats): writes m_b, S_b, O_b.
-__device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t (*Kt)[kAttnBlock],
+// ones, operands staged in LDS (K as Ks[p][d], V as Vs[p][d], q as fp16-rounded
+// floats): writes m_b, S_b, O_b.  Lane = position for the scores: each lane
+// reads its K row 8 dims at a time (ds_read_b128) and runs the d = 0..255 fma
+// chain; the weighted V sum visits positions j = 0..nvalid-1 in order, taking
+// w_j by readlane and prefetching 8 V rows at a time.
+__device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t (*Ks)[kKLd],
                                                 const uint16_t (*Vs)[kHeadDim], int b, int npos, int lane,
                                                 float* part) {
   const int p = kAttnBlock * b + lane;
   float sc = -INFINITY;
   if (p < npos) {
     float dot = 0.0f;
-#pragma unroll 8
-    for (int d = 0; d < kHeadDim; ++d) dot = __builtin_fmaf(qs[d], spk::h2f(Kt[d][lane]), dot);
+#pragma unroll 4
+    for (int d8 = 0; d8 < kHeadDim / 8; ++d8) {
+      const uint4 kk = *reinterpret_cast<const uint4*>(&Ks[lane][8 * d8]);
+      const float4 q0 = *reinterpret_cast<const float4*>(&qs[8 * d8]);
+      const float4 q1 = *reinterpret_cast<const float4*>(&qs[8 * d8 + 4]);
+      float kf[8];
+      unpack8(kk, kf);
+      dot = __builtin_fmaf(q0.x, kf[0], dot);
+      dot = __builtin_fmaf(q0.y, kf[1], dot);
+      dot = __builtin_fmaf(q0.z, kf[2], dot);
+      dot = __builtin_fmaf(q0.w, kf[3], dot);
+      dot = __builtin_fmaf(q1.x, kf[4], dot);
+      dot = __builtin_fmaf(q1.y, kf[5], dot);
+      dot = __builtin_fmaf(q1.z, kf[6], dot);
+      dot = __builtin_fmaf(q1.w, kf[7], dot);
+    }
     sc = dot * 0.0625f;
   }
   float m = sc;
@@ -320,12 +407,21 @@ __device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t 
   const float S = spk::tree64_to_lane0(w);
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int nvalid = min(kAttnBlock, npos - kAttnBlock * b);
-  for (int j = 0; j < nvalid; ++j) {
-    const float wj = __shfl(w, j, 64);
-    float vf[4];
-    load4h(&Vs[j][4 * lane], vf);
+  const int wbits = __float_as_int(w);
+  for (int j0 = 0; j0 < nvalid; j0 += 8) {
+    uint2 vv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(wj, vf[i], acc[i]);
+    for (int i = 0; i < 8; ++i) vv[i] = *reinterpret_cast<const uint2*>(&Vs[j0 + i][4 * lane]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (j0 + i < nvalid) {
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(wbits, j0 + i));
+        const float vf[4] = {spk::h2f(vv[i].x & 0xffffu), spk::h2f(vv[i].x >> 16), spk::h2f(vv[i].y & 0xffffu),
+                             spk::h2f(vv[i].y >> 16)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(wj, vf[e], acc[e]);
+      }
+    }
   }
   if (lane == 0) {
     part[0] = m;
@@ -336,8 +432,8 @@ __device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t 
 
 // grid (max_blocks, kv_heads, T); block 256.
 __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
-  __shared__ float qs[4][kHeadDim];
-  __shared__ __align__(16) uint16_t Kt[kHeadDim][kAttnBlock];
+  __shared__ __align__(16) float qs[4][kHeadDim];
+  __shared__ __align__(16) uint16_t Ks[kAttnBlock][kKLd];
   __shared__ __align__(16) uint16_t Vs[kAttnBlock][kHeadDim];
   const int b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -347,65 +443,63 @@ __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
   if (kAttnBlock * b >= npos) return;
   const float* cs = a.rope + (size_t)pos * 64;
   const int cur = (a.store_kv && (pos / kAttnBlock) == b) ? pos - kAttnBlock * b : -1;
-  // Stage the block's K (transposed) and V rows: thread (p = tid/4, quarter tid%4)
-  // moves 64 dims of K and of V of position 64b + p; all loads first.
-  {
-    const int p = tid >> 2, q4 = tid & 3;
-    const int gp = kAttnBlock * b + p;
-    uint4 kv4[8], vv4[8];
-    const bool live = gp < npos && p != cur;
+  const int qh = kvh * 4 + wave;
+  // Loads first, small operands ahead of the block's K/V rows (a wave's loads
+  // complete in issue order): this wave's q head with its norm weights and
+  // RoPE pairs, the new K/V row when this block holds the current position,
+  // then K/V of position 64b + tid/4 (quarter tid%4: 64 dims of K and of V;
+  // rows past the current position read row 0 and stage zeros).
+  float qv[4], qw[4], c8[8];
+  load4h(a.qg + (size_t)t * 4096 + qh * 512 + 4 * lane, qv);
+  load4h(a.q_norm_w + 4 * lane, qw);
+  load_rope(cs, lane, c8);
+  // the new K/V row is read by every wave (a few hundred bytes) so that no
+  // load sits under a branch; only the block holding the position uses it
+  const bool newrow = cur >= 0 && wave == 0;
+  const uint2 nk16 = *reinterpret_cast<const uint2*>(a.k + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
+  const uint2 kw16 = *reinterpret_cast<const uint2*>(a.k_norm_w + 4 * lane);
+  const uint2 vb = *reinterpret_cast<const uint2*>(a.v + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
+  const int p = tid >> 2, q4 = tid & 3;
+  const int gp = kAttnBlock * b + p;
+  const bool live = gp < npos && p != cur;
+  const uint16_t* row = a.kv + (size_t)(live ? gp : 0) * kKvRow + kvh * kHeadDim + q4 * 64;
+  uint4 kv4[8], vv4[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    kv4[i] = *reinterpret_cast<const uint4*>(row + 8 * i);
+    vv4[i] = *reinterpret_cast<const uint4*>(row + 512 + 8 * i);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the q work below
+  head_norm_wave(qv, qw);
+  rope_wave(qv, c8, lane);
+  *reinterpret_cast<float4*>(&qs[wave][4 * lane]) = make_float4(qv[0], qv[1], qv[2], qv[3]);
+  if (newrow) {  // new K row: norm + rope; V row as projected
+    float nk[4] = {spk::h2f(nk16.x & 0xffffu), spk::h2f(nk16.x >> 16), spk::h2f(nk16.y & 0xffffu),
+                   spk::h2f(nk16.y >> 16)};
+    const float kw[4] = {spk::h2f(kw16.x & 0xffffu), spk::h2f(kw16.x >> 16), spk::h2f(kw16.y & 0xffffu),
+                         spk::h2f(kw16.y >> 16)};
+    head_norm_wave(nk, kw);
+    rope_wave(nk, c8, lane);
+    const uint2 kb = pack4h(nk);
+    *reinterpret_cast<uint2*>(&Ks[cur][4 * lane]) = kb;
+    *reinterpret_cast<uint2*>(&Vs[cur][4 * lane]) = vb;
+    uint16_t* crow = a.kv + (size_t)pos * kKvRow;  // kv_cache_store.comp:27-48
+    *reinterpret_cast<uint2*>(crow + kvh * kHeadDim + 4 * lane) = kb;
+    *reinterpret_cast<uint2*>(crow + 512 + kvh * kHeadDim + 4 * lane) = vb;
+  }
+  if (p != cur) {
+    const uint32_t keep = live ? 0xffffffffu : 0u;  // rows past the current position stage zeros
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if (live) {
-        const uint16_t* row = a.kv + (size_t)gp * kKvRow + kvh * kHeadDim + q4 * 64;
-        kv4[i] = *reinterpret_cast<const uint4*>(row + 8 * i);
-        vv4[i] = *reinterpret_cast<const uint4*>(row + 512 + 8 * i);
-      } else {
-        kv4[i] = make_uint4(0, 0, 0, 0);
-        vv4[i] = make_uint4(0, 0, 0, 0);
-      }
+      const uint4 k = make_uint4(kv4[i].x & keep, kv4[i].y & keep, kv4[i].z & keep, kv4[i].w & keep);
+      const uint4 v = make_uint4(vv4[i].x & keep, vv4[i].y & keep, vv4[i].z & keep, vv4[i].w & keep);
+      *reinterpret_cast<uint4*>(&Ks[p][q4 * 64 + 8 * i]) = k;
+      *reinterpret_cast<uint4*>(&Vs[p][q4 * 64 + 8 * i]) = v;
     }
-    if (p != cur) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t w4[4] = {kv4[i].x, kv4[i].y, kv4[i].z, kv4[i].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          Kt[q4 * 64 + 8 * i + 2 * e][p] = (uint16_t)(w4[e] & 0xffffu);
-          Kt[q4 * 64 + 8 * i + 2 * e + 1][p] = (uint16_t)(w4[e] >> 16);
-        }
-        *reinterpret_cast<uint4*>(&Vs[p][q4 * 64 + 8 * i]) = vv4[i];
-      }
-    }
-  }
-  const int qh = kvh * 4 + wave;
-  {
-    float v[4];
-    load4h(a.qg + (size_t)t * 4096 + qh * 512 + 4 * lane, v);
-    head_norm_wave(v, a.q_norm_w, lane);
-    rope_wave(v, cs, lane);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = v[i];
-  }
-  if (cur >= 0 && wave == 0) {  // new K row: norm + rope; V row as projected
-    float v[4];
-    load4h(a.k + (size_t)t * 512 + kvh * kHeadDim + 4 * lane, v);
-    head_norm_wave(v, a.k_norm_w, lane);
-    rope_wave(v, cs, lane);
-    const uint2 kb = pack4h(v);
-    const uint2 vb = *reinterpret_cast<const uint2*>(a.v + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
-    const uint16_t k16[4] = {(uint16_t)(kb.x & 0xffffu), (uint16_t)(kb.x >> 16), (uint16_t)(kb.y & 0xffffu),
-                             (uint16_t)(kb.y >> 16)};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) Kt[4 * lane + i][cur] = k16[i];
-    *reinterpret_cast<uint2*>(&Vs[cur][4 * lane]) = vb;
-    uint16_t* row = a.kv + (size_t)pos * kKvRow;  // kv_cache_store.comp:27-48
-    *reinterpret_cast<uint2*>(row + kvh * kHeadDim + 4 * lane) = kb;
-    *reinterpret_cast<uint2*>(row + 512 + kvh * kHeadDim + 4 * lane) = vb;
   }
   __syncthreads();
   float* part = a.part + (((size_t)t * kQHeads + qh) * a.max_blocks + b) * kPartFloats;
-  attn_block_wave(qs[wave], Kt, Vs, b, npos, lane, part);
+  attn_block_wave(qs[wave], Ks, Vs, b, npos, lane, part);
 }
 
 // Prefill: K/V rows of positions pos0..pos0+T-1, before any block pass reads
@@ -425,16 +519,22 @@ __global__ __launch_bounds__(64) void attn_store_kv_kernel(AttnArgs a) {
 }
 
 // grid (8 query heads, T); block 256 (thread = output dim).  Blocks are
-// combined in order; their partials are loaded 8 at a time so the loads are
-// in flight together.
+// combined in order.  The O partials of the first 16 blocks are loaded
+// together with the m/S values, ahead of the max reduction; later blocks'
+// partials are loaded 8 at a time so the loads are in flight together.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   __shared__ float cfac[1024], sfac[1024];
   __shared__ float red[257];
+  constexpr int kPre = 16;
   const int qh = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
   const int pos = a.pos_dev ? a.pos_dev[0] : a.pos0 + t;
   if (pos < 0 || pos >= a.max_seq) return;
   const int nb = (pos + kAttnBlock) / kAttnBlock;  // <= max_blocks <= 1024
   const float* part = a.part + ((size_t)t * kQHeads + qh) * a.max_blocks * kPartFloats;
+  const uint16_t g16 = a.qg[(size_t)t * 4096 + qh * 512 + 256 + d];
+  float ov0[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) ov0[i] = part[(size_t)min(i, nb - 1) * kPartFloats + 2 + d];
   float M = -INFINITY;
   for (int b = d; b < nb; b += 256) {
     const float m = part[(size_t)b * kPartFloats];
@@ -455,10 +555,18 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   for (int b = d; b < nb; b += 256) cfac[b] = spk::expf_det(cfac[b] - M);
   __syncthreads();
   float tot = 0.0f, o = 0.0f;
-  for (int b0 = 0; b0 < nb; b0 += 8) {
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    if (i < nb) {
+      const float c = cfac[i];
+      tot = tot + sfac[i] * c;
+      o = o + ov0[i] * c;
+    }
+  }
+  for (int b0 = kPre; b0 < nb; b0 += 8) {
     float ov[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ov[i] = b0 + i < nb ? part[(size_t)(b0 + i) * kPartFloats + 2 + d] : 0.0f;
+    for (int i = 0; i < 8; ++i) ov[i] = part[(size_t)min(b0 + i, nb - 1) * kPartFloats + 2 + d];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if (b0 + i < nb) {
@@ -469,7 +577,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     }
   }
   const float att = round16(o * (1.0f / (tot + 1e-30f)));
-  const float g = spk::h2f(a.qg[(size_t)t * 4096 + qh * 512 + 256 + d]);
+  const float g = spk::h2f(g16);
   const float sig = 1.0f / (1.0f + spk::expf_det(-g));
   a.out[(size_t)t * 2048 + qh * kHeadDim + d] = spk::f2h(att * sig);
 }
@@ -618,13 +726,23 @@ extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs,
   a.first_block[kMaxOut] = blocks;
   hipStream_t s = spk::to_hip(stream);
   const bool pair = outs[0].W_up != nullptr;
+#define SPK_FGK(n8, r, kind)                                                                            \
+  if (pair)                                                                                             \
+    hipLaunchKernelGGL((fused_gemv_kernel<n8, r, true, kind>), dim3(blocks), dim3(256), 0, s, a);       \
+  else                                                                                                  \
+    hipLaunchKernelGGL((fused_gemv_kernel<n8, r, false, kind>), dim3(blocks), dim3(256), 0, s, a);
 #define SPK_FG(n8, r)                                                                                   \
   case n8:                                                                                              \
-    if (pair)                                                                                           \
-      hipLaunchKernelGGL((fused_gemv_kernel<n8, r, true>), dim3(blocks), dim3(256), 0, s, a);           \
-    else                                                                                                \
-      hipLaunchKernelGGL((fused_gemv_kernel<n8, r, false>), dim3(blocks), dim3(256), 0, s, a);          \
+    if (in->kind == SPK_GEMV_IN_SILU_GATE) {                                                            \
+      SPK_FGK(n8, r, SPK_GEMV_IN_SILU_GATE)                                                             \
+    } else {                                                                                            \
+      SPK_FGK(n8, r, SPK_GEMV_IN_PLAIN)                                                                 \
+    }                                                                                                   \
     break;
+  if (in->kind == SPK_GEMV_IN_RMSNORM) {  // in_dim == kHidden (checked above)
+    SPK_FGK(2, 2, SPK_GEMV_IN_RMSNORM)
+    return spk::check_launch("spk_gemv_fused");
+  }
   switch (n8) {
     SPK_FG(1, 2)
     SPK_FG(2, 2)
@@ -636,6 +754,7 @@ extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs,
     SPK_FG(8, 1)
     default: return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: in_dim %d", in_dim);
   }
+#undef SPK_FGK
 #undef SPK_FG
   return spk::check_launch("spk_gemv_fused");
 }
