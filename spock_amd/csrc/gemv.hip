@@ -99,31 +99,34 @@ __device__ __forceinline__ void unpack8(const uint4& u, float* f) {
 template <int N8, int R, bool STREAM = false>
 __device__ __forceinline__ void rows_dot(const uint16_t* __restrict__ W, int in_dim, int row0,
                                          int out_dim, const float* xf, int lane, float* sums) {
+  // rows past out_dim re-read the last row (no load under a branch); callers
+  // discard their sums
   uint4 wv[R][N8];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = row0 + r;
-    if (row < out_dim) {
-      const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
+    const int row = min(row0 + r, out_dim - 1);
+    const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
 #pragma unroll
-      for (int k = 0; k < N8; ++k) wv[r][k] = STREAM ? ld_stream(src + k) : ld_w(src + k);
-    } else {
-#pragma unroll
-      for (int k = 0; k < N8; ++k) wv[r][k] = make_uint4(0, 0, 0, 0);
-    }
+    for (int k = 0; k < N8; ++k) wv[r][k] = STREAM ? ld_stream(src + k) : ld_w(src + k);
   }
+  // all R*N8 loads in flight before any use (else the scheduler trades
+  // bytes in flight for registers)
+  __builtin_amdgcn_sched_barrier(0);
+  float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float acc = 0.0f;
+    acc[r] = 0.0f;
 #pragma unroll
     for (int k = 0; k < N8; ++k) {
       float wf[8];
       unpack8(wv[r][k], wf);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
+      for (int e = 0; e < 8; ++e) acc[r] = __builtin_fmaf(wf[e], xf[8 * k + e], acc[r]);
     }
-    sums[r] = spk::tree64_to_lane0(acc);
   }
+  spk::tree64_rows<R>(acc);
+#pragma unroll
+  for (int r = 0; r < R; ++r) sums[r] = acc[r];
 }
 
 template <int N8>
@@ -241,6 +244,12 @@ __device__ __forceinline__ void batched_rows(const uint16_t* __restrict__ W, con
   constexpr int R = batch_rows(N8);
   constexpr int in_dim = 512 * N8;
   const int row0 = (blk * 4 + wave) * R;
+  // x first (a wave's loads complete in issue order, so the dot can start on
+  // the first weight row to arrive), then the weight rows
+  uint4 xr[N8];
+  const uint4* xsrc = reinterpret_cast<const uint4*>(x + lane * (8 * N8));
+#pragma unroll
+  for (int k = 0; k < N8; ++k) xr[k] = xsrc[k];
   uint4 wv[R][N8];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -249,21 +258,26 @@ __device__ __forceinline__ void batched_rows(const uint16_t* __restrict__ W, con
 #pragma unroll
     for (int k = 0; k < N8; ++k) wv[r][k] = ld_w(src + k);
   }
+  __builtin_amdgcn_sched_barrier(0);  // all loads in flight before any use
   float xf[8 * N8];
-  load_x<N8>(x, lane, xf);
+#pragma unroll
+  for (int k = 0; k < N8; ++k) unpack8(xr[k], xf + 8 * k);
+  float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float acc = 0.0f;
+    acc[r] = 0.0f;
 #pragma unroll
     for (int k = 0; k < N8; ++k) {
       float wf[8];
       unpack8(wv[r][k], wf);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[e], xf[8 * k + e], acc);
+      for (int e = 0; e < 8; ++e) acc[r] = __builtin_fmaf(wf[e], xf[8 * k + e], acc[r]);
     }
-    acc = spk::tree64_to_lane0(acc);
-    if (lane == 0 && row0 + r < out_dim) y[row0 + r] = spk::f2h(acc);
   }
+  spk::tree64_rows<R>(acc);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (lane == 0 && row0 + r < out_dim) y[row0 + r] = spk::f2h(acc[r]);
 }
 
 __global__ __launch_bounds__(256) void gemv_batched_kernel(GemvBatch b) {

@@ -120,38 +120,6 @@ __device__ __forceinline__ float lane_dot(const uint4 (&wr)[N8], const float* xf
   return acc;
 }
 
-// v <- v + (v of lane l + S), for lanes whose partner lies in the same row of
-// 16 lanes (DPP row_shl:S); other lanes receive values no later level reads.
-template <int S>
-__device__ __forceinline__ float add_row_shl(float v) {
-  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + S, 0xF, 0xF, true));
-}
-
-// N independent 64-lane trees s[l] += s[l+stride], stride 32..1 (the order of
-// spk::tree64_to_lane0), interleaved so each level's cross-lane moves are in
-// flight together: strides 32 and 16 through the LDS permute, 8..1 as DPP
-// row shifts.  Sums end in lane 0.
-template <int N>
-__device__ __forceinline__ void tree64_rows(float (&v)[N]) {
-  float t[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) t[i] = __shfl_down(v[i], 32, 64);
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
-#pragma unroll
-  for (int i = 0; i < N; ++i) t[i] = __shfl_down(v[i], 16, 64);
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = add_row_shl<8>(v[i]);
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = add_row_shl<4>(v[i]);
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = add_row_shl<2>(v[i]);
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = add_row_shl<1>(v[i]);
-}
-
 // KIND is the input kind (compile time, so the input and weight loads sit in
 // one straight-line block: the input operands are issued first and the
 // prologue waits for them alone while the weight rows are in flight).
@@ -201,6 +169,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   uint4 wv2[PAIR ? R : 1][N8];
   load_rows<N8, R>(a.W[d], row0, out_dim, lane, wv);
   if (PAIR) load_rows<N8, PAIR ? R : 1>(a.W2[d], row0, out_dim, lane, wv2);
+  __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue
   if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {
     const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
                         spk::h2f(hv.y >> 16)};
@@ -248,7 +217,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
     acc[r] = lane_dot<N8>(wv[r], xf);
     if (PAIR) acc[R + r] = lane_dot<N8>(wv2[PAIR ? r : 0], xf);
   }
-  tree64_rows<NT>(acc);
+  spk::tree64_rows<NT>(acc);
   uint16_t* __restrict__ y = a.y[d];
 #pragma unroll
   for (int r = 0; r < R; ++r) {

@@ -114,4 +114,36 @@ __device__ __forceinline__ float tree64_to_lane0(float v) {
   return v;
 }
 
+// v <- v + (v of lane l + S), for lanes whose partner lies in the same row of
+// 16 lanes (DPP row_shl:S); other lanes receive values no later level reads.
+template <int S>
+__device__ __forceinline__ float add_row_shl(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + S, 0xF, 0xF, true));
+}
+
+// N independent 64-lane trees s[l] += s[l+stride], stride 32..1 (the order of
+// tree64_to_lane0), interleaved so each level's cross-lane moves are in
+// flight together: strides 32 and 16 through the LDS permute, 8..1 as DPP
+// row shifts.  Sums end in lane 0.
+template <int N>
+__device__ __forceinline__ void tree64_rows(float (&v)[N]) {
+  float t[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = __shfl_down(v[i], 32, 64);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = __shfl_down(v[i], 16, 64);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = add_row_shl<8>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = add_row_shl<4>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = add_row_shl<2>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = add_row_shl<1>(v[i]);
+}
+
 }  // namespace spk
