@@ -131,8 +131,22 @@ __device__ __forceinline__ float ld_in(const void* p, bool f16, long long i) {
   return f16 ? spk::h2f(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
 
+// Per chunk, the state-independent results of the chunk body: solved (U)
+// [64][128], kcd (W) [64][128], local (decayed QK^T) [64][64], eg [64],
+// wlast [64].
+constexpr int kChunkWs = 2 * kC * kD + kC * kC + 2 * kC;
+
+// Per head: qs, ks, vs [total][128], then kChunkWs floats per chunk.
+__host__ __device__ __forceinline__ size_t head_ws_floats(int total) {
+  return (size_t)3 * total * kD + (size_t)(total / kC) * kChunkWs;
+}
+
 __device__ __forceinline__ float* head_ws(const OrdArgs& a, int h) {
-  return a.ws + (size_t)h * ((size_t)3 * a.total * kD + 4 * kC * kD);
+  return a.ws + (size_t)h * head_ws_floats(a.total);
+}
+
+__device__ __forceinline__ float* chunk_ws(const OrdArgs& a, int h, int ci) {
+  return head_ws(a, h) + (size_t)3 * a.total * kD + (size_t)ci * kChunkWs;
 }
 
 // Padded, optionally L2-normalised (deltanet_chunk.cpp:27-39, 78-85) and
@@ -170,124 +184,208 @@ __global__ void ordered_prep_kernel(OrdArgs a) {
   for (int d = 0; d < kD; ++d) qs[d] = qs[d] * a.q_scale;
 }
 
-// One workgroup per head; chunks in order; each phase of the reference's
-// chunk body split over independent outputs, every reduction sequential.
-__global__ __launch_bounds__(kThreads) void ordered_chunk_kernel(OrdArgs a) {
-  __shared__ float gcum[kC], bc[kC], eg[kC], wlast[kC], old_row[kC];
-  __shared__ float decay[kC][kC + 1], attn[kC][kC + 1], local[kC][kC + 1];
-  const int h = blockIdx.x, tid = threadIdx.x;
+// Chunk body, part 1 (run_deltanet_chunk_rule's loops that do not read the
+// state): one workgroup per (chunk, head), every chunk at once.  Each phase is
+// split over its independent outputs; every reduction runs in the reference's
+// sequential order.
+__global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a) {
+  __shared__ float gcum[kC], bc[kC], eg[kC], old_row[kC];
+  __shared__ float decay[kC][kC + 1], attn[kC][kC + 1];
+  const int ci = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  float* w = head_ws(a, h);
+  const int base = ci * kC;
+  const float* qc = w + (size_t)base * kD;
+  const float* kc = w + (size_t)a.total * kD + (size_t)base * kD;
+  const float* vc = w + (size_t)2 * a.total * kD + (size_t)base * kD;
+  float* cw = chunk_ws(a, h, ci);
+  float* solved = cw;
+  float* kcd = cw + kC * kD;
+  float* local = cw + 2 * kC * kD;
+  float* egw = local + kC * kC;
+  float* wlast = egw + kC;
+  if (tid == 0) {  // :137-151
+    float running = 0.0f;
+    for (int t = 0; t < kC; ++t) {
+      const int tok = base + t;
+      const float gt = tok < a.T ? a.g[(size_t)h * a.T + tok] : 0.0f;
+      gcum[t] = running + gt;
+      running = gcum[t];
+      bc[t] = tok < a.T ? a.beta[(size_t)h * a.T + tok] : 0.0f;
+    }
+  }
+  __syncthreads();
+  if (tid < kC) {
+    eg[tid] = spk::expf_det(gcum[tid]);
+    egw[tid] = eg[tid];
+    wlast[tid] = spk::expf_det(gcum[kC - 1] - gcum[tid]);
+  }
+  for (int i = tid; i < kC * kC; i += kThreads) {  // :153-159
+    const int r = i / kC, c = i % kC;
+    decay[r][c] = c <= r ? spk::expf_det(gcum[r] - gcum[c]) : 0.0f;
+  }
+  __syncthreads();
+  for (int i = tid; i < kC * kC; i += kThreads) {  // :161-170
+    const int r = i / kC, c = i % kC;
+    float val = 0.0f;
+    if (c < r) {
+      float dot = 0.0f;
+      for (int d = 0; d < kD; ++d) dot = dot + (kc[r * kD + d] * bc[r]) * kc[c * kD + d];
+      val = -dot * decay[r][c];
+    }
+    attn[r][c] = val;
+  }
+  for (int i = tid; i < kC * kC; i += kThreads) {  // :204-213
+    const int r = i / kC, c = i % kC;
+    float val = 0.0f;
+    if (c <= r) {
+      float dot = 0.0f;
+      for (int d = 0; d < kD; ++d) dot = dot + qc[r * kD + d] * kc[c * kD + d];
+      val = dot * decay[r][c];
+    }
+    local[i] = val;
+  }
+  __syncthreads();
+  for (int r = 1; r < kC; ++r) {  // :171-181 forward substitution, row by row
+    if (tid < r) old_row[tid] = attn[r][tid];
+    __syncthreads();
+    if (tid < r) {
+      const int c = tid;
+      float sum = old_row[c];
+      for (int in = 0; in < r; ++in) sum = sum + old_row[in] * attn[in][c];
+      attn[r][c] = sum;
+    }
+    __syncthreads();
+  }
+  if (tid < kC) attn[tid][tid] = attn[tid][tid] + 1.0f;  // :182-184
+  __syncthreads();
+  for (int i = tid; i < kC * kD; i += kThreads) {  // :186-202
+    const int r = i / kD, d = i % kD;
+    float sv = 0.0f, sk = 0.0f;
+    for (int c = 0; c < kC; ++c) {
+      const float coeff = attn[r][c];
+      if (coeff == 0.0f) continue;
+      const float bcol = bc[c];
+      sv = sv + coeff * (vc[c * kD + d] * bcol);
+      sk = sk + coeff * ((kc[c * kD + d] * bcol) * eg[c]);
+    }
+    solved[i] = sv;
+    kcd[i] = sk;
+  }
+}
+
+// Chunk body, part 2 (the loops that read or write the state, :215-268): the
+// state's value columns are independent, so one workgroup per (head, slice of
+// kSlice columns) scans the chunks in order with its 128 x kSlice block of the
+// state in LDS.
+constexpr int kSlice = 16;
+constexpr int kScanThreads = 256;
+
+__global__ __launch_bounds__(kScanThreads) void ordered_chunk_scan_kernel(OrdArgs a) {
+  __shared__ __align__(16) float Ss[kD][kSlice];
+  __shared__ __align__(16) float vn[kC][kSlice];
+  const int h = blockIdx.x / (kD / kSlice);
+  const int v0 = (blockIdx.x % (kD / kSlice)) * kSlice;
+  const int tid = threadIdx.x;
   float* w = head_ws(a, h);
   const float* qs = w;
   const float* ks = w + (size_t)a.total * kD;
-  const float* vs = w + (size_t)2 * a.total * kD;
-  float* solved = w + (size_t)3 * a.total * kD;
-  float* kcd = solved + kC * kD;
-  float* vnew = kcd + kC * kD;
-  float* inter = vnew + kC * kD;
   float* S = a.state + (size_t)h * kD * kD;
-  for (int i = tid; i < kD * kD; i += kThreads) S[i] = a.init ? a.init[(size_t)h * kD * kD + i] : 0.0f;
+  for (int i = tid; i < kD * kSlice; i += kScanThreads) {
+    const int kd = i / kSlice, j = i % kSlice;
+    Ss[kd][j] = a.init ? a.init[(size_t)h * kD * kD + kd * kD + v0 + j] : 0.0f;
+  }
+  // phase A/B mapping: row r of the chunk, 4 columns vq*4..vq*4+3 of the slice
+  const int r = tid >> 2, vq = tid & 3;
+  // phase C mapping: state row kd, 8 columns vh*8..vh*8+7 of the slice
+  const int kd = tid >> 1, vh = tid & 1;
   const int nchunks = a.total / kC;
   for (int ci = 0; ci < nchunks; ++ci) {
     const int base = ci * kC;
     const float* qc = qs + (size_t)base * kD;
     const float* kc = ks + (size_t)base * kD;
-    const float* vc = vs + (size_t)base * kD;
+    const float* cw = chunk_ws(a, h, ci);
+    const float* solved = cw;
+    const float* kcd = cw + kC * kD;
+    const float* local = cw + 2 * kC * kD;
+    const float* eg = local + kC * kC;
+    const float* wlast = eg + kC;
     __syncthreads();
-    if (tid == 0) {  // :137-151
-      float running = 0.0f;
-      for (int t = 0; t < kC; ++t) {
-        const int tok = base + t;
-        const float gt = tok < a.T ? a.g[(size_t)h * a.T + tok] : 0.0f;
-        gcum[t] = running + gt;
-        running = gcum[t];
-        bc[t] = tok < a.T ? a.beta[(size_t)h * a.T + tok] : 0.0f;
-      }
-    }
-    __syncthreads();
-    if (tid < kC) {
-      eg[tid] = spk::expf_det(gcum[tid]);
-      wlast[tid] = spk::expf_det(gcum[kC - 1] - gcum[tid]);
-    }
-    for (int i = tid; i < kC * kC; i += kThreads) {  // :153-159
-      const int r = i / kC, c = i % kC;
-      decay[r][c] = c <= r ? spk::expf_det(gcum[r] - gcum[c]) : 0.0f;
-    }
-    __syncthreads();
-    for (int i = tid; i < kC * kC; i += kThreads) {  // :161-170
-      const int r = i / kC, c = i % kC;
-      float val = 0.0f;
-      if (c < r) {
-        float dot = 0.0f;
-        for (int d = 0; d < kD; ++d) dot = dot + (kc[r * kD + d] * bc[r]) * kc[c * kD + d];
-        val = -dot * decay[r][c];
-      }
-      attn[r][c] = val;
-    }
-    __syncthreads();
-    for (int r = 1; r < kC; ++r) {  // :171-181 forward substitution, row by row
-      if (tid < r) old_row[tid] = attn[r][tid];
-      __syncthreads();
-      if (tid < r) {
-        const int c = tid;
-        float sum = old_row[c];
-        for (int in = 0; in < r; ++in) sum = sum + old_row[in] * attn[in][c];
-        attn[r][c] = sum;
-      }
-      __syncthreads();
-    }
-    if (tid < kC) attn[tid][tid] = attn[tid][tid] + 1.0f;  // :182-184
-    __syncthreads();
-    for (int i = tid; i < kC * kD; i += kThreads) {  // :186-202
-      const int r = i / kD, d = i % kD;
-      float sv = 0.0f, sk = 0.0f;
-      for (int c = 0; c < kC; ++c) {
-        const float coeff = attn[r][c];
-        if (coeff == 0.0f) continue;
-        const float bcol = bc[c];
-        sv = sv + coeff * (vc[c * kD + d] * bcol);
-        sk = sk + coeff * ((kc[c * kD + d] * bcol) * eg[c]);
-      }
-      solved[i] = sv;
-      kcd[i] = sk;
-    }
-    for (int i = tid; i < kC * kC; i += kThreads) {  // :204-213
-      const int r = i / kC, c = i % kC;
-      float val = 0.0f;
-      if (c <= r) {
-        float dot = 0.0f;
-        for (int d = 0; d < kD; ++d) dot = dot + qc[r * kD + d] * kc[c * kD + d];
-        val = dot * decay[r][c];
-      }
-      local[r][c] = val;
-    }
-    __syncthreads();
-    for (int i = tid; i < kC * kD; i += kThreads) {  // :215-233
-      const int r = i / kD, vd = i % kD;
+    // A (:215-233): carry = kcd[r] . S[:, vd], inter = (q[r] * eg[r]) . S[:, vd]
+    float inter[4];
+    {
       const float egr = eg[r];
-      float carry = 0.0f, it = 0.0f;
-      for (int kd = 0; kd < kD; ++kd) {
-        const float s = S[kd * kD + vd];
-        carry = carry + kcd[r * kD + kd] * s;
-        it = it + (qc[r * kD + kd] * egr) * s;
+      float carry[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) inter[j] = 0.0f;
+      for (int k4 = 0; k4 < kD; k4 += 4) {
+        const float4 kw = *reinterpret_cast<const float4*>(kcd + r * kD + k4);
+        const float4 qw = *reinterpret_cast<const float4*>(qc + r * kD + k4);
+        const float kk[4] = {kw.x, kw.y, kw.z, kw.w};
+        const float qq[4] = {qw.x, qw.y, qw.z, qw.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float4 s4 = *reinterpret_cast<const float4*>(&Ss[k4 + e][vq * 4]);
+          const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+          const float qe = qq[e] * egr;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            carry[j] = carry[j] + kk[e] * sv[j];
+            inter[j] = inter[j] + qe * sv[j];
+          }
+        }
       }
-      vnew[i] = solved[i] - carry;
-      inter[i] = it;
+      const float4 so = *reinterpret_cast<const float4*>(solved + r * kD + v0 + vq * 4);
+      const float sol[4] = {so.x, so.y, so.z, so.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vn[r][vq * 4 + j] = sol[j] - carry[j];
     }
     __syncthreads();
-    for (int i = tid; i < kC * kD; i += kThreads) {  // :235-244
-      const int r = i / kD, vd = i % kD;
-      float sum = inter[i];
-      for (int c = 0; c <= r; ++c) sum = sum + local[r][c] * vnew[c * kD + vd];
-      if (base + r < a.T) a.core[((size_t)h * a.core_head_stride + base + r) * kD + vd] = sum;
+    // B (:235-244): core[r] = inter + sum_{c <= r} local[r][c] * vnew[c]
+    {
+      float sum[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sum[j] = inter[j];
+      for (int c = 0; c <= r; ++c) {
+        const float l = local[r * kC + c];
+        const float4 v4 = *reinterpret_cast<const float4*>(&vn[c][vq * 4]);
+        sum[0] = sum[0] + l * v4.x;
+        sum[1] = sum[1] + l * v4.y;
+        sum[2] = sum[2] + l * v4.z;
+        sum[3] = sum[3] + l * v4.w;
+      }
+      if (base + r < a.T) {
+        float* o = a.core + ((size_t)h * a.core_head_stride + base + r) * kD + v0 + vq * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = sum[j];
+      }
     }
-    const float eglast = eg[kC - 1];
-    for (int i = tid; i < kD * kD; i += kThreads) {  // :246-268
-      const int kd = i / kD, vd = i % kD;
-      const float ws = S[i] * eglast;
-      float upd = 0.0f;
-      for (int r = 0; r < kC; ++r) upd = upd + (kc[r * kD + kd] * wlast[r]) * vnew[r * kD + vd];
-      S[i] = ws + upd;
+    // C (:246-268): S[kd][vd] = S * eg[63] + sum_r (k[r][kd] * wlast[r]) * vnew[r][vd]
+    {
+      const float eglast = eg[kC - 1];
+      float upd[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) upd[j] = 0.0f;
+      for (int rr = 0; rr < kC; ++rr) {
+        const float kw = kc[rr * kD + kd] * wlast[rr];
+        const float4 lo = *reinterpret_cast<const float4*>(&vn[rr][vh * 8]);
+        const float4 hi = *reinterpret_cast<const float4*>(&vn[rr][vh * 8 + 4]);
+        const float vv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) upd[j] = upd[j] + kw * vv[j];
+      }
+      // Ss row kd is read by phase A of this chunk only (before the barrier
+      // above) and written here by this thread alone
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float ws = Ss[kd][vh * 8 + j] * eglast;
+        Ss[kd][vh * 8 + j] = ws + upd[j];
+      }
     }
+  }
+  __syncthreads();
+  for (int i = tid; i < kD * kSlice; i += kScanThreads) {
+    const int k = i / kSlice, j = i % kSlice;
+    S[(size_t)k * kD + v0 + j] = Ss[k][j];
   }
 }
 
@@ -311,7 +409,7 @@ extern "C" int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t
 extern "C" size_t spk_chunk_prefill_ordered_workspace_size(int32_t num_heads, int32_t total_tokens) {
   if (num_heads <= 0 || total_tokens <= 0) return 0;
   const size_t total = ((size_t)total_tokens + kC - 1) / kC * kC;
-  return (size_t)num_heads * (3 * total * kD + 4 * kC * kD) * sizeof(float);
+  return (size_t)num_heads * head_ws_floats((int)total) * sizeof(float);
 }
 
 extern "C" int spk_chunk_prefill_ordered(const SpkChunkArgs* p, spk_stream_t stream) {
@@ -356,6 +454,9 @@ extern "C" int spk_chunk_prefill_ordered(const SpkChunkArgs* p, spk_stream_t str
   hipLaunchKernelGGL(ordered_prep_kernel, dim3((n + 127) / 128), dim3(128), 0, s, a);
   int rc = spk::check_launch("spk_chunk_prefill_ordered (prep)");
   if (rc) return rc;
-  hipLaunchKernelGGL(ordered_chunk_kernel, dim3(a.H), dim3(kThreads), 0, s, a);
-  return spk::check_launch("spk_chunk_prefill_ordered");
+  hipLaunchKernelGGL(ordered_chunk_prep_kernel, dim3(a.total / kC, a.H), dim3(kThreads), 0, s, a);
+  rc = spk::check_launch("spk_chunk_prefill_ordered (chunk prep)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(ordered_chunk_scan_kernel, dim3(a.H * (kD / kSlice)), dim3(kScanThreads), 0, s, a);
+  return spk::check_launch("spk_chunk_prefill_ordered (scan)");
 }

@@ -400,7 +400,8 @@ def test_matvec_rows_bitexact(dev, rows, out_dim, in_dim, res):
 
 
 @pytest.mark.parametrize("T,f16,l2,init", [(104, False, False, False), (64, True, False, True),
-                                          (1, False, True, True), (200, True, False, True)])
+                                          (1, False, True, True), (200, True, False, True),
+                                          (520, True, True, True)])
 def test_chunk_prefill_ordered_bitexact(dev, oracle, T, f16, l2, init):
     """spk_chunk_prefill_ordered: run_deltanet_chunk_rule's loops with the
     deterministic exp, bit-identical to orc_chunk_rule_det."""
