@@ -38,6 +38,15 @@ struct Acc16 {
   float v[16];
 };
 
+__device__ __forceinline__ void unpack8h(const uint4& u, float* f) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = spk::h2f((uint16_t)(w[i] & 0xffffu));
+    f[2 * i + 1] = spk::h2f((uint16_t)(w[i] >> 16));
+  }
+}
+
 // Leaf i (in bit-reversed order: span l = bitrev6(i)) of the 64-span tree for
 // the thread's 4 x 4 outputs.  The tree s[l] += s[l+32], ..., s[l] += s[l+1]
 // pairs spans whose indices differ in bit 5 first; visiting spans in
@@ -102,6 +111,112 @@ __global__ __launch_bounds__(256) void matvec_rows_kernel(RowsArgs a) {
         uint16_t o = spk::f2h(s.v[p * 4 + q]);
         if (a.R) o = spk::f2h(spk::h2f(a.R[(long long)t * a.ldy + r]) + spk::h2f(o));
         a.Y[(long long)t * a.ldy + r] = o;
+      }
+    }
+}
+
+// Matrix-core form (in_dim % 512 == 0).  v_mfma_f32_16x16x1_4b_f32 adds one
+// product per output per instruction, C + a*b with a single rounding; with
+// fp16-valued operands the product is exact, so a chain of these is the
+// sequential fma chain bit for bit.  Its 4 blocks run spans l, l+16, l+32 and
+// l+48 together (lane = block * 16 + row/column): blocks 0+2 and 1+3 are the
+// tree's stride-32 pairs and their sum its stride-16 pair, all register-wise
+// adds (every block keeps row 4*(lane/16) + k, column lane%16 in register
+// 4*block + k).  The 16 values of l are visited in 4-bit bit-reversed order
+// and merged like a binary counter, which reproduces strides 8..1.  One wave
+// computes TR x TT tiles of 16 W rows x 16 prompt rows; operands are read
+// straight from global memory (L1/L2), 8 halves per lane per load, one chunk
+// of 8 steps ahead.
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+template <int S, int TR, int TT>
+__global__ __launch_bounds__(256) void matvec_rows_mfma_kernel(RowsArgs a, int n_tt, int n_tiles) {
+  const int lane = threadIdx.x & 63;
+  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= n_tiles) return;  // whole wave; the kernel has no barrier
+  const int r0 = (tile / n_tt) * 16 * TR, t0 = (tile % n_tt) * 16 * TT;
+  const int blk = lane >> 4, li = lane & 15;
+  constexpr int C = S / 8;  // 16-byte chunks per span
+  const uint16_t* wrow[TR];
+  const uint16_t* xrow[TT];
+#pragma unroll
+  for (int i = 0; i < TR; ++i) wrow[i] = a.W + (size_t)min(r0 + 16 * i + li, a.out_dim - 1) * a.in_dim;
+#pragma unroll
+  for (int j = 0; j < TT; ++j) xrow[j] = a.X + (size_t)min(t0 + 16 * j + li, a.rows - 1) * a.ldx;
+  auto span_of = [&](int v) { return (int)(__builtin_bitreverse32((uint32_t)v) >> 28) + 16 * blk; };
+  uint4 nw[TR], nx[TT];
+  auto issue = [&](int v, int c) {
+    const int off = span_of(v) * S + 8 * c;
+#pragma unroll
+    for (int i = 0; i < TR; ++i) nw[i] = *reinterpret_cast<const uint4*>(wrow[i] + off);
+#pragma unroll
+    for (int j = 0; j < TT; ++j) nx[j] = *reinterpret_cast<const uint4*>(xrow[j] + off);
+  };
+  float stack[4][TR * TT * 4];
+  float cur[TR * TT * 4];
+  issue(0, 0);
+#pragma unroll 1
+  for (int v = 0; v < 16; ++v) {
+    v16f acc[TR][TT];
+#pragma unroll
+    for (int i = 0; i < TR; ++i)
+#pragma unroll
+      for (int j = 0; j < TT; ++j) acc[i][j] = v16f{};
+    for (int c = 0; c < C; ++c) {
+      float wf[TR][8], xf[TT][8];
+#pragma unroll
+      for (int i = 0; i < TR; ++i) unpack8h(nw[i], wf[i]);
+#pragma unroll
+      for (int j = 0; j < TT; ++j) unpack8h(nx[j], xf[j]);
+      if (c + 1 < C)
+        issue(v, c + 1);
+      else if (v + 1 < 16)
+        issue(v + 1, 0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int i = 0; i < TR; ++i)
+#pragma unroll
+          for (int j = 0; j < TT; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x1f32(wf[i][e], xf[j][e], acc[i][j], 0, 0, 0);
+    }
+    // (P_l + P_{l+32}) + (P_{l+16} + P_{l+48})
+#pragma unroll
+    for (int i = 0; i < TR; ++i)
+#pragma unroll
+      for (int j = 0; j < TT; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          cur[(i * TT + j) * 4 + k] = (acc[i][j][k] + acc[i][j][8 + k]) + (acc[i][j][4 + k] + acc[i][j][12 + k]);
+    // binary-counter merge: visits v and v ^ (1 << lev) pair at level lev
+    bool carry = true;
+#pragma unroll
+    for (int lev = 0; lev < 4; ++lev) {
+      if (carry) {
+        if ((v >> lev) & 1) {
+#pragma unroll
+          for (int q = 0; q < TR * TT * 4; ++q) cur[q] = stack[lev][q] + cur[q];
+        } else {
+#pragma unroll
+          for (int q = 0; q < TR * TT * 4; ++q) stack[lev][q] = cur[q];
+          carry = false;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TR; ++i)
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+      const int t = t0 + 16 * j + li;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = r0 + 16 * i + 4 * blk + k;
+        if (r < a.out_dim && t < a.rows) {
+          uint16_t o = spk::f2h(cur[(i * TT + j) * 4 + k]);
+          if (a.R) o = spk::f2h(spk::h2f(a.R[(long long)t * a.ldy + r]) + spk::h2f(o));
+          a.Y[(long long)t * a.ldy + r] = o;
+        }
       }
     }
 }
@@ -401,8 +516,28 @@ extern "C" int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t
   if (ldx < in_dim || ldy < out_dim) return spk::fail(SPK_ERR_SHAPE, "spk_matvec_f16_rows: leading dimensions");
   if (residual == X || Y == X) return spk::fail(SPK_ERR_ARG, "spk_matvec_f16_rows: output aliases the input");
   RowsArgs a{W, X, (long long)ldx, Y, (long long)ldy, residual, rows, out_dim, in_dim, in_dim / 64};
+  hipStream_t s = spk::to_hip(stream);
+  const int S = in_dim / 64;
+  if ((S == 16 || S == 32 || S == 56) && spk::aligned(W, 16) && spk::aligned(X, 16) && ldx % 8 == 0) {
+    // 2 x 2 tiles per wave unless that leaves SIMDs idle (1024 on the chip)
+    const int n_rt2 = (out_dim + 31) / 32, n_tt = (rows + 31) / 32;
+    const bool wide = (long long)n_rt2 * n_tt >= 1024;
+    const int n_rt = wide ? n_rt2 : (out_dim + 15) / 16;
+    const int n_tiles = n_rt * n_tt;
+    const dim3 grid((n_tiles + 3) / 4);
+#define SPK_MVR(s_, tr_)                                                                                      hipLaunchKernelGGL((matvec_rows_mfma_kernel<s_, tr_, 2>), grid, dim3(256), 0, s, a, n_tt, n_tiles)
+    if (S == 16) {
+      if (wide) SPK_MVR(16, 2); else SPK_MVR(16, 1);
+    } else if (S == 32) {
+      if (wide) SPK_MVR(32, 2); else SPK_MVR(32, 1);
+    } else {
+      if (wide) SPK_MVR(56, 2); else SPK_MVR(56, 1);
+    }
+#undef SPK_MVR
+    return spk::check_launch("spk_matvec_f16_rows");
+  }
   dim3 grid((out_dim + kTile - 1) / kTile, (rows + kTile - 1) / kTile);
-  hipLaunchKernelGGL(matvec_rows_kernel, grid, dim3(256), 0, spk::to_hip(stream), a);
+  hipLaunchKernelGGL(matvec_rows_kernel, grid, dim3(256), 0, s, a);
   return spk::check_launch("spk_matvec_f16_rows");
 }
 
