@@ -221,6 +221,116 @@ __global__ __launch_bounds__(256) void matvec_rows_mfma_kernel(RowsArgs a, int n
     }
 }
 
+// in_dim == 1024 (S = 16, a span is 32 B): the same leaves and tree, with
+// operands staged through LDS four leaves at a time.  Leaves v, v+4, v+8,
+// v+12 (v < 4) are l = L..L+3 with L = bitrev4(v), i.e. spans L..L+3 (+16b
+// per block): four whole 128-byte lines of every row, loaded coalesced.  The
+// groups arrive in the order L = 0, 8, 4, 12 and are merged as the tree
+// pairs them: s[m] + s[m+8] once L = 8 is in, s[4+m] + s[12+m] once L = 12 is
+// in, then strides 4, 2, 1.  Workgroup tile: 64 W rows x 32 prompt rows, one
+// 32 x 16 (2 x 1 MFMA tiles) per wave; three workgroups per CU.
+constexpr int kGrpLd = 264;  // halves per LDS row: 4 blocks x 64 + 8 pad (row starts 4 banks apart)
+constexpr int kGrpRows = 64, kGrpToks = 32;
+
+__global__ __launch_bounds__(256, 3) void matvec_rows_grp_kernel(RowsArgs a) {
+  __shared__ __align__(16) uint16_t Ws[kGrpRows][kGrpLd];
+  __shared__ __align__(16) uint16_t Xs[kGrpToks][kGrpLd];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int blk = lane >> 4, li = lane & 15;
+  const int r0 = blockIdx.x * kGrpRows, t0 = blockIdx.y * kGrpToks;
+  const int wr = 32 * (wave & 1), wt = 16 * (wave >> 1);  // wave tile inside the workgroup tile
+  float H[4][8], G[4][8];
+#pragma unroll 1
+  for (int g = 0; g < 4; ++g) {
+    const int L = (int)(__builtin_bitreverse32((uint32_t)g) >> 28);
+    __syncthreads();  // the previous group's operand reads are done
+    // rows x 4 blocks x 8 pieces of 16 B: 8 W + 4 X pieces per thread
+    uint4 pw[8], px[4];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int pc = tid + 256 * k;
+      const int row = pc >> 5, b = (pc >> 3) & 3, q = pc & 7;
+      pw[k] = *reinterpret_cast<const uint4*>(a.W + (size_t)min(r0 + row, a.out_dim - 1) * 1024 +
+                                              (16 * b + L) * 16 + 8 * q);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int pc = tid + 256 * k;
+      const int row = pc >> 5, b = (pc >> 3) & 3, q = pc & 7;
+      px[k] = *reinterpret_cast<const uint4*>(a.X + (size_t)min(t0 + row, a.rows - 1) * a.ldx +
+                                              (16 * b + L) * 16 + 8 * q);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int pc = tid + 256 * k;
+      *reinterpret_cast<uint4*>(&Ws[pc >> 5][64 * ((pc >> 3) & 3) + 8 * (pc & 7)]) = pw[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int pc = tid + 256 * k;
+      *reinterpret_cast<uint4*>(&Xs[pc >> 5][64 * ((pc >> 3) & 3) + 8 * (pc & 7)]) = px[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {  // leaf l = L + m: span L + m (+16 per block)
+      v16f acc[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) acc[i] = v16f{};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float wf[2][8], xf[8];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          unpack8h(*reinterpret_cast<const uint4*>(&Ws[wr + 16 * i + li][64 * blk + 16 * m + 8 * c]), wf[i]);
+        unpack8h(*reinterpret_cast<const uint4*>(&Xs[wt + li][64 * blk + 16 * m + 8 * c]), xf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x1f32(wf[i][e], xf[e], acc[i], 0, 0, 0);
+      }
+      float R[8];  // (P_l + P_{l+32}) + (P_{l+16} + P_{l+48})
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          R[i * 4 + k] = (acc[i][k] + acc[i][8 + k]) + (acc[i][4 + k] + acc[i][12 + k]);
+      if (g == 0) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) H[m][q] = R[q];  // s[m]
+      } else if (g == 1) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) H[m][q] = H[m][q] + R[q];  // s[m] + s[m+8]
+      } else if (g == 2) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) G[m][q] = R[q];  // s[4+m]
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) G[m][q] = G[m][q] + R[q];  // s[4+m] + s[12+m]
+      }
+    }
+  }
+  float out[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float b0 = H[0][q] + G[0][q], b1 = H[1][q] + G[1][q];  // stride 4
+    const float b2 = H[2][q] + G[2][q], b3 = H[3][q] + G[3][q];
+    out[q] = (b0 + b2) + (b1 + b3);  // strides 2, 1
+  }
+  const int t = t0 + wt + li;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = r0 + wr + 16 * i + 4 * blk + k;
+      if (r < a.out_dim && t < a.rows) {
+        uint16_t o = spk::f2h(out[i * 4 + k]);
+        if (a.R) o = spk::f2h(spk::h2f(a.R[(long long)t * a.ldy + r]) + spk::h2f(o));
+        a.Y[(long long)t * a.ldy + r] = o;
+      }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // spk_chunk_prefill_ordered
 // ---------------------------------------------------------------------------
@@ -518,7 +628,13 @@ extern "C" int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t
   RowsArgs a{W, X, (long long)ldx, Y, (long long)ldy, residual, rows, out_dim, in_dim, in_dim / 64};
   hipStream_t s = spk::to_hip(stream);
   const int S = in_dim / 64;
-  if ((S == 16 || S == 32 || S == 56) && spk::aligned(W, 16) && spk::aligned(X, 16) && ldx % 8 == 0) {
+  const bool vec_ok = spk::aligned(W, 16) && spk::aligned(X, 16) && ldx % 8 == 0;
+  if (S == 16 && vec_ok && (long long)((out_dim + kGrpRows - 1) / kGrpRows) * ((rows + kGrpToks - 1) / kGrpToks) >= 256) {
+    const dim3 grid((out_dim + kGrpRows - 1) / kGrpRows, (rows + kGrpToks - 1) / kGrpToks);
+    hipLaunchKernelGGL(matvec_rows_grp_kernel, grid, dim3(256), 0, s, a);
+    return spk::check_launch("spk_matvec_f16_rows");
+  }
+  if ((S == 16 || S == 32 || S == 56) && vec_ok) {
     // 2 x 2 tiles per wave unless that leaves SIMDs idle (1024 on the chip)
     const int n_rt2 = (out_dim + 31) / 32, n_tt = (rows + 31) / 32;
     const bool wide = (long long)n_rt2 * n_tt >= 1024;
