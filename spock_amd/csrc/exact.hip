@@ -361,9 +361,10 @@ __device__ __forceinline__ float ld_in(const void* p, bool f16, long long i) {
 // wlast [64].
 constexpr int kChunkWs = 2 * kC * kD + kC * kC + 2 * kC;
 
-// Per head: qs, ks, vs [total][128], then kChunkWs floats per chunk.
+// Per head: the padded, normalised and q-scaled qs, ks [total][128], then
+// kChunkWs floats per chunk.
 __host__ __device__ __forceinline__ size_t head_ws_floats(int total) {
-  return (size_t)3 * total * kD + (size_t)(total / kC) * kChunkWs;
+  return (size_t)2 * total * kD + (size_t)(total / kC) * kChunkWs;
 }
 
 __device__ __forceinline__ float* head_ws(const OrdArgs& a, int h) {
@@ -371,63 +372,44 @@ __device__ __forceinline__ float* head_ws(const OrdArgs& a, int h) {
 }
 
 __device__ __forceinline__ float* chunk_ws(const OrdArgs& a, int h, int ci) {
-  return head_ws(a, h) + (size_t)3 * a.total * kD + (size_t)ci * kChunkWs;
-}
-
-// Padded, optionally L2-normalised (deltanet_chunk.cpp:27-39, 78-85) and
-// q-scaled (:87-88) copies of q, k, v; one thread per (head, token).
-__global__ void ordered_prep_kernel(OrdArgs a) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= a.H * a.total) return;
-  const int h = i / a.total, t = i - (i / a.total) * a.total;
-  float* w = head_ws(a, h);
-  float* qs = w + (size_t)t * kD;
-  float* ks = w + (size_t)a.total * kD + (size_t)t * kD;
-  float* vs = w + (size_t)2 * a.total * kD + (size_t)t * kD;
-  if (t >= a.T) {
-    for (int d = 0; d < kD; ++d) qs[d] = ks[d] = vs[d] = 0.0f;
-    return;
-  }
-  const long long src = ((long long)h * a.T + t) * kD;
-  for (int d = 0; d < kD; ++d) {
-    qs[d] = ld_in(a.q, a.f16, src + d);
-    ks[d] = ld_in(a.k, a.f16, src + d);
-    vs[d] = ld_in(a.v, a.f16, src + d);
-  }
-  if (a.l2) {
-    float sq = 0.0f, sk = 0.0f;
-    for (int d = 0; d < kD; ++d) {
-      sq = sq + qs[d] * qs[d];
-      sk = sk + ks[d] * ks[d];
-    }
-    const float iq = 1.0f / __builtin_sqrtf(sq + 1e-6f), ik = 1.0f / __builtin_sqrtf(sk + 1e-6f);
-    for (int d = 0; d < kD; ++d) {
-      qs[d] = qs[d] * iq;
-      ks[d] = ks[d] * ik;
-    }
-  }
-  for (int d = 0; d < kD; ++d) qs[d] = qs[d] * a.q_scale;
+  return head_ws(a, h) + (size_t)2 * a.total * kD + (size_t)ci * kChunkWs;
 }
 
 // Chunk body, part 1 (run_deltanet_chunk_rule's loops that do not read the
-// state): one workgroup per (chunk, head), every chunk at once.  Each phase is
-// split over its independent outputs; every reduction runs in the reference's
-// sequential order.
+// state): one workgroup per (chunk, head), every chunk at once.  The chunk's
+// q, k, v rows are loaded once into LDS, padded with zeros past T, optionally
+// L2-normalised (deltanet_chunk.cpp:27-39, 78-85: sequential sum of squares,
+// then x * (1 / sqrt(sum + 1e-6))) and q-scaled (:87-88); q and k are also
+// written out for the state scan.  Each phase is split over its independent
+// outputs; every reduction runs in the reference's sequential order.
+constexpr int kRowLd = kD + 1;  // LDS row pitch: a column walk over rows is conflict-free
+
 __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a) {
-  __shared__ float gcum[kC], bc[kC], eg[kC], old_row[kC];
+  __shared__ float qs[kC][kRowLd], ks[kC][kRowLd], vs[kC][kRowLd];
+  __shared__ float gcum[kC], bc[kC], eg[kC], old_row[kC], inv_q[kC], inv_k[kC];
   __shared__ float decay[kC][kC + 1], attn[kC][kC + 1];
   const int ci = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   float* w = head_ws(a, h);
   const int base = ci * kC;
-  const float* qc = w + (size_t)base * kD;
-  const float* kc = w + (size_t)a.total * kD + (size_t)base * kD;
-  const float* vc = w + (size_t)2 * a.total * kD + (size_t)base * kD;
   float* cw = chunk_ws(a, h, ci);
   float* solved = cw;
   float* kcd = cw + kC * kD;
   float* local = cw + 2 * kC * kD;
   float* egw = local + kC * kC;
   float* wlast = egw + kC;
+  for (int i = tid; i < kC * kD; i += kThreads) {
+    const int t = i / kD, d = i % kD, tok = base + t;
+    float q = 0.0f, k = 0.0f, v = 0.0f;
+    if (tok < a.T) {
+      const long long src = ((long long)h * a.T + tok) * kD + d;
+      q = ld_in(a.q, a.f16, src);
+      k = ld_in(a.k, a.f16, src);
+      v = ld_in(a.v, a.f16, src);
+    }
+    qs[t][d] = q;
+    ks[t][d] = k;
+    vs[t][d] = v;
+  }
   if (tid == 0) {  // :137-151
     float running = 0.0f;
     for (int t = 0; t < kC; ++t) {
@@ -439,6 +421,29 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
     }
   }
   __syncthreads();
+  if (a.l2) {
+    if (tid < 2 * kC) {
+      const int t = tid & (kC - 1);
+      const float(*x)[kRowLd] = tid < kC ? qs : ks;
+      float sq = 0.0f;
+      for (int d = 0; d < kD; ++d) sq = sq + x[t][d] * x[t][d];
+      (tid < kC ? inv_q : inv_k)[t] = 1.0f / __builtin_sqrtf(sq + 1e-6f);
+    }
+    __syncthreads();
+  }
+  for (int i = tid; i < kC * kD; i += kThreads) {
+    const int t = i / kD, d = i % kD;
+    float q = qs[t][d], k = ks[t][d];
+    if (a.l2) {
+      q = q * inv_q[t];
+      k = k * inv_k[t];
+    }
+    q = q * a.q_scale;
+    qs[t][d] = q;
+    ks[t][d] = k;
+    w[(size_t)(base + t) * kD + d] = q;
+    w[(size_t)a.total * kD + (size_t)(base + t) * kD + d] = k;
+  }
   if (tid < kC) {
     eg[tid] = spk::expf_det(gcum[tid]);
     egw[tid] = eg[tid];
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
     float val = 0.0f;
     if (c < r) {
       float dot = 0.0f;
-      for (int d = 0; d < kD; ++d) dot = dot + (kc[r * kD + d] * bc[r]) * kc[c * kD + d];
+      for (int d = 0; d < kD; ++d) dot = dot + (ks[r][d] * bc[r]) * ks[c][d];
       val = -dot * decay[r][c];
     }
     attn[r][c] = val;
@@ -464,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
     float val = 0.0f;
     if (c <= r) {
       float dot = 0.0f;
-      for (int d = 0; d < kD; ++d) dot = dot + qc[r * kD + d] * kc[c * kD + d];
+      for (int d = 0; d < kD; ++d) dot = dot + qs[r][d] * ks[c][d];
       val = dot * decay[r][c];
     }
     local[i] = val;
@@ -490,8 +495,8 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
       const float coeff = attn[r][c];
       if (coeff == 0.0f) continue;
       const float bcol = bc[c];
-      sv = sv + coeff * (vc[c * kD + d] * bcol);
-      sk = sk + coeff * ((kc[c * kD + d] * bcol) * eg[c]);
+      sv = sv + coeff * (vs[c][d] * bcol);
+      sk = sk + coeff * ((ks[c][d] * bcol) * eg[c]);
     }
     solved[i] = sv;
     kcd[i] = sk;
@@ -701,12 +706,8 @@ extern "C" int spk_chunk_prefill_ordered(const SpkChunkArgs* p, spk_stream_t str
   a.state = p->out_state;
   a.ws = static_cast<float*>(p->workspace);
   hipStream_t s = spk::to_hip(stream);
-  const int n = a.H * a.total;
-  hipLaunchKernelGGL(ordered_prep_kernel, dim3((n + 127) / 128), dim3(128), 0, s, a);
-  int rc = spk::check_launch("spk_chunk_prefill_ordered (prep)");
-  if (rc) return rc;
   hipLaunchKernelGGL(ordered_chunk_prep_kernel, dim3(a.total / kC, a.H), dim3(kThreads), 0, s, a);
-  rc = spk::check_launch("spk_chunk_prefill_ordered (chunk prep)");
+  int rc = spk::check_launch("spk_chunk_prefill_ordered (chunk prep)");
   if (rc) return rc;
   hipLaunchKernelGGL(ordered_chunk_scan_kernel, dim3(a.H * (kD / kSlice)), dim3(kScanThreads), 0, s, a);
   return spk::check_launch("spk_chunk_prefill_ordered (scan)");
