@@ -382,13 +382,18 @@ __device__ __forceinline__ float* chunk_ws(const OrdArgs& a, int h, int ci) {
 // then x * (1 / sqrt(sum + 1e-6))) and q-scaled (:87-88); q and k are also
 // written out for the state scan.  Each phase is split over its independent
 // outputs; every reduction runs in the reference's sequential order.
-constexpr int kRowLd = kD + 1;  // LDS row pitch: a column walk over rows is conflict-free
+constexpr int kRowLd = kD + 4;  // LDS row pitch: 16-byte reads, rows 4 banks apart
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
 __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a) {
-  __shared__ float qs[kC][kRowLd], ks[kC][kRowLd], vs[kC][kRowLd];
-  __shared__ float gcum[kC], bc[kC], eg[kC], old_row[kC], inv_q[kC], inv_k[kC];
+  __shared__ __align__(16) float qs[kC][kRowLd];
+  __shared__ __align__(16) float ks[kC][kRowLd];
+  __shared__ __align__(16) float vs[kC][kRowLd];
+  __shared__ float gcum[kC], bc[kC], eg[kC], inv_q[kC], inv_k[kC];
   __shared__ float decay[kC][kC + 1], attn[kC][kC + 1];
   const int ci = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   float* w = head_ws(a, h);
   const int base = ci * kC;
   float* cw = chunk_ws(a, h, ci);
@@ -424,9 +429,15 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
   if (a.l2) {
     if (tid < 2 * kC) {
       const int t = tid & (kC - 1);
-      const float(*x)[kRowLd] = tid < kC ? qs : ks;
+      const float* x = tid < kC ? qs[t] : ks[t];
       float sq = 0.0f;
-      for (int d = 0; d < kD; ++d) sq = sq + x[t][d] * x[t][d];
+      for (int d = 0; d < kD; d += 4) {
+        const float4 v = ld4(x + d);
+        sq = sq + v.x * v.x;
+        sq = sq + v.y * v.y;
+        sq = sq + v.z * v.z;
+        sq = sq + v.w * v.w;
+      }
       (tid < kC ? inv_q : inv_k)[t] = 1.0f / __builtin_sqrtf(sq + 1e-6f);
     }
     __syncthreads();
@@ -454,52 +465,68 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
     decay[r][c] = c <= r ? spk::expf_det(gcum[r] - gcum[c]) : 0.0f;
   }
   __syncthreads();
-  for (int i = tid; i < kC * kC; i += kThreads) {  // :161-170
-    const int r = i / kC, c = i % kC;
-    float val = 0.0f;
-    if (c < r) {
-      float dot = 0.0f;
-      for (int d = 0; d < kD; ++d) dot = dot + (ks[r][d] * bc[r]) * ks[c][d];
-      val = -dot * decay[r][c];
+  // :161-170 (attn, strictly lower) and :204-213 (local, lower): lane = column
+  // c, wave-uniform row r; the d = 0..127 sums in order, 4 per 16-byte read.
+  for (int r = wave; r < kC; r += kThreads / 64) {
+    const int c = lane;
+    const float br = bc[r];
+    float da = 0.0f, dl = 0.0f;
+    for (int d = 0; d < kD; d += 4) {
+      const float4 kr = ld4(&ks[r][d]), qr = ld4(&qs[r][d]), kc4 = ld4(&ks[c][d]);
+      da = da + (kr.x * br) * kc4.x;
+      da = da + (kr.y * br) * kc4.y;
+      da = da + (kr.z * br) * kc4.z;
+      da = da + (kr.w * br) * kc4.w;
+      dl = dl + qr.x * kc4.x;
+      dl = dl + qr.y * kc4.y;
+      dl = dl + qr.z * kc4.z;
+      dl = dl + qr.w * kc4.w;
     }
-    attn[r][c] = val;
-  }
-  for (int i = tid; i < kC * kC; i += kThreads) {  // :204-213
-    const int r = i / kC, c = i % kC;
-    float val = 0.0f;
-    if (c <= r) {
-      float dot = 0.0f;
-      for (int d = 0; d < kD; ++d) dot = dot + qs[r][d] * ks[c][d];
-      val = dot * decay[r][c];
-    }
-    local[i] = val;
+    attn[r][c] = c < r ? -da * decay[r][c] : 0.0f;
+    local[r * kC + c] = c <= r ? dl * decay[r][c] : 0.0f;
   }
   __syncthreads();
-  for (int r = 1; r < kC; ++r) {  // :171-181 forward substitution, row by row
-    if (tid < r) old_row[tid] = attn[r][tid];
-    __syncthreads();
-    if (tid < r) {
-      const int c = tid;
-      float sum = old_row[c];
-      for (int in = 0; in < r; ++in) sum = sum + old_row[in] * attn[in][c];
-      attn[r][c] = sum;
+  // :171-181 forward substitution.  Row r is updated from its original values
+  // (the reference's old_row) and rows < r already updated; lane c keeps its
+  // column of the updated matrix in registers, so the original rows stay in
+  // LDS untouched until the end and no barrier is needed between rows.
+  if (wave == 0) {
+    const int c = lane;
+    float col[kC];
+#pragma unroll
+    for (int in = 0; in < kC; ++in) col[in] = attn[in][c];
+#pragma unroll
+    for (int r = 1; r < kC; ++r) {
+      if (c < r) {
+        float sum = col[r];
+#pragma unroll
+        for (int in = 0; in < r; ++in) sum = sum + attn[r][in] * col[in];
+        col[r] = sum;
+      }
     }
-    __syncthreads();
+    // (one wave: its LDS reads above complete before the writes below)
+#pragma unroll
+    for (int in = 0; in < kC; ++in) attn[in][c] = in == c ? col[in] + 1.0f : col[in];  // :182-184 +I
   }
-  if (tid < kC) attn[tid][tid] = attn[tid][tid] + 1.0f;  // :182-184
   __syncthreads();
-  for (int i = tid; i < kC * kD; i += kThreads) {  // :186-202
-    const int r = i / kD, d = i % kD;
-    float sv = 0.0f, sk = 0.0f;
+  // :186-202: thread = (row r, 4 consecutive d), the c = 0..63 sums in order
+  for (int u = tid; u < kC * (kD / 4); u += kThreads) {
+    const int r = u / (kD / 4), d = (u % (kD / 4)) * 4;
+    float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c = 0; c < kC; ++c) {
       const float coeff = attn[r][c];
       if (coeff == 0.0f) continue;
-      const float bcol = bc[c];
-      sv = sv + coeff * (vs[c][d] * bcol);
-      sk = sk + coeff * ((ks[c][d] * bcol) * eg[c]);
+      const float bcol = bc[c], egc = eg[c];
+      const float4 v4 = ld4(&vs[c][d]), k4 = ld4(&ks[c][d]);
+      const float vv[4] = {v4.x, v4.y, v4.z, v4.w}, kk[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sv[j] = sv[j] + coeff * (vv[j] * bcol);
+        sk[j] = sk[j] + coeff * ((kk[j] * bcol) * egc);
+      }
     }
-    solved[i] = sv;
-    kcd[i] = sk;
+    *reinterpret_cast<float4*>(solved + r * kD + d) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    *reinterpret_cast<float4*>(kcd + r * kD + d) = make_float4(sk[0], sk[1], sk[2], sk[3]);
   }
 }
 
