@@ -402,34 +402,58 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
   float* local = cw + 2 * kC * kD;
   float* egw = local + kC * kC;
   float* wlast = egw + kC;
-  for (int i = tid; i < kC * kD; i += kThreads) {
-    const int t = i / kD, d = i % kD, tok = base + t;
-    float q = 0.0f, k = 0.0f, v = 0.0f;
-    if (tok < a.T) {
-      const long long src = ((long long)h * a.T + tok) * kD + d;
-      q = ld_in(a.q, a.f16, src);
-      k = ld_in(a.k, a.f16, src);
-      v = ld_in(a.v, a.f16, src);
+  // q, k, v rows of the chunk: 4 elements per piece, every load issued before
+  // any use (rows past T read row T-1 and stage zeros)
+  {
+    constexpr int kPieces = kC * kD / 4 / kThreads;  // 4
+    float4 lq[kPieces], lk[kPieces], lv[kPieces];
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      const int pc = tid + kThreads * j, t = pc / (kD / 4), d = (pc % (kD / 4)) * 4;
+      const long long src = ((long long)h * a.T + min(base + t, a.T - 1)) * kD + d;
+      if (a.f16) {
+        const uint2 uq = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.q) + src);
+        const uint2 uk = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.k) + src);
+        const uint2 uv = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.v) + src);
+        lq[j] = make_float4(spk::h2f(uq.x & 0xffffu), spk::h2f(uq.x >> 16), spk::h2f(uq.y & 0xffffu), spk::h2f(uq.y >> 16));
+        lk[j] = make_float4(spk::h2f(uk.x & 0xffffu), spk::h2f(uk.x >> 16), spk::h2f(uk.y & 0xffffu), spk::h2f(uk.y >> 16));
+        lv[j] = make_float4(spk::h2f(uv.x & 0xffffu), spk::h2f(uv.x >> 16), spk::h2f(uv.y & 0xffffu), spk::h2f(uv.y >> 16));
+      } else {
+        lq[j] = ld4(static_cast<const float*>(a.q) + src);
+        lk[j] = ld4(static_cast<const float*>(a.k) + src);
+        lv[j] = ld4(static_cast<const float*>(a.v) + src);
+      }
     }
-    qs[t][d] = q;
-    ks[t][d] = k;
-    vs[t][d] = v;
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      const int pc = tid + kThreads * j, t = pc / (kD / 4), d = (pc % (kD / 4)) * 4;
+      const bool live = base + t < a.T;
+      const float4 q = lq[j], k = lk[j], v = lv[j];
+      *reinterpret_cast<float4*>(&qs[t][d]) =
+          make_float4(live ? q.x : 0.0f, live ? q.y : 0.0f, live ? q.z : 0.0f, live ? q.w : 0.0f);
+      *reinterpret_cast<float4*>(&ks[t][d]) =
+          make_float4(live ? k.x : 0.0f, live ? k.y : 0.0f, live ? k.z : 0.0f, live ? k.w : 0.0f);
+      *reinterpret_cast<float4*>(&vs[t][d]) =
+          make_float4(live ? v.x : 0.0f, live ? v.y : 0.0f, live ? v.z : 0.0f, live ? v.w : 0.0f);
+    }
   }
-  if (tid == 0) {  // :137-151
-    float running = 0.0f;
-    for (int t = 0; t < kC; ++t) {
-      const int tok = base + t;
-      const float gt = tok < a.T ? a.g[(size_t)h * a.T + tok] : 0.0f;
-      gcum[t] = running + gt;
-      running = gcum[t];
-      bc[t] = tok < a.T ? a.beta[(size_t)h * a.T + tok] : 0.0f;
-    }
+  if (tid < kC) {
+    const int tok = base + tid;
+    gcum[tid] = tok < a.T ? a.g[(size_t)h * a.T + tok] : 0.0f;  // g until the prefix below
+    bc[tid] = tok < a.T ? a.beta[(size_t)h * a.T + tok] : 0.0f;
   }
   __syncthreads();
+  if (tid == 0) {  // :137-151, in place
+    float running = 0.0f;
+    for (int t = 0; t < kC; ++t) {
+      gcum[t] = running + gcum[t];
+      running = gcum[t];
+    }
+  }
   if (a.l2) {
-    if (tid < 2 * kC) {
+    if (tid >= 64 && tid < 64 + 2 * kC) {  // waves 1, 2 (wave 0 runs the prefix)
       const int t = tid & (kC - 1);
-      const float* x = tid < kC ? qs[t] : ks[t];
+      const float* x = tid < 128 ? qs[t] : ks[t];
       float sq = 0.0f;
       for (int d = 0; d < kD; d += 4) {
         const float4 v = ld4(x + d);
@@ -438,10 +462,10 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
         sq = sq + v.z * v.z;
         sq = sq + v.w * v.w;
       }
-      (tid < kC ? inv_q : inv_k)[t] = 1.0f / __builtin_sqrtf(sq + 1e-6f);
+      (tid < 128 ? inv_q : inv_k)[t] = 1.0f / __builtin_sqrtf(sq + 1e-6f);
     }
-    __syncthreads();
   }
+  __syncthreads();
   for (int i = tid; i < kC * kD; i += kThreads) {
     const int t = i / kD, d = i % kD;
     float q = qs[t][d], k = ks[t][d];
@@ -465,32 +489,33 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
     decay[r][c] = c <= r ? spk::expf_det(gcum[r] - gcum[c]) : 0.0f;
   }
   __syncthreads();
-  // :161-170 (attn, strictly lower) and :204-213 (local, lower): lane = column
-  // c, wave-uniform row r; the d = 0..127 sums in order, 4 per 16-byte read.
-  for (int r = wave; r < kC; r += kThreads / 64) {
+  // :161-170 (attn, strictly lower): lane = column c, wave-uniform rows, four
+  // rows per pass; each d = 0..127 sum in order, 4 terms per 16-byte read.
+  for (int r0 = 4 * wave; r0 < kC; r0 += 4 * (kThreads / 64)) {
     const int c = lane;
-    const float br = bc[r];
-    float da = 0.0f, dl = 0.0f;
+    float da[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int d = 0; d < kD; d += 4) {
-      const float4 kr = ld4(&ks[r][d]), qr = ld4(&qs[r][d]), kc4 = ld4(&ks[c][d]);
-      da = da + (kr.x * br) * kc4.x;
-      da = da + (kr.y * br) * kc4.y;
-      da = da + (kr.z * br) * kc4.z;
-      da = da + (kr.w * br) * kc4.w;
-      dl = dl + qr.x * kc4.x;
-      dl = dl + qr.y * kc4.y;
-      dl = dl + qr.z * kc4.z;
-      dl = dl + qr.w * kc4.w;
+      const float4 kc4 = ld4(&ks[c][d]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 kr = ld4(&ks[r0 + j][d]);
+        const float br = bc[r0 + j];
+        da[j] = da[j] + (kr.x * br) * kc4.x;
+        da[j] = da[j] + (kr.y * br) * kc4.y;
+        da[j] = da[j] + (kr.z * br) * kc4.z;
+        da[j] = da[j] + (kr.w * br) * kc4.w;
+      }
     }
-    attn[r][c] = c < r ? -da * decay[r][c] : 0.0f;
-    local[r * kC + c] = c <= r ? dl * decay[r][c] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) attn[r0 + j][c] = c < r0 + j ? -da[j] * decay[r0 + j][c] : 0.0f;
   }
   __syncthreads();
-  // :171-181 forward substitution.  Row r is updated from its original values
-  // (the reference's old_row) and rows < r already updated; lane c keeps its
-  // column of the updated matrix in registers, so the original rows stay in
-  // LDS untouched until the end and no barrier is needed between rows.
   if (wave == 0) {
+    // :171-181 forward substitution.  Row r is updated from its original
+    // values (the reference's old_row) and rows < r already updated; lane c
+    // keeps its column of the updated matrix in registers, so the original
+    // rows stay in LDS untouched until the end and no barrier is needed
+    // between rows.
     const int c = lane;
     float col[kC];
 #pragma unroll
@@ -507,39 +532,88 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
     // (one wave: its LDS reads above complete before the writes below)
 #pragma unroll
     for (int in = 0; in < kC; ++in) attn[in][c] = in == c ? col[in] + 1.0f : col[in];  // :182-184 +I
+  } else if (wave != 4) {
+    // :204-213 (local, lower), meanwhile on the six waves that do not share
+    // SIMD 0 with the solve (waves are dealt to SIMDs round-robin)
+    const int lw = wave < 4 ? wave - 1 : wave - 2;  // 0..5
+    for (int r0 = 4 * lw; r0 < kC; r0 += 4 * 6) {
+      const int c = lane;
+      float dl[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int d = 0; d < kD; d += 4) {
+        const float4 kc4 = ld4(&ks[c][d]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float4 qr = ld4(&qs[r0 + j][d]);
+          dl[j] = dl[j] + qr.x * kc4.x;
+          dl[j] = dl[j] + qr.y * kc4.y;
+          dl[j] = dl[j] + qr.z * kc4.z;
+          dl[j] = dl[j] + qr.w * kc4.w;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) local[(r0 + j) * kC + c] = c <= r0 + j ? dl[j] * decay[r0 + j][c] : 0.0f;
+    }
   }
   __syncthreads();
-  // :186-202: thread = (row r, 4 consecutive d), the c = 0..63 sums in order
-  for (int u = tid; u < kC * (kD / 4); u += kThreads) {
-    const int r = u / (kD / 4), d = (u % (kD / 4)) * 4;
-    float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // :186-202.  The factors v*beta and (k*beta)*e^g depend on (c, d) only:
+  // computed once, rounded as in the reference, in place of v and k.
+  for (int i = tid; i < kC * kD; i += kThreads) {
+    const int c = i / kD, d = i % kD;
+    const float bcol = bc[c];
+    vs[c][d] = vs[c][d] * bcol;
+    ks[c][d] = (ks[c][d] * bcol) * eg[c];
+  }
+  __syncthreads();
+  // thread = 4 rows x 4 consecutive d; c = 0..63 in order, zero coefficients
+  // skipped per row as in the reference
+  {
+    const int r0 = (tid / (kD / 4)) * 4, d = (tid % (kD / 4)) * 4;
+    float sv[4][4], sk[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[j][e] = sk[j][e] = 0.0f;
     for (int c = 0; c < kC; ++c) {
-      const float coeff = attn[r][c];
-      if (coeff == 0.0f) continue;
-      const float bcol = bc[c], egc = eg[c];
       const float4 v4 = ld4(&vs[c][d]), k4 = ld4(&ks[c][d]);
       const float vv[4] = {v4.x, v4.y, v4.z, v4.w}, kk[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        sv[j] = sv[j] + coeff * (vv[j] * bcol);
-        sk[j] = sk[j] + coeff * ((kk[j] * bcol) * egc);
+        const float coeff = attn[r0 + j][c];
+        if (coeff == 0.0f) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sv[j][e] = sv[j][e] + coeff * vv[e];
+          sk[j][e] = sk[j][e] + coeff * kk[e];
+        }
       }
     }
-    *reinterpret_cast<float4*>(solved + r * kD + d) = make_float4(sv[0], sv[1], sv[2], sv[3]);
-    *reinterpret_cast<float4*>(kcd + r * kD + d) = make_float4(sk[0], sk[1], sk[2], sk[3]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<float4*>(solved + (r0 + j) * kD + d) = make_float4(sv[j][0], sv[j][1], sv[j][2], sv[j][3]);
+      *reinterpret_cast<float4*>(kcd + (r0 + j) * kD + d) = make_float4(sk[j][0], sk[j][1], sk[j][2], sk[j][3]);
+    }
   }
 }
 
 // Chunk body, part 2 (the loops that read or write the state, :215-268): the
 // state's value columns are independent, so one workgroup per (head, slice of
 // kSlice columns) scans the chunks in order with its 128 x kSlice block of the
-// state in LDS.
+// state in LDS.  Each chunk's state-independent operands (kcd, q, k, local,
+// the slice of solved, eg, wlast) are staged in LDS; the next chunk's are
+// loaded into registers while the current one is computed.
 constexpr int kSlice = 16;
-constexpr int kScanThreads = 256;
+constexpr int kScanThreads = 512;
+constexpr int kScanLd = kD + 4;
 
 __global__ __launch_bounds__(kScanThreads) void ordered_chunk_scan_kernel(OrdArgs a) {
-  __shared__ __align__(16) float Ss[kD][kSlice];
-  __shared__ __align__(16) float vn[kC][kSlice];
+  __shared__ __align__(16) float Kc[kC][kScanLd];  // kcd (W)
+  __shared__ __align__(16) float Qc[kC][kScanLd];  // scaled q
+  __shared__ __align__(16) float Kk[kC][kScanLd];  // k
+  __shared__ __align__(16) float Lc[kC][kC + 1];   // local
+  __shared__ __align__(16) float Sol[kC][kSlice];  // solved (U), this slice
+  __shared__ float Eg[kC], Wl[kC];
+  __shared__ __align__(16) float Ss[kD][kSlice];   // the state slice
+  __shared__ __align__(16) float vn[kC][kSlice];   // v_new, this slice
   const int h = blockIdx.x / (kD / kSlice);
   const int v0 = (blockIdx.x % (kD / kSlice)) * kSlice;
   const int tid = threadIdx.x;
@@ -551,91 +625,115 @@ __global__ __launch_bounds__(kScanThreads) void ordered_chunk_scan_kernel(OrdArg
     const int kd = i / kSlice, j = i % kSlice;
     Ss[kd][j] = a.init ? a.init[(size_t)h * kD * kD + kd * kD + v0 + j] : 0.0f;
   }
-  // phase A/B mapping: row r of the chunk, 4 columns vq*4..vq*4+3 of the slice
-  const int r = tid >> 2, vq = tid & 3;
-  // phase C mapping: state row kd, 8 columns vh*8..vh*8+7 of the slice
-  const int kd = tid >> 1, vh = tid & 1;
+  // prefetch registers: kcd, q, k (4 float4 each), local (2 float4), the
+  // solved slice (float2), eg or wlast (one float for tid < 128)
+  float4 pk[4], pq[4], pkk[4], pl[2];
+  float2 ps;
+  float pe = 0.0f;
+  auto prefetch = [&](int ci) {
+    const float* cw = chunk_ws(a, h, ci);
+    const float* kcd = cw + kC * kD;
+    const float* loc = cw + 2 * kC * kD;
+    const float* qc = qs + (size_t)ci * kC * kD;
+    const float* kc = ks + (size_t)ci * kC * kD;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pc = tid + kScanThreads * j;  // float4 index in a [64][128] block
+      pk[j] = ld4(kcd + 4 * pc);
+      pq[j] = ld4(qc + 4 * pc);
+      pkk[j] = ld4(kc + 4 * pc);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) pl[j] = ld4(loc + 4 * (tid + kScanThreads * j));
+    ps = *reinterpret_cast<const float2*>(cw + (tid >> 3) * kD + v0 + (tid & 7) * 2);
+    if (tid < 2 * kC) pe = cw[2 * kC * kD + kC * kC + tid];  // eg[0..63], then wlast[0..63]
+  };
   const int nchunks = a.total / kC;
+  prefetch(0);
   for (int ci = 0; ci < nchunks; ++ci) {
     const int base = ci * kC;
-    const float* qc = qs + (size_t)base * kD;
-    const float* kc = ks + (size_t)base * kD;
-    const float* cw = chunk_ws(a, h, ci);
-    const float* solved = cw;
-    const float* kcd = cw + kC * kD;
-    const float* local = cw + 2 * kC * kD;
-    const float* eg = local + kC * kC;
-    const float* wlast = eg + kC;
-    __syncthreads();
-    // A (:215-233): carry = kcd[r] . S[:, vd], inter = (q[r] * eg[r]) . S[:, vd]
-    float inter[4];
-    {
-      const float egr = eg[r];
-      float carry[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();  // the previous chunk's reads of the staged operands are done
 #pragma unroll
-      for (int j = 0; j < 4; ++j) inter[j] = 0.0f;
+    for (int j = 0; j < 4; ++j) {
+      const int pc = tid + kScanThreads * j, r = pc / (kD / 4), d = (pc % (kD / 4)) * 4;
+      *reinterpret_cast<float4*>(&Kc[r][d]) = pk[j];
+      *reinterpret_cast<float4*>(&Qc[r][d]) = pq[j];
+      *reinterpret_cast<float4*>(&Kk[r][d]) = pkk[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int pc = tid + kScanThreads * j, r = pc / (kC / 4), c = (pc % (kC / 4)) * 4;
+      Lc[r][c] = pl[j].x;
+      Lc[r][c + 1] = pl[j].y;
+      Lc[r][c + 2] = pl[j].z;
+      Lc[r][c + 3] = pl[j].w;
+    }
+    *reinterpret_cast<float2*>(&Sol[tid >> 3][(tid & 7) * 2]) = ps;
+    if (tid < kC)
+      Eg[tid] = pe;
+    else if (tid < 2 * kC)
+      Wl[tid - kC] = pe;
+    __syncthreads();
+    if (ci + 1 < nchunks) prefetch(ci + 1);
+    // A (:215-233): thread = row r, columns 2cp, 2cp+1 of the slice
+    const int r = tid >> 3, cp = tid & 7;
+    float inter[2] = {0.0f, 0.0f};
+    {
+      const float egr = Eg[r];
+      float carry[2] = {0.0f, 0.0f};
       for (int k4 = 0; k4 < kD; k4 += 4) {
-        const float4 kw = *reinterpret_cast<const float4*>(kcd + r * kD + k4);
-        const float4 qw = *reinterpret_cast<const float4*>(qc + r * kD + k4);
+        const float4 kw = ld4(&Kc[r][k4]);
+        const float4 qw = ld4(&Qc[r][k4]);
         const float kk[4] = {kw.x, kw.y, kw.z, kw.w};
         const float qq[4] = {qw.x, qw.y, qw.z, qw.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float4 s4 = *reinterpret_cast<const float4*>(&Ss[k4 + e][vq * 4]);
-          const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+          const float2 s2 = *reinterpret_cast<const float2*>(&Ss[k4 + e][cp * 2]);
           const float qe = qq[e] * egr;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            carry[j] = carry[j] + kk[e] * sv[j];
-            inter[j] = inter[j] + qe * sv[j];
-          }
+          carry[0] = carry[0] + kk[e] * s2.x;
+          carry[1] = carry[1] + kk[e] * s2.y;
+          inter[0] = inter[0] + qe * s2.x;
+          inter[1] = inter[1] + qe * s2.y;
         }
       }
-      const float4 so = *reinterpret_cast<const float4*>(solved + r * kD + v0 + vq * 4);
-      const float sol[4] = {so.x, so.y, so.z, so.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) vn[r][vq * 4 + j] = sol[j] - carry[j];
+      vn[r][cp * 2] = Sol[r][cp * 2] - carry[0];
+      vn[r][cp * 2 + 1] = Sol[r][cp * 2 + 1] - carry[1];
     }
     __syncthreads();
     // B (:235-244): core[r] = inter + sum_{c <= r} local[r][c] * vnew[c]
     {
-      float sum[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sum[j] = inter[j];
+      float s0 = inter[0], s1 = inter[1];
       for (int c = 0; c <= r; ++c) {
-        const float l = local[r * kC + c];
-        const float4 v4 = *reinterpret_cast<const float4*>(&vn[c][vq * 4]);
-        sum[0] = sum[0] + l * v4.x;
-        sum[1] = sum[1] + l * v4.y;
-        sum[2] = sum[2] + l * v4.z;
-        sum[3] = sum[3] + l * v4.w;
+        const float l = Lc[r][c];
+        const float2 v2 = *reinterpret_cast<const float2*>(&vn[c][cp * 2]);
+        s0 = s0 + l * v2.x;
+        s1 = s1 + l * v2.y;
       }
       if (base + r < a.T) {
-        float* o = a.core + ((size_t)h * a.core_head_stride + base + r) * kD + v0 + vq * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = sum[j];
+        float* o = a.core + ((size_t)h * a.core_head_stride + base + r) * kD + v0 + cp * 2;
+        o[0] = s0;
+        o[1] = s1;
       }
     }
-    // C (:246-268): S[kd][vd] = S * eg[63] + sum_r (k[r][kd] * wlast[r]) * vnew[r][vd]
+    // C (:246-268): thread = state row kd, columns 4cq..4cq+3 of the slice
     {
-      const float eglast = eg[kC - 1];
-      float upd[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) upd[j] = 0.0f;
+      const int kd = tid >> 2, cq = tid & 3;
+      const float eglast = Eg[kC - 1];
+      float upd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       for (int rr = 0; rr < kC; ++rr) {
-        const float kw = kc[rr * kD + kd] * wlast[rr];
-        const float4 lo = *reinterpret_cast<const float4*>(&vn[rr][vh * 8]);
-        const float4 hi = *reinterpret_cast<const float4*>(&vn[rr][vh * 8 + 4]);
-        const float vv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) upd[j] = upd[j] + kw * vv[j];
+        const float kw = Kk[rr][kd] * Wl[rr];
+        const float4 v4 = ld4(&vn[rr][cq * 4]);
+        upd[0] = upd[0] + kw * v4.x;
+        upd[1] = upd[1] + kw * v4.y;
+        upd[2] = upd[2] + kw * v4.z;
+        upd[3] = upd[3] + kw * v4.w;
       }
-      // Ss row kd is read by phase A of this chunk only (before the barrier
-      // above) and written here by this thread alone
+      // Ss row kd was read by phase A (before the barrier above) and is
+      // written here by this thread alone
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float ws = Ss[kd][vh * 8 + j] * eglast;
-        Ss[kd][vh * 8 + j] = ws + upd[j];
+      for (int j = 0; j < 4; ++j) {
+        const float ws = Ss[kd][cq * 4 + j] * eglast;
+        Ss[kd][cq * 4 + j] = ws + upd[j];
       }
     }
   }
@@ -708,6 +806,13 @@ extern "C" int spk_chunk_prefill_ordered(const SpkChunkArgs* p, spk_stream_t str
     return spk::fail(SPK_ERR_NULL, "spk_chunk_prefill_ordered: NULL pointer");
   if (p->input_dtype != SPK_F32 && p->input_dtype != SPK_F16)
     return spk::fail(SPK_ERR_ARG, "spk_chunk_prefill_ordered: input_dtype %d", p->input_dtype);
+  {
+    const size_t vec = p->input_dtype == SPK_F16 ? 8 : 16;  // 4 elements per load
+    if (!spk::aligned(p->q, vec) || !spk::aligned(p->k, vec) || !spk::aligned(p->v, vec) ||
+        !spk::aligned(p->workspace, 16) || !spk::aligned(p->out_state, 4) || !spk::aligned(p->out_core, 4))
+      return spk::fail(SPK_ERR_ALIGN, "spk_chunk_prefill_ordered: q/k/v must be %zu-byte aligned, workspace 16-byte",
+                       vec);
+  }
   if (p->workspace_bytes < spk_chunk_prefill_ordered_workspace_size(p->num_heads, p->total_tokens))
     return spk::fail(SPK_ERR_ARG, "spk_chunk_prefill_ordered: workspace %zu < %zu bytes", p->workspace_bytes,
                      spk_chunk_prefill_ordered_workspace_size(p->num_heads, p->total_tokens));
