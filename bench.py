@@ -269,9 +269,11 @@ def model_decode_bytes(layers=24, vocab=VOCAB, pos=MODEL_PROMPT + MODEL_NEW // 2
     return weights + state + kv
 
 
-def bench_model(steps, warmup):
+def bench_model(steps, warmup, use_graph=True):
     """Config 4: the full Qwen3.5-0.8B-shaped random-init model, 512-token
-    prompt, 128 greedy tokens at batch 1; decode is HBM-bound."""
+    prompt, 128 greedy tokens at batch 1; decode is HBM-bound.  use_graph=False
+    enqueues each decode step's kernels one by one instead of replaying the
+    recorded HIP graph (for kernel traces)."""
     import tempfile
     from spock_amd import model, synth
     work = Path(tempfile.mkdtemp(prefix="spock-config4-"))
@@ -284,7 +286,7 @@ def bench_model(steps, warmup):
     res = {"workload": "config4: 24 layers (18 gated DeltaNet + 6 gated attention), hidden 1024, vocab 248320, "
                        "fp16 weights N(0,0.02) seed 2026, prompt 512, 128 greedy tokens, batch 1"}
     for mode, matrix in (("ordered_prefill", False), ("matrix_prefill", True)):
-        with model.Session(art, matrix_prefill=matrix) as s:
+        with model.Session(art, use_graph=use_graph, matrix_prefill=matrix) as s:
             s.generate(prompt[:64], 4)  # warm-up: kernels loaded, graph recorded
             runs = [s.generate(prompt, MODEL_NEW) for _ in range(max(1, min(3, steps)))]
         best = min(runs, key=lambda r: r.gpu_decode_ms)
@@ -357,6 +359,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="model workload: launch the decode kernels one by one instead of the HIP graph")
     ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy", "model"],
                     help="run one workload and print its own JSON (for profiler runs)")
     args = ap.parse_args()
@@ -373,7 +377,8 @@ def main():
     log(f"[bench] device {torch.cuda.get_device_name(0)}")
     if args.only:
         fns = {"prefill": bench_prefill, "config0": bench_config0, "gemv": bench_gemv_chain,
-               "lm_head": bench_lm_head, "copy": bench_copy, "model": bench_model,
+               "lm_head": bench_lm_head, "copy": bench_copy,
+               "model": lambda s, w: bench_model(s, w, use_graph=not args.no_graph),
                "decode": lambda s, w: [bench_decode(B, s, w) for B in (1, 16, 64, 256)]}
         r = fns[args.only](args.steps, args.warmup)
         print(json.dumps({"only": args.only, "result": r}, default=float), flush=True)
