@@ -325,6 +325,30 @@ def bench_copy(steps, warmup):
             "achieved_gbs": round(2 * n / avg / 1e9, 1)}
 
 
+def bench_ceilings(steps, warmup):
+    """Measured ceilings beside the datasheet peaks: dense fp32 MFMA issue
+    (8 independent v_mfma_f32_16x16x4_f32 chains per wavefront, 4 workgroups
+    per CU) and a read-only non-temporal stream over 2 GiB of HBM."""
+    import torch
+    from spock_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    stream = _stream()
+    blocks, iters = 4096, 4096  # 16 workgroups per CU
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    _, ms = timed_launches(lambda i: lib.spk_selftest_mfma_peak(blocks, iters, out.data_ptr(), stream),
+                           max(3, steps // 4), max(3, warmup // 4))
+    flop = blocks * 4 * 8 * iters * 2.0 * 16 * 16 * 4
+    nbytes = 2 << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
+    sink = torch.empty(32768, dtype=torch.int32, device=dev)
+    # 32768 workgroups (16 loads of 16 B per thread): the best of a 1k..32k sweep
+    _, ms_r = timed_launches(lambda i: lib.spk_selftest_stream_read(buf.data_ptr(), nbytes, 32768, sink.data_ptr(),
+                                                                    stream), steps, warmup)
+    return {"fp32_mfma_tflops": round(flop / (ms / 1e3) / 1e12, 1), "fp32_mfma_datasheet_tflops": FP32_MFMA_PEAK_TFLOPS,
+            "hbm_read_gbs": round(nbytes / (ms_r / 1e3) / 1e9, 1), "hbm_datasheet_gbs": HBM_PEAK_GBS}
+
+
 def cpu_baseline():
     """The reference's chunk rule on a bounded sample: one 2048-token sequence
     of the same shape (16 heads, fp32), single thread, median of 5 runs."""
@@ -361,7 +385,7 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="model workload: launch the decode kernels one by one instead of the HIP graph")
-    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy", "model"],
+    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy", "model", "ceilings"],
                     help="run one workload and print its own JSON (for profiler runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -377,7 +401,7 @@ def main():
     log(f"[bench] device {torch.cuda.get_device_name(0)}")
     if args.only:
         fns = {"prefill": bench_prefill, "config0": bench_config0, "gemv": bench_gemv_chain,
-               "lm_head": bench_lm_head, "copy": bench_copy,
+               "lm_head": bench_lm_head, "copy": bench_copy, "ceilings": bench_ceilings,
                "model": lambda s, w: bench_model(s, w, use_graph=not args.no_graph),
                "decode": lambda s, w: [bench_decode(B, s, w) for B in (1, 16, 64, 256)]}
         r = fns[args.only](args.steps, args.warmup)
@@ -403,6 +427,8 @@ def main():
         log(f"[bench] lm_head {secondary['lm_head_argmax']}")
         secondary["config4_full_model"] = bench_model(args.steps, args.warmup)
         log(f"[bench] full model {secondary['config4_full_model']}")
+        secondary["measured_ceilings"] = bench_ceilings(args.steps, args.warmup)
+        log(f"[bench] measured ceilings {secondary['measured_ceilings']}")
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log(f"[bench] cpu baseline {cpu}")

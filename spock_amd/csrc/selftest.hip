@@ -25,3 +25,70 @@ extern "C" int spk_selftest_numerics(const float* x, int32_t n, float* out, spk_
   hipLaunchKernelGGL(numerics_kernel, dim3((n + 255) / 256), dim3(256), 0, spk::to_hip(stream), x, n, out);
   return spk::check_launch("spk_selftest_numerics");
 }
+
+// ---------------------------------------------------------------------------
+// Measured ceilings for the roofline denominators (reported beside the
+// datasheet peaks): dense fp32 MFMA issue and a read-only HBM stream.
+// ---------------------------------------------------------------------------
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Every wavefront runs 8 independent v_mfma_f32_16x16x4_f32 chains of `iters`
+// steps (2 * 16 * 16 * 4 FLOP per instruction).
+__global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  float a = 1.0f + 1e-7f * (float)lane, b = 1.0f - 1e-7f * (float)lane;
+  v4f acc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[c], 0, 0, 0);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) s += acc[c][0] + acc[c][1] + acc[c][2] + acc[c][3];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// Grid-stride 16-byte non-temporal reads of the whole buffer.  Each thread's
+// XOR of what it read is stored only if it equals a fixed constant, so the
+// reads cannot be dropped and (almost) nothing is written.
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, long long n16,
+                                                          uint32_t* __restrict__ out) {
+  uint32_t acc = 0;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += 4 * stride) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long long j = min(i + u * stride, n16 - 1);
+      v[u] = __builtin_nontemporal_load(p + j);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == 0x9e3779b9u) out[blockIdx.x] = acc;
+}
+
+}  // namespace
+
+extern "C" int spk_selftest_mfma_peak(int32_t blocks, int32_t iters, float* out, spk_stream_t stream) {
+  if (!out) return spk::fail(SPK_ERR_NULL, "spk_selftest_mfma_peak: NULL out");
+  if (blocks <= 0 || iters <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_selftest_mfma_peak: blocks %d iters %d", blocks, iters);
+  hipLaunchKernelGGL(mfma_peak_kernel, dim3(blocks), dim3(256), 0, spk::to_hip(stream), iters, out);
+  return spk::check_launch("spk_selftest_mfma_peak");
+}
+
+extern "C" int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, uint32_t* out,
+                                        spk_stream_t stream) {
+  if (!p || !out) return spk::fail(SPK_ERR_NULL, "spk_selftest_stream_read: NULL pointer");
+  if (bytes < 16 || bytes % 16 || blocks <= 0 || !spk::aligned(p, 16))
+    return spk::fail(SPK_ERR_SHAPE, "spk_selftest_stream_read: bytes %zu blocks %d (16-byte multiple and alignment)",
+                     bytes, blocks);
+  hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, spk::to_hip(stream),
+                     static_cast<const u32x4*>(p), (long long)(bytes / 16), out);
+  return spk::check_launch("spk_selftest_stream_read");
+}
