@@ -332,8 +332,9 @@ int spk_record_token(const int32_t* token, int32_t* pos, int32_t* count, int32_t
 /* ---- prompt-wide kernels in the CPU restatement's operation order -------
  * The parity forms of spk_gemm_f16 and spk_chunk_prefill: bit-identical to
  * the oracle, so a prompt prefilled with them leaves exactly the state (and
- * greedy tokens) of the CPU path.  They trade the matrix cores for the
- * reference's sequential reduction orders. */
+ * greedy tokens) of the CPU path.  They keep the reference's sequential
+ * reduction orders: the matvec runs on fp32 matrix cores one product per
+ * instruction (exact for fp16 operands), the chunk rule on the vector ALUs. */
 
 /* Y[t][r] (+ residual as in spk_gemm_f16) for every row t of X: each output
  * bit-identical to spk_matvec_f16 of X's row t (the matvec_tiled /
@@ -345,8 +346,9 @@ int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t ldx, uint1
 /* run_deltanet_chunk_rule (deltanet_chunk.cpp:53-284) with the reference's
  * loop nests and sequential reductions, exp = the library's deterministic exp;
  * one sequence (cu_seqlens NULL), dk == dv == 128, chunk_size == 64;
- * initial_state must not alias out_state.  Same argument struct as
- * spk_chunk_prefill; workspace of spk_chunk_prefill_ordered_workspace_size(). */
+ * initial_state must not alias out_state.  Same argument struct and
+ * alignment rules as spk_chunk_prefill (q/k/v 16-byte aligned for fp32, 8 for
+ * fp16; workspace 16); workspace of spk_chunk_prefill_ordered_workspace_size(). */
 size_t spk_chunk_prefill_ordered_workspace_size(int32_t num_heads, int32_t total_tokens);
 int spk_chunk_prefill_ordered(const SpkChunkArgs* args, spk_stream_t stream);
 
