@@ -87,6 +87,35 @@ def timed_launches(fn, steps, warmup, rotate=1):
     return wall, e0.elapsed_time(e1) / steps
 
 
+def timed_graph(fn, steps, warmup, rotate=1, reps=3):
+    """Runs fn(i) warmup times eagerly, then records `steps` calls into one HIP
+    graph (fn launches on torch's current stream, read at call time) and
+    replays it: returns the median device milliseconds per step over `reps`
+    timed replays.  For launches of a few microseconds, where host launch
+    overhead would otherwise set the pace."""
+    import statistics
+    import torch
+    for i in range(warmup):
+        fn(i % rotate)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn((warmup + i) % rotate)
+    g.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / steps)
+    return statistics.median(per)
+
+
 def _stream():
     import torch
     return torch.cuda.current_stream().cuda_stream
@@ -137,7 +166,7 @@ def bench_config0(steps, warmup):
     ws = torch.empty(ops.chunk_workspace_bytes(H, 104, 1), dtype=torch.uint8, device=dev)
     fn = lambda i: ops.chunk_prefill(t["q"], t["k"], t["v"], t["g"], t["beta"], out_core=core,
                                      out_state=state, workspace=ws)
-    wall, ms = timed_launches(fn, steps, warmup)
+    ms = timed_graph(fn, steps, warmup)
     flops = 2 * H * FLOP_PER_HEAD_CHUNK
     avg = ms / 1e3
     return {"workload": "config0: H16 T104->128 C64 fp32", "launch_us": round(avg * 1e6, 2),
@@ -175,9 +204,8 @@ def bench_decode(B, steps, warmup):
         d.z, d.z_stride = st["z"].data_ptr(), 2048
         d.norm_weight = shared["norm_w"].data_ptr()
         args.append(d)
-    stream = _stream()
-    fn = lambda i: lib.spk_deltanet_decode_step(ctypes.byref(args[i]), stream)
-    wall, ms = timed_launches(fn, steps, warmup, rotate=copies)
+    fn = lambda i: lib.spk_deltanet_decode_step(ctypes.byref(args[i]), _stream())
+    ms = timed_graph(fn, steps, warmup, rotate=copies)
     avg = ms / 1e3
     nbytes = per_copy + DECODE_SHARED_BYTES
     gbs = nbytes / avg / 1e9
@@ -212,13 +240,12 @@ def bench_gemv_chain(steps, warmup):
     # stage 1: qkv, z, gate, up from x (one launch); stage 2: out from z, down from gate
     plans = [(descs([(W[0], x, outs[0]), (W[1], x, outs[1]), (W[3], x, outs[3]), (W[4], x, outs[4])]),
               descs([(W[2], outs[1], outs[2]), (W[5], outs[3], outs[5])])) for W in Ws]
-    stream = _stream()
-
     def fn(i):
+        stream = _stream()
         lib.spk_matvec_f16_batched(plans[i][0], 4, stream)
         lib.spk_matvec_f16_batched(plans[i][1], 2, stream)
 
-    wall, ms = timed_launches(fn, steps, warmup, rotate=copies)
+    ms = timed_graph(fn, steps, warmup, rotate=copies)
     avg = ms / 1e3
     gbs = nbytes / avg / 1e9
     return {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
@@ -238,11 +265,10 @@ def bench_lm_head(steps, warmup):
     import ctypes
     from spock_amd import _lib
     lib = _lib.lib()
-    stream = _stream()
     wsb = ws.numel()
     fn = lambda i: lib.spk_lm_head_argmax(Ws[i].data_ptr(), x.data_ptr(), VOCAB, HIDDEN, None,
-                                          out.data_ptr(), ws.data_ptr(), wsb, stream)
-    wall, ms = timed_launches(fn, steps, warmup, rotate=2)
+                                          out.data_ptr(), ws.data_ptr(), wsb, _stream())
+    ms = timed_graph(fn, steps, warmup, rotate=2)
     avg = ms / 1e3
     nbytes = VOCAB * HIDDEN * 2
     gbs = nbytes / avg / 1e9
