@@ -765,20 +765,37 @@ extern "C" int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t
     return spk::check_launch("spk_matvec_f16_rows");
   }
   if ((S == 16 || S == 32 || S == 56) && vec_ok) {
-    // 2 x 2 tiles per wave unless that leaves SIMDs idle (1024 on the chip)
-    const int n_rt2 = (out_dim + 31) / 32, n_tt = (rows + 31) / 32;
-    const bool wide = (long long)n_rt2 * n_tt >= 1024;
-    const int n_rt = wide ? n_rt2 : (out_dim + 15) / 16;
+    // 2 x 2 tiles per wave unless that leaves SIMDs idle (1024 on the chip);
+    // then 1 x 2, then 1 x 1 (two waves per SIMD hide more operand latency)
+    const int n_rt32 = (out_dim + 31) / 32, n_rt16 = (out_dim + 15) / 16;
+    const int n_tt32 = (rows + 31) / 32, n_tt16 = (rows + 15) / 16;
+    int shape, n_rt, n_tt;
+    if ((long long)n_rt32 * n_tt32 >= 1024) {
+      shape = 0, n_rt = n_rt32, n_tt = n_tt32;
+    } else if ((long long)n_rt16 * n_tt32 >= 2048) {
+      shape = 1, n_rt = n_rt16, n_tt = n_tt32;
+    } else {
+      shape = 2, n_rt = n_rt16, n_tt = n_tt16;
+    }
     const int n_tiles = n_rt * n_tt;
     const dim3 grid((n_tiles + 3) / 4);
-#define SPK_MVR(s_, tr_)                                                                                      hipLaunchKernelGGL((matvec_rows_mfma_kernel<s_, tr_, 2>), grid, dim3(256), 0, s, a, n_tt, n_tiles)
+#define SPK_MVR(s_, tr_, tt_) \
+  hipLaunchKernelGGL((matvec_rows_mfma_kernel<s_, tr_, tt_>), grid, dim3(256), 0, s, a, n_tt, n_tiles)
+#define SPK_MVR3(s_)        \
+  if (shape == 0)           \
+    SPK_MVR(s_, 2, 2);      \
+  else if (shape == 1)      \
+    SPK_MVR(s_, 1, 2);      \
+  else                      \
+    SPK_MVR(s_, 1, 1);
     if (S == 16) {
-      if (wide) SPK_MVR(16, 2); else SPK_MVR(16, 1);
+      SPK_MVR3(16)
     } else if (S == 32) {
-      if (wide) SPK_MVR(32, 2); else SPK_MVR(32, 1);
+      SPK_MVR3(32)
     } else {
-      if (wide) SPK_MVR(56, 2); else SPK_MVR(56, 1);
+      SPK_MVR3(56)
     }
+#undef SPK_MVR3
 #undef SPK_MVR
     return spk::check_launch("spk_matvec_f16_rows");
   }
