@@ -248,9 +248,45 @@ def bench_gemv_chain(steps, warmup):
     ms = timed_graph(fn, steps, warmup, rotate=copies)
     avg = ms / 1e3
     gbs = nbytes / avg / 1e9
+    # stage 1 reads qkv, z, gate, up; stage 2 out and down
+    floor = read_floor_us([sum(2 * o * n for o, n in (CHAIN[j] for j in (0, 1, 3, 4))),
+                           sum(2 * o * n for o, n in (CHAIN[j] for j in (2, 5)))], steps, warmup)
     return {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "rotated_copies": copies,
-            "kernels": 6, "launches": 2}
+            "kernels": 6, "launches": 2, "read_floor": floor,
+            "frac_of_read_floor": round(floor["us"] / (avg * 1e6), 4)}
+
+
+def read_floor_us(stage_bytes, steps, warmup):
+    """The same byte counts read by a plain read-only kernel in the same
+    number of dependent launches (one launch per entry of stage_bytes,
+    rotated over buffers like the weights): the fastest of cached and
+    non-temporal loads and of 1 or 2 four-load rounds per thread.  A kernel
+    that only streams these bytes can do no better than this."""
+    import torch
+    from spock_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    total = sum(stage_bytes)
+    copies = math.ceil(ROTATE_BYTES / total)
+    bufs = [torch.empty(total, dtype=torch.uint8, device=dev).fill_(1) for _ in range(copies)]
+    sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+    offs = [sum(stage_bytes[:j]) for j in range(len(stage_bytes))]
+    best = None
+    for cached in (1, 0):
+        for rounds in (1, 2):
+            blocks = [max(1, -(-(b // 16) // (256 * 4 * rounds))) for b in stage_bytes]
+
+            def fn(i, cached=cached, blocks=blocks):
+                stream = _stream()
+                for b, off, nb in zip(stage_bytes, offs, blocks):
+                    lib.spk_selftest_stream_read(bufs[i].data_ptr() + off, b, nb, cached, sink.data_ptr(), stream)
+            us = timed_graph(fn, steps, warmup, rotate=copies) * 1e3
+            if best is None or us < best["us"]:
+                best = {"us": round(us, 2), "cached": bool(cached), "loads_per_thread": 4 * rounds,
+                        "launches": len(stage_bytes), "bytes": total}
+    del bufs
+    return best
 
 
 def bench_lm_head(steps, warmup):
@@ -369,7 +405,7 @@ def bench_ceilings(steps, warmup):
     buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
     sink = torch.empty(32768, dtype=torch.int32, device=dev)
     # 32768 workgroups (16 loads of 16 B per thread): the best of a 1k..32k sweep
-    _, ms_r = timed_launches(lambda i: lib.spk_selftest_stream_read(buf.data_ptr(), nbytes, 32768, sink.data_ptr(),
+    _, ms_r = timed_launches(lambda i: lib.spk_selftest_stream_read(buf.data_ptr(), nbytes, 32768, 0, sink.data_ptr(),
                                                                     stream), steps, warmup)
     return {"fp32_mfma_tflops": round(flop / (ms / 1e3) / 1e12, 1), "fp32_mfma_datasheet_tflops": FP32_MFMA_PEAK_TFLOPS,
             "hbm_read_gbs": round(nbytes / (ms_r / 1e3) / 1e9, 1), "hbm_datasheet_gbs": HBM_PEAK_GBS}

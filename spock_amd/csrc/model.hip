@@ -331,6 +331,7 @@ struct AttnArgs {
   float* part;         // [T][8][max_blocks][kPartFloats]
   int max_blocks;      // blocks of 64 positions the grid covers
   int store_kv;        // decode: the current position's block stores its K/V row
+  int tokens;          // T
 };
 
 // K rows in LDS are padded to 264 halves (528 B): lane p reading 16 B of row p
@@ -469,6 +470,155 @@ __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
   __syncthreads();
   float* part = a.part + (((size_t)t * kQHeads + qh) * a.max_blocks + b) * kPartFloats;
   attn_block_wave(qs[wave], Ks, Vs, b, npos, lane, part);
+}
+
+// Prefill block pass: one workgroup per (64-position block b, KV head, group
+// of kAttnGroup consecutive tokens), wave w = query head 4*kvh + w.  The
+// block's K/V rows are staged once for the group (rows up to the group's last
+// position; the rows themselves were stored by attn_store_kv_kernel).  Each
+// wave runs its head's score chains for the group's tokens together: lane =
+// position, one 16-byte K read per 8 dims feeds kAttnGroup independent
+// d = 0..255 fma chains, q read as fp16 (its values are fp16-rounded, so
+// this is exact).  Per token the arithmetic is attn_block_wave's: positions
+// past the token's own are masked to -inf (weight 0), the weighted V sum
+// visits positions 0..nvalid_t-1 in order.  Positions every token of the
+// group sees are summed for all tokens at once; the last kAttnGroup-1 are
+// added token by token, so a token never touches a position it cannot see.
+constexpr int kAttnGroup = 4;
+
+__global__ __launch_bounds__(256) void attn_prefill_blocks_kernel(AttnArgs a) {
+  __shared__ __align__(16) uint16_t qs[4][kAttnGroup][kHeadDim];
+  __shared__ __align__(16) uint16_t Ks[kAttnBlock][kKLd];
+  __shared__ __align__(16) uint16_t Vs[kAttnBlock][kHeadDim];
+  const int b = blockIdx.x, kvh = blockIdx.y, t0 = blockIdx.z * kAttnGroup;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tl = min(t0 + kAttnGroup, a.tokens) - 1;  // last token of the group
+  const int npos0 = a.pos0 + t0 + 1;                  // positions token t0 sees
+  const int npos_max = a.pos0 + tl + 1;
+  if (kAttnBlock * b >= npos_max) return;
+  const int qh = kvh * 4 + wave;
+  // Loads first: q rows and RoPE pairs of the group's tokens (tokens past the
+  // call's last read the last one's), the q norm weights, then the block's
+  // K/V rows (position 64b + tid/4, quarter tid%4; rows past the group's last
+  // position read row 0 and stage zeros).
+  float qv[kAttnGroup][4], c8[kAttnGroup][8], qw[4];
+#pragma unroll
+  for (int i = 0; i < kAttnGroup; ++i) {
+    const int t = min(t0 + i, tl);
+    load4h(a.qg + (size_t)t * 4096 + qh * 512 + 4 * lane, qv[i]);
+    load_rope(a.rope + (size_t)(a.pos0 + t) * 64, lane, c8[i]);
+  }
+  load4h(a.q_norm_w + 4 * lane, qw);
+  const int p = tid >> 2, q4 = tid & 3;
+  const int gp = kAttnBlock * b + p;
+  const bool live = gp < npos_max;
+  const uint16_t* row = a.kv + (size_t)(live ? gp : 0) * kKvRow + kvh * kHeadDim + q4 * 64;
+  uint4 kv4[8], vv4[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    kv4[i] = *reinterpret_cast<const uint4*>(row + 8 * i);
+    vv4[i] = *reinterpret_cast<const uint4*>(row + 512 + 8 * i);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the q work below
+#pragma unroll
+  for (int i = 0; i < kAttnGroup; ++i) {
+    head_norm_wave(qv[i], qw);
+    rope_wave(qv[i], c8[i], lane);
+    *reinterpret_cast<uint2*>(&qs[wave][i][4 * lane]) = pack4h(qv[i]);
+  }
+  const uint32_t keep = live ? 0xffffffffu : 0u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint4 k = make_uint4(kv4[i].x & keep, kv4[i].y & keep, kv4[i].z & keep, kv4[i].w & keep);
+    const uint4 v = make_uint4(vv4[i].x & keep, vv4[i].y & keep, vv4[i].z & keep, vv4[i].w & keep);
+    *reinterpret_cast<uint4*>(&Ks[p][q4 * 64 + 8 * i]) = k;
+    *reinterpret_cast<uint4*>(&Vs[p][q4 * 64 + 8 * i]) = v;
+  }
+  __syncthreads();
+
+  // scores: kAttnGroup chains per lane (position 64b + lane)
+  float dot[kAttnGroup];
+#pragma unroll
+  for (int i = 0; i < kAttnGroup; ++i) dot[i] = 0.0f;
+#pragma unroll 2
+  for (int d8 = 0; d8 < kHeadDim / 8; ++d8) {
+    float kf[8];
+    unpack8(*reinterpret_cast<const uint4*>(&Ks[lane][8 * d8]), kf);
+#pragma unroll
+    for (int i = 0; i < kAttnGroup; ++i) {
+      float qf[8];
+      unpack8(*reinterpret_cast<const uint4*>(&qs[wave][i][8 * d8]), qf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot[i] = __builtin_fmaf(qf[e], kf[e], dot[i]);
+    }
+  }
+  const int pp = kAttnBlock * b + lane;
+  float m[kAttnGroup], w[kAttnGroup];
+  int nvalid[kAttnGroup];
+#pragma unroll
+  for (int i = 0; i < kAttnGroup; ++i) {
+    const bool tok = t0 + i < a.tokens;
+    nvalid[i] = tok ? min(kAttnBlock, npos0 + i - kAttnBlock * b) : 0;  // may be <= 0
+    m[i] = (tok && pp < npos0 + i) ? dot[i] * 0.0625f : -INFINITY;
+  }
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1)
+#pragma unroll
+    for (int i = 0; i < kAttnGroup; ++i) m[i] = fmaxf(m[i], __shfl_xor(m[i], sh, 64));
+#pragma unroll
+  for (int i = 0; i < kAttnGroup; ++i)
+    w[i] = (lane < nvalid[i]) ? spk::expf_det(dot[i] * 0.0625f - m[i]) : 0.0f;
+  float acc[kAttnGroup][4];
+#pragma unroll
+  for (int i = 0; i < kAttnGroup; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[i][e] = 0.0f;
+  // positions 0..nv_all-1 are seen by every token of the group
+  const int nv_all = max(0, nvalid[0]);
+  const int nv_max = min(kAttnBlock, npos_max - kAttnBlock * b);
+  for (int j0 = 0; j0 < nv_all; j0 += 8) {
+    uint2 vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vv[i] = *reinterpret_cast<const uint2*>(&Vs[j0 + i][4 * lane]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (j0 + i < nv_all) {
+        const float vf[4] = {spk::h2f(vv[i].x & 0xffffu), spk::h2f(vv[i].x >> 16), spk::h2f(vv[i].y & 0xffffu),
+                             spk::h2f(vv[i].y >> 16)};
+#pragma unroll
+        for (int t = 0; t < kAttnGroup; ++t) {
+          const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[t]), j0 + i));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(wj, vf[e], acc[t][e]);
+        }
+      }
+    }
+  }
+  for (int j = nv_all; j < nv_max; ++j) {  // at most kAttnGroup - 1 positions
+    const uint2 v2 = *reinterpret_cast<const uint2*>(&Vs[j][4 * lane]);
+    const float vf[4] = {spk::h2f(v2.x & 0xffffu), spk::h2f(v2.x >> 16), spk::h2f(v2.y & 0xffffu),
+                         spk::h2f(v2.y >> 16)};
+#pragma unroll
+    for (int t = 0; t < kAttnGroup; ++t) {
+      if (j < nvalid[t]) {
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[t]), j));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(wj, vf[e], acc[t][e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kAttnGroup; ++i) {
+    const float S = spk::tree64_to_lane0(w[i]);
+    if (nvalid[i] > 0) {
+      float* part = a.part + (((size_t)(t0 + i) * kQHeads + qh) * a.max_blocks + b) * kPartFloats;
+      if (lane == 0) {
+        part[0] = m[i];
+        part[1] = S;
+      }
+      *reinterpret_cast<float4*>(part + 2 + 4 * lane) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    }
+  }
 }
 
 // Prefill: K/V rows of positions pos0..pos0+T-1, before any block pass reads
@@ -758,6 +908,7 @@ static int attention_common(const SpkAttnArgs* p, int T, int positions, const ch
   a.out = p->out;
   a.part = static_cast<float*>(p->workspace);
   a.max_blocks = (positions + kAttnBlock - 1) / kAttnBlock;
+  a.tokens = T;
   return SPK_OK;
 }
 
@@ -794,7 +945,8 @@ extern "C" int spk_attention_prefill(const SpkAttnArgs* p, int32_t pos0, int32_t
   hipLaunchKernelGGL(attn_store_kv_kernel, dim3(tokens, kKvHeads), dim3(64), 0, s, a);
   rc = spk::check_launch("spk_attention_prefill (store)");
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_blocks_kernel, dim3(a.max_blocks, kKvHeads, tokens), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_prefill_blocks_kernel, dim3(a.max_blocks, kKvHeads, (tokens + kAttnGroup - 1) / kAttnGroup),
+                     dim3(256), 0, s, a);
   rc = spk::check_launch("spk_attention_prefill (blocks)");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(kQHeads, tokens), dim3(256), 0, s, a);

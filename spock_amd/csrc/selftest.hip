@@ -53,9 +53,11 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* __rest
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-// Grid-stride 16-byte non-temporal reads of the whole buffer.  Each thread's
-// XOR of what it read is stored only if it equals a fixed constant, so the
-// reads cannot be dropped and (almost) nothing is written.
+// Grid-stride 16-byte reads of the whole buffer, non-temporal (NT) or plain
+// cached loads.  Each thread's XOR of what it read is stored only if it equals
+// a fixed constant, so the reads cannot be dropped and (almost) nothing is
+// written.
+template <bool NT>
 __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, long long n16,
                                                           uint32_t* __restrict__ out) {
   uint32_t acc = 0;
@@ -65,7 +67,7 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const long long j = min(i + u * stride, n16 - 1);
-      v[u] = __builtin_nontemporal_load(p + j);
+      v[u] = NT ? __builtin_nontemporal_load(p + j) : p[j];
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
@@ -82,13 +84,18 @@ extern "C" int spk_selftest_mfma_peak(int32_t blocks, int32_t iters, float* out,
   return spk::check_launch("spk_selftest_mfma_peak");
 }
 
-extern "C" int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, uint32_t* out,
-                                        spk_stream_t stream) {
+extern "C" int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, int32_t cached,
+                                        uint32_t* out, spk_stream_t stream) {
   if (!p || !out) return spk::fail(SPK_ERR_NULL, "spk_selftest_stream_read: NULL pointer");
   if (bytes < 16 || bytes % 16 || blocks <= 0 || !spk::aligned(p, 16))
     return spk::fail(SPK_ERR_SHAPE, "spk_selftest_stream_read: bytes %zu blocks %d (16-byte multiple and alignment)",
                      bytes, blocks);
-  hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, spk::to_hip(stream),
-                     static_cast<const u32x4*>(p), (long long)(bytes / 16), out);
+  const u32x4* src = static_cast<const u32x4*>(p);
+  if (cached)
+    hipLaunchKernelGGL(stream_read_kernel<false>, dim3(blocks), dim3(256), 0, spk::to_hip(stream), src,
+                       (long long)(bytes / 16), out);
+  else
+    hipLaunchKernelGGL(stream_read_kernel<true>, dim3(blocks), dim3(256), 0, spk::to_hip(stream), src,
+                       (long long)(bytes / 16), out);
   return spk::check_launch("spk_selftest_stream_read");
 }

@@ -198,7 +198,7 @@ def test_attention_decode_bitexact(dev, pos):
     assert np.array_equal(_u16(d["out"]), exp)
 
 
-@pytest.mark.parametrize("pos0,T", [(0, 1), (0, 70), (30, 100), (190, 66)])
+@pytest.mark.parametrize("pos0,T", [(0, 1), (0, 3), (61, 5), (0, 70), (30, 100), (190, 66)])
 def test_attention_prefill_bitexact(dev, pos0, T):
     from spock_amd import _lib
     print(f"[attention prefill pos0={pos0} T={T}]", flush=True)
