@@ -19,6 +19,10 @@ cache cannot serve them.
 cpu_baseline: the reference's own chunk rule (oracle/_ref, compiled from
 src/runtime/deltanet_chunk.cpp, single-threaded) timed on a bounded sample of
 the same workload; the oracle restatement is used when _ref is absent.
+secondary.cpu_baselines holds the CPU path beside every secondary line
+(config 0 on one thread, config 2 split over heads on N threads, configs 1 and
+3 from the oracle's C restatement on one and N threads); the config-4 line
+carries its own (the oracle's full-model restatement, one thread).
 """
 from __future__ import annotations
 
@@ -331,7 +335,7 @@ def model_decode_bytes(layers=24, vocab=VOCAB, pos=MODEL_PROMPT + MODEL_NEW // 2
     return weights + state + kv
 
 
-def bench_model(steps, warmup, use_graph=True):
+def bench_model(steps, warmup, use_graph=True, cpu=False):
     """Config 4: the full Qwen3.5-0.8B-shaped random-init model, 512-token
     prompt, 128 greedy tokens at batch 1; decode is HBM-bound.  use_graph=False
     enqueues each decode step's kernels one by one instead of replaying the
@@ -369,6 +373,22 @@ def bench_model(steps, warmup, use_graph=True):
     res["decode_bytes_per_token"] = nbytes
     res["decode_achieved_gbs"] = round(nbytes / per_tok / 1e9, 1)
     res["decode_frac_hbm"] = round(nbytes / per_tok / 1e9 / HBM_PEAK_GBS, 4)
+    if cpu:
+        # the oracle's full-model restatement on the same artifact, one thread:
+        # an 8-token prompt, then 2 greedy tokens
+        sys.path.insert(0, str(ROOT / "tests"))
+        import oracle_model
+        om = oracle_model.OracleModel(art)
+        t0 = time.perf_counter()
+        tok = om.prefill(prompt[:8])
+        t1 = time.perf_counter()
+        for _ in range(2):
+            tok = om.decode(tok)
+        t2 = time.perf_counter()
+        res["cpu_baseline"] = {"prefill_tok_per_s": round(8 / (t1 - t0), 2),
+                               "decode_tok_per_s": round(2 / (t2 - t1), 3), "cores": 1, "kind": "port",
+                               "sample": "oracle full-model restatement: 8-token prompt, then 2 greedy tokens"}
+        del om
     import shutil
     shutil.rmtree(work, ignore_errors=True)
     return res
@@ -436,6 +456,85 @@ def cpu_baseline():
                       f"{med:.2f} s per run"}
 
 
+def _cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def _median_s(fn, reps=5):
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_baselines_secondary():
+    """The CPU path beside every secondary line, each on a bounded sample:
+    the reference's chunk rule (oracle/_ref when built, else the oracle
+    restatement) for configs 0 and 2, the oracle's C restatement of the
+    shader arithmetic for configs 1 and 3.  N-core variants split
+    independent units (heads, sequences, row ranges) over threads; ctypes
+    releases the GIL during each call."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from concurrent.futures import ThreadPoolExecutor
+    import oracle_lib
+    from spock_amd import synth
+    use_ref = oracle_lib.ref_available()
+    kind = "reference" if use_ref else "port"
+    nt = _cpu_threads()
+    out = {}
+    # config 0: the 104-token call, one thread
+    inp0 = synth.chunk_inputs(H, 104, seed=0)
+    s = _median_s(lambda: oracle_lib.chunk_rule(**inp0, use_ref=use_ref))
+    out["config0"] = {"value": round(104 / s, 1), "unit": "tok/s", "us_per_call": round(s * 1e6, 1), "cores": 1,
+                      "kind": kind, "sample": "the config-0 call (16 heads, T=104 -> 128), median of 5"}
+    # config 2, N cores: one 2048-token sequence, its 16 heads over threads
+    L = 2048
+    inp = synth.chunk_inputs(H, L, seed=3)
+    for n in ("q", "k", "v"):
+        inp[n] = inp[n].astype(np.float16).astype(np.float32)
+    heads = [{k: np.ascontiguousarray(v[h:h + 1]) for k, v in inp.items()} for h in range(H)]
+    with ThreadPoolExecutor(nt) as ex:
+        s = _median_s(lambda: list(ex.map(lambda a: oracle_lib.chunk_rule(**a, use_ref=use_ref), heads)), reps=3)
+    out["config2_ncore"] = {"value": round(L / s, 1), "unit": "tok/s", "cores": nt, "kind": kind,
+                            "sample": f"one {L}-token sequence, 16 heads split over {nt} threads, median of 3"}
+    # config 1: the decode step, B = 16 in one thread and split over threads
+    dec = synth.decode_inputs(16, seed=16)
+    s1 = _median_s(lambda: oracle_lib.decode_step(dec))
+    per_seq = [{k: (np.ascontiguousarray(v[b:b + 1]) if k in ("qkv", "state", "conv_state", "z", "a", "b") else v)
+                for k, v in dec.items()} for b in range(16)]
+    with ThreadPoolExecutor(nt) as ex:
+        sn = _median_s(lambda: list(ex.map(oracle_lib.decode_step, per_seq)))
+    out["config1_decode"] = {"unit": "sequence-steps/s", "b16_one_core": round(16 / s1, 1),
+                             "b16_ncore": round(16 / sn, 1), "cores": nt, "kind": "port",
+                             "sample": "one fused decode step of 16 sequences (oracle restatement), median of 5",
+                             "gbs_one_core": round(16 * DECODE_BYTES_PER_SEQ / s1 / 1e9, 2)}
+    # config 3: the six-GEMV chain (one thread) and lm_head + argmax on 1/16 of
+    # the vocabulary rows (one thread, and those rows split over threads)
+    Ws = [synth.gemv_weights(o, n, seed=j) for j, (o, n) in enumerate(CHAIN)]
+    xs = {n: synth.gemv_input(n, seed=5 + n) for n in (1024, 2048, 3584)}
+    s = _median_s(lambda: [oracle_lib.matvec_f16(W, xs[W.shape[1]]) for W in Ws])
+    rows = VOCAB // 16
+    Wl = synth.gemv_weights(rows, HIDDEN, seed=31)
+    x = synth.gemv_input(HIDDEN, seed=32)
+    sl = _median_s(lambda: oracle_lib.lm_head_argmax(Wl, x))
+    parts = [np.ascontiguousarray(Wl[i * rows // nt:(i + 1) * rows // nt]) for i in range(nt)]
+    with ThreadPoolExecutor(nt) as ex:
+        sln = _median_s(lambda: list(ex.map(lambda W: oracle_lib.lm_head_argmax(W, x), parts)))
+    out["config3"] = {"gemv_chain_us": round(s * 1e6, 1), "gemv_chain_gbs": round(sum(2 * o * n for o, n in CHAIN) / s / 1e9, 2),
+                      "lm_head_argmax_ms_one_core": round(sl * 16 * 1e3, 1),
+                      "lm_head_argmax_ms_ncore": round(sln * 16 * 1e3, 1), "cores": nt, "kind": "port",
+                      "sample": f"GEMV chain once per run; lm_head + argmax over {rows} of {VOCAB} rows, "
+                                "scaled x16 to the full vocabulary; medians of 5"}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -447,7 +546,7 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="model workload: launch the decode kernels one by one instead of the HIP graph")
-    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy", "model", "ceilings"],
+    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy", "model", "ceilings", "cpu"],
                     help="run one workload and print its own JSON (for profiler runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -465,6 +564,7 @@ def main():
         fns = {"prefill": bench_prefill, "config0": bench_config0, "gemv": bench_gemv_chain,
                "lm_head": bench_lm_head, "copy": bench_copy, "ceilings": bench_ceilings,
                "model": lambda s, w: bench_model(s, w, use_graph=not args.no_graph),
+        "cpu": lambda s, w: cpu_baselines_secondary(),
                "decode": lambda s, w: [bench_decode(B, s, w) for B in (1, 16, 64, 256)]}
         r = fns[args.only](args.steps, args.warmup)
         print(json.dumps({"only": args.only, "result": r}, default=float), flush=True)
@@ -487,13 +587,16 @@ def main():
         log(f"[bench] gemv chain {secondary['gemv_chain']}")
         secondary["lm_head_argmax"] = bench_lm_head(args.steps, args.warmup)
         log(f"[bench] lm_head {secondary['lm_head_argmax']}")
-        secondary["config4_full_model"] = bench_model(args.steps, args.warmup)
+        secondary["config4_full_model"] = bench_model(args.steps, args.warmup, cpu=not args.no_cpu_baseline)
         log(f"[bench] full model {secondary['config4_full_model']}")
         secondary["measured_ceilings"] = bench_ceilings(args.steps, args.warmup)
         log(f"[bench] measured ceilings {secondary['measured_ceilings']}")
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log(f"[bench] cpu baseline {cpu}")
+        if not args.no_secondary:
+            secondary["cpu_baselines"] = cpu_baselines_secondary()
+            log(f"[bench] cpu baselines {secondary['cpu_baselines']}")
     line = {
         "metric": METRIC,
         "value": round(value, 1),
