@@ -1,45 +1,56 @@
 // gemm.hip -- prompt-length projections: C[M][N] = fp16(A[M][K] . W[N][K]^T),
 // optionally fp16(R + fp16(A . W^T)) (the residual add after out_proj /
 // o_proj / down_proj), fp16 operands, fp32 accumulation on the matrix cores
-// (v_mfma_f32_32x32x8_f16).  This is the prefill form of every decode matvec
-// (matvec_tiled.comp applied to all prompt tokens at once); both operands are
-// K-contiguous, which is how the artifact stores weights.
+// (v_mfma_f32_32x32x16_f16, CDNA4's double-rate fp16 form).  This is the
+// prefill form of every decode matvec (matvec_tiled.comp applied to all prompt
+// tokens at once); both operands are K-contiguous, which is how the artifact
+// stores weights.
 //
 // Tiling: each wave computes 32 rows x (32·TN) columns (TN 32x32 MFMA tiles);
-// a workgroup holds WM x WN waves.  Two shapes: 64 x 128 (2 x 2 waves, TN = 2)
-// when that gives at least 256 workgroups, else 32 x 64 (1 x 2 waves, TN = 1)
-// so the N = 1024 projections of a 512-token prompt still fill the chip.  K in
-// steps of BK (64 when K allows, else 32) staged through LDS, double-buffered:
-// the next step's global loads are in flight while the current one is
-// multiplied.  LDS rows are padded by 8 halves so the 8-byte fragment reads of
-// one MFMA spread over the banks.
+// a workgroup holds WM x WN x KS waves, the KS groups splitting each staged
+// K step and adding their partials in order at the end.  Shapes:
+//   64 x 128 (2 x 2 waves, TN = 2) when that gives at least 256 workgroups;
+//   32 x 64 with KS = 4 and K steps of 256 when 32 x 64 tiles number fewer
+//     than 512 and K allows (the N = 1024 out/o/down projections of a
+//     512-token prompt: 256 workgroups of 8 waves, a quarter of the K steps,
+//     so 4x the bytes in flight per step of memory latency);
+//   32 x 64 (1 x 2 waves) otherwise.
+// K in steps of BK staged through LDS, double-buffered: the next step's global
+// loads are in flight while the current one is multiplied.  LDS rows are
+// padded by 8 halves so the 16-byte fragment reads of 16 consecutive lanes
+// (16 consecutive rows) fall in distinct banks.
 #include "capi_common.hpp"
 #include "numerics.hpp"
 
 namespace {
 
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-template <int WM, int WN, int TN, int BK, bool RES>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(const uint16_t* __restrict__ A,
-                                                              const uint16_t* __restrict__ W,
-                                                              uint16_t* __restrict__ C,
-                                                              const uint16_t* __restrict__ R, int M, int N, int K,
-                                                              long long lda, long long ldw, long long ldc) {
+template <int WM, int WN, int TN, int KS, int BK, bool RES>
+__global__ __launch_bounds__(64 * WM * WN * KS) void gemm_nt_kernel(const uint16_t* __restrict__ A,
+                                                                   const uint16_t* __restrict__ W, uint16_t* C,
+                                                                   const uint16_t* R, int M, int N, int K,
+                                                                   long long lda, long long ldw, long long ldc) {
   constexpr int BM = 32 * WM, BN = 32 * WN * TN, LDK = BK + 8;
-  constexpr int NT = 64 * WM * WN;
+  constexpr int NT = 64 * WM * WN * KS;
   constexpr int PPR = BK / 8;                     // 16-byte pieces per row per step
   constexpr int P = (BM + BN) * PPR / NT;         // pieces per thread per step
+  constexpr int KW = BK / KS;                     // k values per wave per step
   static_assert((BM + BN) * PPR % NT == 0, "staging must divide evenly");
-  __shared__ __align__(16) uint16_t As[2][BM][LDK];
-  __shared__ __align__(16) uint16_t Ws[2][BN][LDK];
+  static_assert(KW % 16 == 0, "a wave's k range is whole 32x32x16 steps");
+  static_assert(KS == 1 || (KS - 1) * WM * WN * TN * 1024 * 4 <= 2 * (BM + BN) * LDK * 2,
+                "the k-split partials fit in the staging buffers");
+  __shared__ __align__(16) uint16_t smem[2 * (BM + BN) * LDK];
+  auto As = reinterpret_cast<uint16_t(*)[BM][LDK]>(smem);
+  auto Ws = reinterpret_cast<uint16_t(*)[BN][LDK]>(smem + 2 * BM * LDK);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;
-  const int wm = wave / WN, wn = wave % WN;
+  const int ks = wave / (WM * WN), wmn = wave % (WM * WN);
+  const int wm = wmn / WN, wn = wmn % WN;
 
   // global -> register staging; rows past M / N read row 0 and stage zeros
   const uint16_t* src[P];
@@ -81,7 +92,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(const uint16_t* _
     for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
 
   const int fr = lane & 31;        // fragment row (A) / column (B)
-  const int fk = (lane >> 5) * 4;  // fragment k offset within a step of 8
+  const int fk = (lane >> 5) * 8;  // fragment k offset within a step of 16
   load(0);
   store(0);
   __syncthreads();
@@ -90,18 +101,38 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(const uint16_t* _
     const int buf = kt & 1;
     if (kt + 1 < nk) load((kt + 1) * BK);
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 8) {
-      const half4_t a = *reinterpret_cast<const half4_t*>(&As[buf][wm * 32 + fr][kk + fk]);
+    for (int i = 0; i < KW / 16; ++i) {
+      const int kk = ks * KW + 16 * i;
+      const half8_t a = *reinterpret_cast<const half8_t*>(&As[buf][wm * 32 + fr][kk + fk]);
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
-        const half4_t b = *reinterpret_cast<const half4_t*>(&Ws[buf][(wn * TN + t) * 32 + fr][kk + fk]);
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, acc[t], 0, 0, 0);
+        const half8_t b = *reinterpret_cast<const half8_t*>(&Ws[buf][(wn * TN + t) * 32 + fr][kk + fk]);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[t], 0, 0, 0);
       }
     }
     if (kt + 1 < nk) {
       store(buf ^ 1);
       __syncthreads();
     }
+  }
+  if constexpr (KS > 1) {
+    // k-split partials: waves ks > 0 park theirs in the staging buffers, the
+    // ks = 0 waves add them in ks order
+    float* red = reinterpret_cast<float*>(smem);
+    __syncthreads();
+    if (ks > 0) {
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[(((ks - 1) * (WM * WN) + wmn) * TN + t) * 1024 + r * 64 + lane] = acc[t][r];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+    for (int j = 1; j < KS; ++j)
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] += red[(((j - 1) * (WM * WN) + wmn) * TN + t) * 1024 + r * 64 + lane];
   }
   // D[i][j]: lane j = lane%32, row i = 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll
@@ -119,17 +150,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(const uint16_t* _
   }
 }
 
-template <int WM, int WN, int TN, int BK>
+template <int WM, int WN, int TN, int KS, int BK>
 void launch_gemm(const uint16_t* A, const uint16_t* W, uint16_t* C, const uint16_t* R, int M, int N, int K,
                  long long lda, long long ldw, long long ldc, hipStream_t s) {
   constexpr int BM = 32 * WM, BN = 32 * WN * TN;
   const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+  const dim3 block(64 * WM * WN * KS);
   if (R)
-    hipLaunchKernelGGL((gemm_nt_kernel<WM, WN, TN, BK, true>), grid, dim3(64 * WM * WN), 0, s, A, W, C, R, M, N, K,
-                       lda, ldw, ldc);
+    hipLaunchKernelGGL((gemm_nt_kernel<WM, WN, TN, KS, BK, true>), grid, block, 0, s, A, W, C, R, M, N, K, lda, ldw,
+                       ldc);
   else
-    hipLaunchKernelGGL((gemm_nt_kernel<WM, WN, TN, BK, false>), grid, dim3(64 * WM * WN), 0, s, A, W, C, R, M, N,
-                       K, lda, ldw, ldc);
+    hipLaunchKernelGGL((gemm_nt_kernel<WM, WN, TN, KS, BK, false>), grid, block, 0, s, A, W, C, R, M, N, K, lda,
+                       ldw, ldc);
 }
 
 }  // namespace
@@ -148,16 +180,18 @@ extern "C" int spk_gemm_f16(const uint16_t* A, int64_t lda, const uint16_t* W, i
     return spk::fail(SPK_ERR_ARG, "spk_gemm_f16: the output or residual aliases an operand");
   hipStream_t s = spk::to_hip(stream);
   const bool big = (long long)((N + 127) / 128) * ((M + 63) / 64) >= 256;
-  if (K % 64 == 0) {
-    if (big)
-      launch_gemm<2, 2, 2, 64>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
+  const long long tiles32x64 = (long long)((N + 63) / 64) * ((M + 31) / 32);
+  if (big) {
+    if (K % 64 == 0)
+      launch_gemm<2, 2, 2, 1, 64>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
     else
-      launch_gemm<1, 2, 1, 64>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
+      launch_gemm<2, 2, 2, 1, 32>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
+  } else if (tiles32x64 < 512 && K % 256 == 0) {
+    launch_gemm<1, 2, 1, 4, 256>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
+  } else if (K % 64 == 0) {
+    launch_gemm<1, 2, 1, 1, 64>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
   } else {
-    if (big)
-      launch_gemm<2, 2, 2, 32>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
-    else
-      launch_gemm<1, 2, 1, 32>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
+    launch_gemm<1, 2, 1, 1, 32>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
   }
   return spk::check_launch("spk_gemm_f16");
 }
