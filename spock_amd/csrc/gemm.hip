@@ -8,13 +8,15 @@
 //
 // Tiling: each wave computes 32 rows x (32·TN) columns (TN 32x32 MFMA tiles);
 // a workgroup holds WM x WN x KS waves, the KS groups splitting each staged
-// K step and adding their partials in order at the end.  Shapes:
-//   64 x 128 (2 x 2 waves, TN = 2) when that gives at least 256 workgroups;
+// K step and adding their partials in order at the end.  Shapes (chosen by a
+// sweep of time per shape; see spk_gemm_f16):
 //   32 x 64 with KS = 4 and K steps of 256 when 32 x 64 tiles number fewer
-//     than 512 and K allows (the N = 1024 out/o/down projections of a
-//     512-token prompt: 256 workgroups of 8 waves, a quarter of the K steps,
-//     so 4x the bytes in flight per step of memory latency);
-//   32 x 64 (1 x 2 waves) otherwise.
+//     than 512 and K allows (the N <= 1024 projections of a 512-token prompt:
+//     256 workgroups of 8 waves, a quarter of the K steps, so 4x the bytes in
+//     flight per step of memory latency);
+//   64 x 64 with KS = 4 up to 384 such tiles (N = 2048 at M = 512);
+//   64 x 64 (2 x 2 waves) for wider outputs, 64 x 128 (TN = 2) only for
+//   outputs large enough to fill the chip four times over.
 // K in steps of BK staged through LDS, double-buffered: the next step's global
 // loads are in flight while the current one is multiplied.  LDS rows are
 // padded by 8 halves so the 16-byte fragment reads of 16 consecutive lanes
@@ -179,19 +181,22 @@ extern "C" int spk_gemm_f16(const uint16_t* A, int64_t lda, const uint16_t* W, i
   if (residual == A || residual == W || C == A || C == W)
     return spk::fail(SPK_ERR_ARG, "spk_gemm_f16: the output or residual aliases an operand");
   hipStream_t s = spk::to_hip(stream);
-  const bool big = (long long)((N + 127) / 128) * ((M + 63) / 64) >= 256;
-  const long long tiles32x64 = (long long)((N + 63) / 64) * ((M + 31) / 32);
-  if (big) {
-    if (K % 64 == 0)
-      launch_gemm<2, 2, 2, 1, 64>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
-    else
-      launch_gemm<2, 2, 2, 1, 32>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
-  } else if (tiles32x64 < 512 && K % 256 == 0) {
+  // tile shape by measured time on MI355X at the config-4 prompt shapes
+  // (M = 512, K = 1024/2048/3584): k-split 32 x 64 tiles while they number
+  // fewer than 512, k-split 64 x 64 up to 384 tiles, plain 64 x 64 above and
+  // 64 x 128 only when its tiles alone fill four waves of workgroups per CU
+  const long long t32x64 = (long long)((N + 63) / 64) * ((M + 31) / 32);
+  const long long t64x64 = (long long)((N + 63) / 64) * ((M + 63) / 64);
+  const long long t64x128 = (long long)((N + 127) / 128) * ((M + 63) / 64);
+  if (K % 256 == 0 && t32x64 < 512)
     launch_gemm<1, 2, 1, 4, 256>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
-  } else if (K % 64 == 0) {
-    launch_gemm<1, 2, 1, 1, 64>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
-  } else {
-    launch_gemm<1, 2, 1, 1, 32>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
-  }
+  else if (K % 256 == 0 && t64x64 < 384)
+    launch_gemm<2, 2, 1, 4, 256>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
+  else if (K % 64 == 0 && t64x128 >= 1024)
+    launch_gemm<2, 2, 2, 1, 64>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
+  else if (K % 64 == 0)
+    launch_gemm<2, 2, 1, 1, 64>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
+  else
+    launch_gemm<2, 2, 1, 1, 32>(A, W, C, residual, M, N, K, lda, ldw, ldc, s);
   return spk::check_launch("spk_gemm_f16");
 }

@@ -344,7 +344,8 @@ def test_deltanet_prefill_gbeta_and_norm_gate_bitexact(dev, oracle):
 
 @pytest.mark.parametrize("M,N,K,res", [(512, 6144, 1024, False), (37, 16, 1024, False), (100, 1000, 64, True),
                                        (70, 1024, 3584, True), (512, 1024, 2048, True), (512, 3584, 1024, False),
-                                       (33, 40, 96, True), (300, 6000, 96, False)])
+                                       (33, 40, 96, True), (300, 6000, 96, False), (512, 2048, 1024, True),
+                                       (2048, 4096, 64, False)])
 def test_gemm_f16_against_fp64(dev, M, N, K, res):
     from spock_amd import _lib
     print(f"[gemm {M}x{N}x{K}]", flush=True)
