@@ -20,12 +20,13 @@
 //     and W are MFMA products over the nonzero blocks of T with beta and the
 //     decays applied to the B operand as it is read.  U^T, W, A, raw K^T and
 //     per-token scales go to the workspace.
-//  2. chunk_state_kernel -- one workgroup per (sequence, head, 32-column tile
+//  2. chunk_state_kernel -- one workgroup per (sequence, head, 16-column tile
 //     of the value dim): columns of S evolve independently, so the sequential
-//     chunk scan runs on 4*H*num_seqs workgroups.  The 128x32 state tile lives
-//     in LDS; each wavefront owns 16 rows of [W; Q e^g] S, of the output and
-//     of the state update (S += K^T diag(Ks) v_new), all 16x16x4 MFMA, with the
-//     next chunk's operands prefetched into registers during the current one.
+//     chunk scan runs on 8*H*num_seqs workgroups.  The 128x16 state tile lives
+//     in LDS; wavefront M owns token block M of W S, Q S and the output, and
+//     state rows 32M..32M+31 of the update (S += K^T diag(Ks) v_new), all
+//     16x16x4 MFMA, with the next chunk's operands prefetched into registers
+//     during the current one.
 // MFMA operand trick: the contraction index of a 16x16x4 step is a free
 // permutation, so lane (m = l%16, g = l/16) reads a float4 at k = 16u + 4g and
 // feeds its elements to 4 consecutive steps; the B operand uses the same map.
