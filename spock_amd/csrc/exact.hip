@@ -221,6 +221,102 @@ __global__ __launch_bounds__(256) void matvec_rows_mfma_kernel(RowsArgs a, int n
     }
 }
 
+// in_dim 2048 / 3584 (S = 32 / 56): the same leaves, order and tree as
+// matvec_rows_mfma_kernel, with each leaf's operands staged through LDS by
+// coalesced loads (a span is 64 / 112 contiguous bytes; the lanes of a load
+// walk a span's 16-byte pieces, then the next block's span, then the next
+// row) instead of per-lane loads from 64 separate rows, which saturate the
+// vector-memory address pipe.  Workgroup tile: 16*WR W rows x 16*WT prompt
+// rows, one 16 x 16 MFMA tile per wave; the next leaf's pieces are loaded into
+// registers while the current leaf is multiplied.  LDS rows hold the 4 spans
+// of a leaf (4*S halves) plus 8 halves of padding, so the 16-byte fragment
+// reads of 16 consecutive rows fall in distinct banks.
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+template <int S, int WR, int WT>
+__global__ __launch_bounds__(64 * WR * WT) void matvec_rows_lds_kernel(RowsArgs a) {
+  constexpr int NT = 64 * WR * WT;
+  constexpr int LD = 4 * S + 8;
+  constexpr int PPS = S / 8;                              // 16-byte pieces per span
+  constexpr int PPR = 4 * PPS;                            // pieces per staged row
+  constexpr int NPW = 16 * WR * PPR, NP = NPW + 16 * WT * PPR;
+  constexpr int P = (NP + NT - 1) / NT;                   // pieces per thread
+  __shared__ __align__(16) uint16_t lds[(16 * WR + 16 * WT) * LD];  // W rows, then X rows
+  auto Ws = reinterpret_cast<uint16_t(*)[LD]>(lds);
+  auto Xs = reinterpret_cast<uint16_t(*)[LD]>(lds + 16 * WR * LD);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int blk = lane >> 4, li = lane & 15;
+  const int wr = wave % WR, wt = wave / WR;
+  const int r0 = blockIdx.x * 16 * WR, t0 = blockIdx.y * 16 * WT;
+  // piece p of this thread: staged row, block, piece within the span
+  const uint16_t* src[P];
+  int dst[P];
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    const int pc = min(tid + NT * k, NP - 1);  // the tail re-stages the last piece
+    const bool isw = pc < NPW;
+    const int pr = isw ? pc : pc - NPW;
+    const int row = pr / PPR, b = (pr % PPR) / PPS, q = pr % PPS;
+    src[k] = isw ? a.W + (size_t)min(r0 + row, a.out_dim - 1) * a.in_dim + b * 16 * S + 8 * q
+                 : a.X + (size_t)min(t0 + row, a.rows - 1) * a.ldx + b * 16 * S + 8 * q;
+    dst[k] = (isw ? 0 : 16 * WR * LD) + row * LD + b * S + 8 * q;
+  }
+  // leaf v: span l = bitrev4(v) (+16 per block)
+  auto span_off = [](int v) { return (int)(__builtin_bitreverse32((uint32_t)v) >> 28) * S; };
+  v4u pv[P];  // a native vector type, which the compiler keeps in registers
+#pragma unroll
+  for (int k = 0; k < P; ++k) pv[k] = *reinterpret_cast<const v4u*>(src[k]);
+  float stack[4][4];
+  float cur[4];
+#pragma unroll 1
+  for (int v = 0; v < 16; ++v) {
+    __syncthreads();  // the previous leaf's fragment reads are done
+#pragma unroll
+    for (int k = 0; k < P; ++k) *reinterpret_cast<v4u*>(lds + dst[k]) = pv[k];
+    __syncthreads();
+    const int noff = span_off(min(v + 1, 15));
+#pragma unroll
+    for (int k = 0; k < P; ++k) pv[k] = *reinterpret_cast<const v4u*>(src[k] + noff);
+    v16f acc = v16f{};
+#pragma unroll
+    for (int c = 0; c < PPS; ++c) {
+      float wf[8], xf[8];
+      unpack8h(*reinterpret_cast<const uint4*>(&Ws[16 * wr + li][blk * S + 8 * c]), wf);
+      unpack8h(*reinterpret_cast<const uint4*>(&Xs[16 * wt + li][blk * S + 8 * c]), xf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x1f32(wf[e], xf[e], acc, 0, 0, 0);
+    }
+    // (P_l + P_{l+32}) + (P_{l+16} + P_{l+48})
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cur[k] = (acc[k] + acc[8 + k]) + (acc[4 + k] + acc[12 + k]);
+    // binary-counter merge: visits v and v ^ (1 << lev) pair at level lev
+    bool carry = true;
+#pragma unroll
+    for (int lev = 0; lev < 4; ++lev) {
+      if (carry) {
+        if ((v >> lev) & 1) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) cur[q] = stack[lev][q] + cur[q];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) stack[lev][q] = cur[q];
+          carry = false;
+        }
+      }
+    }
+  }
+  const int t = t0 + 16 * wt + li;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = r0 + 16 * wr + 4 * blk + k;
+    if (r < a.out_dim && t < a.rows) {
+      uint16_t o = spk::f2h(cur[k]);
+      if (a.R) o = spk::f2h(spk::h2f(a.R[(long long)t * a.ldy + r]) + spk::h2f(o));
+      a.Y[(long long)t * a.ldy + r] = o;
+    }
+  }
+}
+
 // in_dim == 1024 (S = 16, a span is 32 B): the same leaves and tree, with
 // operands staged through LDS four leaves at a time.  Leaves v, v+4, v+8,
 // v+12 (v < 4) are l = L..L+3 with L = bitrev4(v), i.e. spans L..L+3 (+16b
@@ -762,6 +858,14 @@ extern "C" int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t
   if (S == 16 && vec_ok && (long long)((out_dim + kGrpRows - 1) / kGrpRows) * ((rows + kGrpToks - 1) / kGrpToks) >= 256) {
     const dim3 grid((out_dim + kGrpRows - 1) / kGrpRows, (rows + kGrpToks - 1) / kGrpToks);
     hipLaunchKernelGGL(matvec_rows_grp_kernel, grid, dim3(256), 0, s, a);
+    return spk::check_launch("spk_matvec_f16_rows");
+  }
+  if ((S == 32 || S == 56) && vec_ok && (long long)((out_dim + 31) / 32) * ((rows + 31) / 32) >= 256) {
+    const dim3 grid((out_dim + 31) / 32, (rows + 31) / 32);
+    if (S == 32)
+      hipLaunchKernelGGL((matvec_rows_lds_kernel<32, 2, 2>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((matvec_rows_lds_kernel<56, 2, 2>), grid, dim3(256), 0, s, a);
     return spk::check_launch("spk_matvec_f16_rows");
   }
   if ((S == 16 || S == 32 || S == 56) && vec_ok) {

@@ -379,7 +379,8 @@ def test_gemm_f16_against_fp64(dev, M, N, K, res):
 
 @pytest.mark.parametrize("rows,out_dim,in_dim,res", [(1, 6144, 1024, False), (70, 1000, 2048, True),
                                                      (133, 16, 1024, False), (65, 1024, 3584, True),
-                                                     (200, 6144, 1024, True), (300, 2600, 1024, False)])
+                                                     (200, 6144, 1024, True), (300, 2600, 1024, False),
+                                                     (300, 1000, 2048, False), (260, 1024, 3584, True)])
 def test_matvec_rows_bitexact(dev, rows, out_dim, in_dim, res):
     """spk_matvec_f16_rows: each row bit-identical to the decode matvec order."""
     from spock_amd import _lib
