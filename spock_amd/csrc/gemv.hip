@@ -225,7 +225,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
 // results).  A wavefront issues all of its weight loads (batch_rows rows x
 // n8 16-byte loads per lane) before it reads x; one or two rows per
 // wavefront (many workgroups) measured fastest for decode-sized projections.
-constexpr int kMaxBatch = 8;
+constexpr int kMaxBatch = 4;
 __host__ __device__ constexpr int batch_rows(int n8) { return n8 <= 2 ? 2 : 1; }
 struct GemvBatch {
   const uint16_t* W[kMaxBatch];
@@ -281,16 +281,29 @@ __device__ __forceinline__ void batched_rows(const uint16_t* __restrict__ W, con
 }
 
 __global__ __launch_bounds__(256) void gemv_batched_kernel(GemvBatch b) {
-  int d = 0;
+  // Every descriptor is read and the workgroup's one selected by value, so
+  // all kernel-argument loads go out in one round trip (indexing the arrays
+  // by the selected d would wait for first_block before loading W, x, y).
+  const uint16_t* W = b.W[0];
+  const uint16_t* x = b.x[0];
+  uint16_t* y = b.y[0];
+  int out_dim = b.out_dim[0], n8 = b.n8[0], fb = 0;
 #pragma unroll
-  for (int i = 1; i < kMaxBatch; ++i)
-    if (i < b.count && (int)blockIdx.x >= b.first_block[i]) d = i;
+  for (int i = 1; i < kMaxBatch; ++i) {
+    const bool take = i < b.count && (int)blockIdx.x >= b.first_block[i];
+    W = take ? b.W[i] : W;
+    x = take ? b.x[i] : x;
+    y = take ? b.y[i] : y;
+    out_dim = take ? b.out_dim[i] : out_dim;
+    n8 = take ? b.n8[i] : n8;
+    fb = take ? b.first_block[i] : fb;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int blk = (int)blockIdx.x - b.first_block[d];
-  switch (b.n8[d]) {
-#define SPK_BATCH_CASE(n8) \
-  case n8: batched_rows<n8>(b.W[d], b.x[d], b.y[d], b.out_dim[d], blk, wave, lane); break;
+  const int blk = (int)blockIdx.x - fb;
+  switch (n8) {
+#define SPK_BATCH_CASE(n8_) \
+  case n8_: batched_rows<n8_>(W, x, y, out_dim, blk, wave, lane); break;
     SPK_BATCH_CASE(1)
     SPK_BATCH_CASE(2)
     SPK_BATCH_CASE(3)
@@ -298,7 +311,7 @@ __global__ __launch_bounds__(256) void gemv_batched_kernel(GemvBatch b) {
     SPK_BATCH_CASE(5)
     SPK_BATCH_CASE(6)
     SPK_BATCH_CASE(7)
-    default: batched_rows<8>(b.W[d], b.x[d], b.y[d], b.out_dim[d], blk, wave, lane); break;
+    default: batched_rows<8>(W, x, y, out_dim, blk, wave, lane); break;
 #undef SPK_BATCH_CASE
   }
 }

@@ -74,7 +74,8 @@ __device__ __forceinline__ float block_tree256(float p, float* red) {
 // silu_gate.comp: y = fp16(silu(fp16(W . x)) * fp16(W2 . x)), both rows of a
 // pair computed by the same wave.
 // ---------------------------------------------------------------------------
-constexpr int kMaxOut = 8;
+constexpr int kMaxOut = 8;     // outputs per spk_gemv_fused call
+constexpr int kLaunchOut = 4;  // outputs per launch (more are split over launches)
 constexpr int kMaxIn = 4096;
 
 struct FusedGemv {
@@ -86,12 +87,12 @@ struct FusedGemv {
   int token_rows;
   uint16_t* h_out;
   int count;
-  const uint16_t* W[kMaxOut];
-  const uint16_t* W2[kMaxOut];
-  uint16_t* y[kMaxOut];
-  const uint16_t* res[kMaxOut];
-  int out_dim[kMaxOut];
-  int first_block[kMaxOut + 1];
+  const uint16_t* W[kLaunchOut];
+  const uint16_t* W2[kLaunchOut];
+  uint16_t* y[kLaunchOut];
+  const uint16_t* res[kLaunchOut];
+  int out_dim[kLaunchOut];
+  int first_block[kLaunchOut + 1];
 };
 
 template <int N8, int R>
@@ -127,16 +128,30 @@ template <int N8, int R, bool PAIR, int KIND>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   __shared__ float xs[kMaxIn];
   __shared__ float red[257];
-  int d = 0;
+  // Every output's descriptor is read and the workgroup's one selected by
+  // value, so all kernel-argument loads go out in one round trip (indexing
+  // the arrays by the selected output would wait for first_block before
+  // loading the weight pointers).
+  const uint16_t* Wd = a.W[0];
+  const uint16_t* W2d = a.W2[0];
+  uint16_t* yd = a.y[0];
+  const uint16_t* resd = a.res[0];
+  int out_dim = a.out_dim[0], fb = 0;
 #pragma unroll
-  for (int i = 1; i < kMaxOut; ++i)
-    if (i < a.count && (int)blockIdx.x >= a.first_block[i]) d = i;
+  for (int i = 1; i < kLaunchOut; ++i) {
+    const bool take = i < a.count && (int)blockIdx.x >= a.first_block[i];
+    Wd = take ? a.W[i] : Wd;
+    W2d = take ? a.W2[i] : W2d;
+    yd = take ? a.y[i] : yd;
+    resd = take ? a.res[i] : resd;
+    out_dim = take ? a.out_dim[i] : out_dim;
+    fb = take ? a.first_block[i] : fb;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   constexpr int in_dim = 512 * N8;
-  const int out_dim = a.out_dim[d];
-  const int row0 = (((int)blockIdx.x - a.first_block[d]) * 4 + wave) * R;
+  const int row0 = (((int)blockIdx.x - fb) * 4 + wave) * R;
   constexpr int NV = in_dim / 8;  // 16-byte pieces of x
   constexpr int PER = (NV + 255) / 256;
   static_assert(256 * PER * 8 <= kMaxIn, "x staging overruns xs");
@@ -160,15 +175,15 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   }
   // residual rows (or, without a residual, any in-bounds halves) ahead of
   // the weights, so the epilogue waits on no load of its own
-  const uint16_t* __restrict__ res = a.res[d];
-  const uint16_t* rsrc = res ? res : a.W[d];
+  const uint16_t* __restrict__ res = resd;
+  const uint16_t* rsrc = res ? res : Wd;
   uint16_t rv[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) rv[r] = rsrc[min(row0 + r, out_dim - 1)];
   uint4 wv[R][N8];
   uint4 wv2[PAIR ? R : 1][N8];
-  load_rows<N8, R>(a.W[d], row0, out_dim, lane, wv);
-  if (PAIR) load_rows<N8, PAIR ? R : 1>(a.W2[d], row0, out_dim, lane, wv2);
+  load_rows<N8, R>(Wd, row0, out_dim, lane, wv);
+  if (PAIR) load_rows<N8, PAIR ? R : 1>(W2d, row0, out_dim, lane, wv2);
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue
   if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {
     const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
@@ -218,7 +233,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
     if (PAIR) acc[R + r] = lane_dot<N8>(wv2[PAIR ? r : 0], xf);
   }
   spk::tree64_rows<NT>(acc);
-  uint16_t* __restrict__ y = a.y[d];
+  uint16_t* __restrict__ y = yd;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r;
@@ -787,62 +802,34 @@ int grid_for(long long n) {
 // C ABI
 // ---------------------------------------------------------------------------
 
-extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count,
-                              spk_stream_t stream) {
-  if (!in || (count > 0 && !outs)) return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: NULL argument");
-  if (count < 1 || count > kMaxOut) return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: count %d (1..%d)", count, kMaxOut);
-  const int in_dim = in->in_dim;
-  if (in->kind < SPK_GEMV_IN_PLAIN || in->kind > SPK_GEMV_IN_SILU_GATE)
-    return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: input kind %d", in->kind);
-  if (in_dim <= 0 || in_dim % 512 != 0 || in_dim > kMaxIn)
-    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: in_dim %d (multiple of 512, <= %d)", in_dim, kMaxIn);
-  if (in->kind == SPK_GEMV_IN_RMSNORM && in_dim != kHidden)
-    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: RMSNorm input needs in_dim %d", kHidden);
-  if (!in->x || (in->kind != SPK_GEMV_IN_PLAIN && !in->x2))
-    return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: NULL input vector");
-  if (in->kind != SPK_GEMV_IN_RMSNORM && (in->token || in->h_out))
-    return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: token/h_out need the RMSNorm input");
-  if (in->token && in->token_rows <= 0)
-    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: token_rows %d", in->token_rows);
-  if (!spk::aligned(in->x, 16) || (in->x2 && !spk::aligned(in->x2, 16)) || (in->h_out && !spk::aligned(in->h_out, 16)))
-    return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: input vectors must be 16-byte aligned");
+// One launch of up to kLaunchOut outputs of spk_gemv_fused (validated by the
+// caller); only the first launch of a call writes h_out.
+static int launch_fused_gemv(const SpkGemvInput* in, const SpkGemvOutput* outs, int count, bool first, int n8, int R,
+                             spk_stream_t stream) {
   FusedGemv a;
   a.kind = in->kind;
-  a.in_dim = in_dim;
+  a.in_dim = in->in_dim;
   a.x = in->x;
   a.x2 = in->x2;
   a.token = in->token;
   a.token_rows = in->token_rows;
-  a.h_out = in->h_out;
+  a.h_out = first ? in->h_out : nullptr;
   a.count = count;
-  const int n8 = in_dim / 512;
-  const int R = n8 <= 2 ? 2 : 1;
   int blocks = 0;
   for (int i = 0; i < count; ++i) {
-    const SpkGemvOutput& o = outs[i];
-    if (!o.W || !o.y) return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: output %d has a NULL pointer", i);
-    if (o.out_dim <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: output %d out_dim %d", i, o.out_dim);
-    if (!spk::aligned(o.W, 16)) return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: W %d must be 16-byte aligned", i);
-    // y may be the residual (in-place update of the stream) but never an input of this launch.
-    if (o.y == in->x || o.y == in->x2)
-      return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: output %d aliases the input vector", i);
-    if ((o.W_up != nullptr) != (outs[0].W_up != nullptr))
-      return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: SiLU-gated pairs and plain outputs in one launch");
-    if (o.W_up && !spk::aligned(o.W_up, 16))
-      return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: W_up %d must be 16-byte aligned", i);
-    a.W[i] = o.W;
-    a.W2[i] = o.W_up;
-    a.y[i] = o.y;
-    a.res[i] = o.residual;
-    a.out_dim[i] = o.out_dim;
+    a.W[i] = outs[i].W;
+    a.W2[i] = outs[i].W_up;
+    a.y[i] = outs[i].y;
+    a.res[i] = outs[i].residual;
+    a.out_dim[i] = outs[i].out_dim;
     a.first_block[i] = blocks;
-    blocks += (o.out_dim + 4 * R - 1) / (4 * R);
+    blocks += (outs[i].out_dim + 4 * R - 1) / (4 * R);
   }
-  for (int i = count; i < kMaxOut; ++i) {
+  for (int i = count; i < kLaunchOut; ++i) {
     a.W[i] = nullptr; a.W2[i] = nullptr; a.y[i] = nullptr; a.res[i] = nullptr; a.out_dim[i] = 0;
     a.first_block[i] = blocks;
   }
-  a.first_block[kMaxOut] = blocks;
+  a.first_block[kLaunchOut] = blocks;
   hipStream_t s = spk::to_hip(stream);
   const bool pair = outs[0].W_up != nullptr;
 #define SPK_FGK(n8, r, kind)                                                                            \
@@ -871,11 +858,52 @@ extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs,
     SPK_FG(6, 1)
     SPK_FG(7, 1)
     SPK_FG(8, 1)
-    default: return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: in_dim %d", in_dim);
+    default: return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: in_dim %d", in->in_dim);
   }
 #undef SPK_FGK
 #undef SPK_FG
   return spk::check_launch("spk_gemv_fused");
+}
+
+extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count,
+                              spk_stream_t stream) {
+  if (!in || (count > 0 && !outs)) return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: NULL argument");
+  if (count < 1 || count > kMaxOut) return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: count %d (1..%d)", count, kMaxOut);
+  const int in_dim = in->in_dim;
+  if (in->kind < SPK_GEMV_IN_PLAIN || in->kind > SPK_GEMV_IN_SILU_GATE)
+    return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: input kind %d", in->kind);
+  if (in_dim <= 0 || in_dim % 512 != 0 || in_dim > kMaxIn)
+    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: in_dim %d (multiple of 512, <= %d)", in_dim, kMaxIn);
+  if (in->kind == SPK_GEMV_IN_RMSNORM && in_dim != kHidden)
+    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: RMSNorm input needs in_dim %d", kHidden);
+  if (!in->x || (in->kind != SPK_GEMV_IN_PLAIN && !in->x2))
+    return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: NULL input vector");
+  if (in->kind != SPK_GEMV_IN_RMSNORM && (in->token || in->h_out))
+    return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: token/h_out need the RMSNorm input");
+  if (in->token && in->token_rows <= 0)
+    return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: token_rows %d", in->token_rows);
+  if (!spk::aligned(in->x, 16) || (in->x2 && !spk::aligned(in->x2, 16)) || (in->h_out && !spk::aligned(in->h_out, 16)))
+    return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: input vectors must be 16-byte aligned");
+  for (int i = 0; i < count; ++i) {
+    const SpkGemvOutput& o = outs[i];
+    if (!o.W || !o.y) return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: output %d has a NULL pointer", i);
+    if (o.out_dim <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_gemv_fused: output %d out_dim %d", i, o.out_dim);
+    if (!spk::aligned(o.W, 16)) return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: W %d must be 16-byte aligned", i);
+    // y may be the residual (in-place update of the stream) but never an input of this launch.
+    if (o.y == in->x || o.y == in->x2)
+      return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: output %d aliases the input vector", i);
+    if ((o.W_up != nullptr) != (outs[0].W_up != nullptr))
+      return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: SiLU-gated pairs and plain outputs in one launch");
+    if (o.W_up && !spk::aligned(o.W_up, 16))
+      return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: W_up %d must be 16-byte aligned", i);
+  }
+  const int n8 = in_dim / 512;
+  const int R = n8 <= 2 ? 2 : 1;
+  for (int c0 = 0; c0 < count; c0 += kLaunchOut) {
+    const int rc = launch_fused_gemv(in, outs + c0, (count - c0 < kLaunchOut ? count - c0 : kLaunchOut), c0 == 0, n8, R, stream);
+    if (rc) return rc;
+  }
+  return SPK_OK;
 }
 
 extern "C" size_t spk_attention_workspace_size(int32_t positions, int32_t tokens) {
