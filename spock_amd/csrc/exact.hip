@@ -697,7 +697,7 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
 // state in LDS.  Each chunk's state-independent operands (kcd, q, k, local,
 // the slice of solved, eg, wlast) are staged in LDS; the next chunk's are
 // loaded into registers while the current one is computed.
-constexpr int kSlice = 16;
+constexpr int kSlice = 8;   // value columns per workgroup: 16 heads x 16 slices fill the chip
 constexpr int kScanThreads = 512;
 constexpr int kScanLd = kD + 4;
 
@@ -724,7 +724,7 @@ __global__ __launch_bounds__(kScanThreads) void ordered_chunk_scan_kernel(OrdArg
   // prefetch registers: kcd, q, k (4 float4 each), local (2 float4), the
   // solved slice (float2), eg or wlast (one float for tid < 128)
   float4 pk[4], pq[4], pkk[4], pl[2];
-  float2 ps;
+  float ps;
   float pe = 0.0f;
   auto prefetch = [&](int ci) {
     const float* cw = chunk_ws(a, h, ci);
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(kScanThreads) void ordered_chunk_scan_kernel(OrdArg
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) pl[j] = ld4(loc + 4 * (tid + kScanThreads * j));
-    ps = *reinterpret_cast<const float2*>(cw + (tid >> 3) * kD + v0 + (tid & 7) * 2);
+    ps = cw[(tid >> 3) * kD + v0 + (tid & 7)];
     if (tid < 2 * kC) pe = cw[2 * kC * kD + kC * kC + tid];  // eg[0..63], then wlast[0..63]
   };
   const int nchunks = a.total / kC;
@@ -764,19 +764,19 @@ __global__ __launch_bounds__(kScanThreads) void ordered_chunk_scan_kernel(OrdArg
       Lc[r][c + 2] = pl[j].z;
       Lc[r][c + 3] = pl[j].w;
     }
-    *reinterpret_cast<float2*>(&Sol[tid >> 3][(tid & 7) * 2]) = ps;
+    Sol[tid >> 3][tid & 7] = ps;
     if (tid < kC)
       Eg[tid] = pe;
     else if (tid < 2 * kC)
       Wl[tid - kC] = pe;
     __syncthreads();
     if (ci + 1 < nchunks) prefetch(ci + 1);
-    // A (:215-233): thread = row r, columns 2cp, 2cp+1 of the slice
+    // A (:215-233): thread = row r, column cp of the slice
     const int r = tid >> 3, cp = tid & 7;
-    float inter[2] = {0.0f, 0.0f};
+    float inter = 0.0f;
     {
       const float egr = Eg[r];
-      float carry[2] = {0.0f, 0.0f};
+      float carry = 0.0f;
       for (int k4 = 0; k4 < kD; k4 += 4) {
         const float4 kw = ld4(&Kc[r][k4]);
         const float4 qw = ld4(&Qc[r][k4]);
@@ -784,52 +784,38 @@ __global__ __launch_bounds__(kScanThreads) void ordered_chunk_scan_kernel(OrdArg
         const float qq[4] = {qw.x, qw.y, qw.z, qw.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float2 s2 = *reinterpret_cast<const float2*>(&Ss[k4 + e][cp * 2]);
+          const float sv = Ss[k4 + e][cp];
           const float qe = qq[e] * egr;
-          carry[0] = carry[0] + kk[e] * s2.x;
-          carry[1] = carry[1] + kk[e] * s2.y;
-          inter[0] = inter[0] + qe * s2.x;
-          inter[1] = inter[1] + qe * s2.y;
+          carry = carry + kk[e] * sv;
+          inter = inter + qe * sv;
         }
       }
-      vn[r][cp * 2] = Sol[r][cp * 2] - carry[0];
-      vn[r][cp * 2 + 1] = Sol[r][cp * 2 + 1] - carry[1];
+      vn[r][cp] = Sol[r][cp] - carry;
     }
     __syncthreads();
     // B (:235-244): core[r] = inter + sum_{c <= r} local[r][c] * vnew[c]
     {
-      float s0 = inter[0], s1 = inter[1];
-      for (int c = 0; c <= r; ++c) {
-        const float l = Lc[r][c];
-        const float2 v2 = *reinterpret_cast<const float2*>(&vn[c][cp * 2]);
-        s0 = s0 + l * v2.x;
-        s1 = s1 + l * v2.y;
-      }
-      if (base + r < a.T) {
-        float* o = a.core + ((size_t)h * a.core_head_stride + base + r) * kD + v0 + cp * 2;
-        o[0] = s0;
-        o[1] = s1;
-      }
+      float s0 = inter;
+      for (int c = 0; c <= r; ++c) s0 = s0 + Lc[r][c] * vn[c][cp];
+      if (base + r < a.T) a.core[((size_t)h * a.core_head_stride + base + r) * kD + v0 + cp] = s0;
     }
-    // C (:246-268): thread = state row kd, columns 4cq..4cq+3 of the slice
+    // C (:246-268): thread = state row kd, columns 2cq, 2cq+1 of the slice
     {
       const int kd = tid >> 2, cq = tid & 3;
       const float eglast = Eg[kC - 1];
-      float upd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float upd[2] = {0.0f, 0.0f};
       for (int rr = 0; rr < kC; ++rr) {
         const float kw = Kk[rr][kd] * Wl[rr];
-        const float4 v4 = ld4(&vn[rr][cq * 4]);
-        upd[0] = upd[0] + kw * v4.x;
-        upd[1] = upd[1] + kw * v4.y;
-        upd[2] = upd[2] + kw * v4.z;
-        upd[3] = upd[3] + kw * v4.w;
+        const float2 v2 = *reinterpret_cast<const float2*>(&vn[rr][cq * 2]);
+        upd[0] = upd[0] + kw * v2.x;
+        upd[1] = upd[1] + kw * v2.y;
       }
       // Ss row kd was read by phase A (before the barrier above) and is
       // written here by this thread alone
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float ws = Ss[kd][cq * 4 + j] * eglast;
-        Ss[kd][cq * 4 + j] = ws + upd[j];
+      for (int j = 0; j < 2; ++j) {
+        const float ws = Ss[kd][cq * 2 + j] * eglast;
+        Ss[kd][cq * 2 + j] = ws + upd[j];
       }
     }
   }
