@@ -221,6 +221,84 @@ __global__ __launch_bounds__(256) void matvec_rows_mfma_kernel(RowsArgs a, int n
     }
 }
 
+// Few output tiles (small projections, short prompts): the same leaves,
+// order and tree as matvec_rows_mfma_kernel for one 16 x 16 tile, its 16
+// leaves split over the workgroup's 4 waves.  Wave g takes visits v = 4g ..
+// 4g+3, a whole subtree of the binary-counter merge, and merges them exactly
+// as the one-wave kernel would; the four subtree sums are then combined as
+// the counter's last two levels do, (g0 + g1) + (g2 + g3).  A quarter of the
+// sequential chunk loads per wave.
+template <int S>
+__global__ __launch_bounds__(256) void matvec_rows_split_kernel(RowsArgs a, int n_tt) {
+  __shared__ float part[4][4][64];  // [wave][k][lane]
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int tile = blockIdx.x;
+  const int r0 = (tile / n_tt) * 16, t0 = (tile % n_tt) * 16;
+  const int blk = lane >> 4, li = lane & 15;
+  constexpr int C = S / 8;  // 16-byte chunks per span
+  const uint16_t* wrow = a.W + (size_t)min(r0 + li, a.out_dim - 1) * a.in_dim;
+  const uint16_t* xrow = a.X + (size_t)min(t0 + li, a.rows - 1) * a.ldx;
+  auto span_of = [&](int v) { return (int)(__builtin_bitreverse32((uint32_t)v) >> 28) + 16 * blk; };
+  uint4 nw, nx;
+  auto issue = [&](int v, int c) {
+    const int off = span_of(v) * S + 8 * c;
+    nw = *reinterpret_cast<const uint4*>(wrow + off);
+    nx = *reinterpret_cast<const uint4*>(xrow + off);
+  };
+  float stack[2][4];
+  float cur[4];
+  issue(4 * g, 0);
+#pragma unroll 1
+  for (int m = 0; m < 4; ++m) {
+    const int v = 4 * g + m;
+    v16f acc = v16f{};
+    for (int c = 0; c < C; ++c) {
+      float wf[8], xf[8];
+      unpack8h(nw, wf);
+      unpack8h(nx, xf);
+      if (c + 1 < C)
+        issue(v, c + 1);
+      else if (m + 1 < 4)
+        issue(v + 1, 0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x1f32(wf[e], xf[e], acc, 0, 0, 0);
+    }
+    // (P_l + P_{l+32}) + (P_{l+16} + P_{l+48})
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cur[k] = (acc[k] + acc[8 + k]) + (acc[4 + k] + acc[12 + k]);
+    // binary-counter merge inside the subtree (levels 0 and 1; m = v mod 4)
+    bool carry = true;
+#pragma unroll
+    for (int lev = 0; lev < 2; ++lev) {
+      if (carry) {
+        if ((m >> lev) & 1) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) cur[q] = stack[lev][q] + cur[q];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) stack[lev][q] = cur[q];
+          carry = false;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) part[g][k][lane] = cur[k];
+  __syncthreads();
+  if (g != 0) return;
+  const int t = t0 + li;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float s = (part[0][k][lane] + part[1][k][lane]) + (part[2][k][lane] + part[3][k][lane]);
+    const int r = r0 + 4 * blk + k;
+    if (r < a.out_dim && t < a.rows) {
+      uint16_t o = spk::f2h(s);
+      if (a.R) o = spk::f2h(spk::h2f(a.R[(long long)t * a.ldy + r]) + spk::h2f(o));
+      a.Y[(long long)t * a.ldy + r] = o;
+    }
+  }
+}
+
 // in_dim 2048 / 3584 (S = 32 / 56): the same leaves, order and tree as
 // matvec_rows_mfma_kernel, with each leaf's operands staged through LDS by
 // coalesced loads (a span is 64 / 112 contiguous bytes; the lanes of a load
@@ -855,6 +933,17 @@ extern "C" int spk_matvec_f16_rows(const uint16_t* W, const uint16_t* X, int64_t
     return spk::check_launch("spk_matvec_f16_rows");
   }
   if ((S == 16 || S == 32 || S == 56) && vec_ok) {
+    const int nt16 = (rows + 15) / 16;
+    const long long tiles16 = (long long)((out_dim + 15) / 16) * nt16;
+    if (tiles16 < 512) {  // one wave per tile would leave most of the chip idle
+      if (S == 16)
+        hipLaunchKernelGGL((matvec_rows_split_kernel<16>), dim3(tiles16), dim3(256), 0, s, a, nt16);
+      else if (S == 32)
+        hipLaunchKernelGGL((matvec_rows_split_kernel<32>), dim3(tiles16), dim3(256), 0, s, a, nt16);
+      else
+        hipLaunchKernelGGL((matvec_rows_split_kernel<56>), dim3(tiles16), dim3(256), 0, s, a, nt16);
+      return spk::check_launch("spk_matvec_f16_rows");
+    }
     // 2 x 2 tiles per wave unless that leaves SIMDs idle (1024 on the chip);
     // then 1 x 2, then 1 x 1 (two waves per SIMD hide more operand latency)
     const int n_rt32 = (out_dim + 31) / 32, n_rt16 = (out_dim + 15) / 16;
