@@ -61,13 +61,15 @@ def _gemv(inp, outs):
     _lib.check(_lib.lib().spk_gemv_fused(C.byref(inp), arr, len(outs), _stream()), "spk_gemv_fused")
 
 
-def test_gemv_rmsnorm_with_embedding_row(dev):
+# up to 4 outputs run in one launch; 5..8 are split over two launches (the
+# first alone writes h_out)
+@pytest.mark.parametrize("shapes", [[6144, 2048, 16, 16], [16, 512, 1024, 20, 2048, 48]])
+def test_gemv_rmsnorm_with_embedding_row(dev, shapes):
     from spock_amd import _lib
-    print("[gemv rmsnorm+token]", flush=True)
+    print(f"[gemv rmsnorm+token {shapes}]", flush=True)
     V = 512
     E = _rand16(1, V * 1024, 0.02).reshape(V, 1024)
     w = _rand16(2, 1024, 0.02)
-    shapes = [6144, 2048, 16, 16]
     Ws = [_rand16(10 + i, n * 1024, 0.02).reshape(n, 1024) for i, n in enumerate(shapes)]
     tok = 317
     dE, dw = _h(E, dev), _h(w, dev)
