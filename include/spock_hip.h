@@ -169,7 +169,7 @@ int spk_deltanet_recurrent(const SpkDecodeArgs* args, spk_stream_t stream);
 int spk_matvec_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, int32_t out_dim,
                    int32_t in_dim, spk_stream_t stream);
 
-/* Several independent GEMVs in one launch (the decode projections). */
+/* Several independent GEMVs, up to 4 per launch (the decode projections). */
 typedef struct SpkMatvecDesc {
   const uint16_t* W;
   const uint16_t* x;
@@ -237,7 +237,7 @@ typedef struct SpkGemvOutput {
   const uint16_t* W_up;      /* nullable, [out_dim][in_dim] */
 } SpkGemvOutput;
 
-/* Up to 8 projections of one input in one launch.  Replaces the
+/* Up to 8 projections of one input (one launch per 4 outputs).  Replaces the
  * rms_norm + matvec (+ residual_add / silu_gate) dispatch runs of
  * vk_session.cpp:2606-2870 and :3276-3360. */
 int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count,
