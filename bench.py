@@ -552,7 +552,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
-              "(the DeltaNet hot path shards by sequence/head with no exchange; see DESIGN.md). "
+              "(the DeltaNet hot path would shard by sequence/head with no exchange). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
