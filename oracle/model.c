@@ -323,13 +323,10 @@ static void dn_mixer(const OrcModel* m, OrcModelState* st, const OrcLayer* ly, c
           k[((size_t)h * T + t) * 128 + d] = H2F(row[2048 + h * 128 + d]);
           v[((size_t)h * T + t) * 128 + d] = H2F(row[4096 + h * 128 + d]);
         }
-        /* deltanet_recurrent_gbeta_norm_gate.comp:102-116 */
-        const float av = H2F(A[(size_t)t * 16 + h]), bv = H2F(B[(size_t)t * 16 + h]);
-        const float a_log = st->a_log_bias[((size_t)ly->sub_idx * 16 + h) * 2];
-        const float dt_bias = st->a_log_bias[((size_t)ly->sub_idx * 16 + h) * 2 + 1];
-        const float sp = orc_logf(1.0f + orc_expf(av + dt_bias));
-        g[(size_t)h * T + t] = -orc_expf(a_log) * sp;
-        beta[(size_t)h * T + t] = 1.0f / (1.0f + orc_expf(-bv));
+        orc_gbeta(H2F(A[(size_t)t * 16 + h]), H2F(B[(size_t)t * 16 + h]),
+                  st->a_log_bias[((size_t)ly->sub_idx * 16 + h) * 2],
+                  st->a_log_bias[((size_t)ly->sub_idx * 16 + h) * 2 + 1],
+                  &g[(size_t)h * T + t], &beta[(size_t)h * T + t]);
       }
     }
     if (!g_chunk_f64) {
@@ -364,18 +361,9 @@ static void dn_mixer(const OrcModel* m, OrcModelState* st, const OrcLayer* ly, c
     uint16_t* Gt = (uint16_t*)malloc(2 * (size_t)T * 2048);
 #pragma omp parallel for schedule(static)
     for (int32_t t = 0; t < T; ++t)
-      for (int32_t h = 0; h < ORC_DN_HEADS; ++h) {
-        const float* o = core + ((size_t)h * T + t) * 128;
-        float s[128];
-        for (size_t l = 0; l < 128; ++l) s[l] = o[l] * o[l];
-        const float r = orc_rsqrtf(tree_pow2(s, 128) / 128.0f + eps);
-        for (size_t l = 0; l < 128; ++l) {
-          const float normed = o[l] * r;
-          const float zz = H2F(Z[(size_t)t * 2048 + h * 128 + l]);
-          const float weighted = H2F(F2H(ly->dn_norm[l] * normed));
-          Gt[(size_t)t * 2048 + h * 128 + l] = F2H(weighted * silu_f(zz));
-        }
-      }
+      for (int32_t h = 0; h < ORC_DN_HEADS; ++h)
+        orc_norm_gate_row(core + ((size_t)h * T + t) * 128, Z + (size_t)t * 2048 + h * 128,
+                          ly->dn_norm, eps, Gt + (size_t)t * 2048 + h * 128);
     matmul_impl(ly->dn_out, Gt, MIX, ORC_HIDDEN, 2048, T, f64);
     free(q); free(k); free(v); free(g); free(beta); free(core); free(init); free(Gt);
   }

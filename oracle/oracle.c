@@ -538,18 +538,52 @@ static void recur_head(float* S, const float* qf, const float* kf, const float* 
   for (size_t j = 0; j < 128; ++j) o[j] = col_dot128(S, j, qf);
 }
 
+/* g and beta of one head (deltanet_recurrent_gbeta_norm_gate.comp:102-116):
+ * g = -exp(A_log) * log(1 + exp(a + dt_bias)) (softplus with no overflow
+ * threshold), beta = 1 / (1 + exp(-b)). */
+void orc_gbeta(float a, float b, float a_log, float dt_bias, float* g, float* beta) {
+  const float sp = orc_logf(1.0f + orc_expf(a + dt_bias));
+  *g = -orc_expf(a_log) * sp;
+  *beta = 1.0f / (1.0f + orc_expf(-b));
+}
+
+/* Gated RMSNorm of one 128-wide head row o (fp32):
+ * r = 1/sqrt(tree128(o^2)/128 + eps), out = fp16(fp16(w * (o*r)) * silu(z))
+ * (deltanet_recurrent_gbeta_norm_gate.comp:182-224, deltanet_norm_gate.comp:80-105). */
+void orc_norm_gate_row(const float* o, const uint16_t* z, const float* nw, float eps,
+                       uint16_t* out) {
+  float s[128];
+  for (size_t l = 0; l < 128; ++l) s[l] = o[l] * o[l];
+  const float r = orc_rsqrtf(tree128(s) / 128.0f + eps);
+  for (size_t l = 0; l < 128; ++l) {
+    const float normed = o[l] * r;
+    const float weighted = orc_h2f(orc_f2h_rne(nw[l] * normed));
+    out[l] = orc_f2h_rne(weighted * silu_f(orc_h2f(z[l])));
+  }
+}
+
+/* deltanet_norm_gate.comp:80-105, the unfused norm-gate over fp16 input rows
+ * (dispatch vk_session.cpp:1743-1756, :3245-3257): io [nh][128] in place.
+ * The shader's 256-lane tree adds 128 zero partials at its first level
+ * (exact), so the sum is tree128 of the squares. */
+void orc_norm_gate_f16(size_t nh, float eps, uint16_t* io, const uint16_t* z,
+                       const float* nw) {
+  float o[128];
+  for (size_t h = 0; h < nh; ++h) {
+    for (size_t l = 0; l < 128; ++l) o[l] = orc_h2f(io[h * 128 + l]);
+    orc_norm_gate_row(o, z + h * 128, nw, eps, io + h * 128);
+  }
+}
+
 void orc_recurrent_gbeta_norm_gate(size_t nh, size_t layer, float q_scale, float eps,
                                    const uint16_t* a, const uint16_t* b,
                                    const float* alb, uint16_t* qkv, float* state,
                                    const uint16_t* z, const float* nw) {
-  float qf[128], kf[128], vf[128], o[128], s[128];
+  float qf[128], kf[128], vf[128], o[128];
   for (size_t h = 0; h < nh; ++h) {
-    /* :212-227 */
-    const float av = orc_h2f(a[h]), bv = orc_h2f(b[h]);
-    const float a_log = alb[(layer * nh + h) * 2], dt_bias = alb[(layer * nh + h) * 2 + 1];
-    const float sp = orc_logf(1.0f + orc_expf(av + dt_bias));
-    const float g = -orc_expf(a_log) * sp;
-    const float beta = 1.0f / (1.0f + orc_expf(-bv));
+    float g, beta;
+    orc_gbeta(orc_h2f(a[h]), orc_h2f(b[h]), alb[(layer * nh + h) * 2],
+              alb[(layer * nh + h) * 2 + 1], &g, &beta);
     /* :233-241 */
     for (size_t l = 0; l < 128; ++l) {
       qf[l] = orc_h2f(qkv[h * 128 + l]) * q_scale;
@@ -557,16 +591,7 @@ void orc_recurrent_gbeta_norm_gate(size_t nh, size_t layer, float q_scale, float
       vf[l] = orc_h2f(qkv[2 * nh * 128 + h * 128 + l]);
     }
     recur_head(state + h * 128 * 128, qf, kf, vf, g, beta, o);
-    /* :293-323 RMS over the 128 outputs */
-    for (size_t l = 0; l < 128; ++l) s[l] = o[l] * o[l];
-    const float r = orc_rsqrtf(tree128(s) / 128.0f + eps);
-    /* :325-335 */
-    for (size_t l = 0; l < 128; ++l) {
-      const float normed = o[l] * r;
-      const float zz = orc_h2f(z[h * 128 + l]);
-      const float weighted = orc_h2f(orc_f2h_rne(nw[l] * normed));
-      qkv[2 * nh * 128 + h * 128 + l] = orc_f2h_rne(weighted * silu_f(zz));
-    }
+    orc_norm_gate_row(o, z + h * 128, nw, eps, qkv + 2 * nh * 128 + h * 128);
   }
 }
 

@@ -117,6 +117,20 @@ void orc_recurrent_gbeta_norm_gate(size_t num_heads, size_t layer_idx,
                                    uint16_t* qkv, float* state,
                                    const uint16_t* z, const float* norm_w);
 
+/* g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) for one head
+ * (deltanet_recurrent_gbeta_norm_gate.comp:102-116). */
+void orc_gbeta(float a, float b, float a_log, float dt_bias, float* g, float* beta);
+
+/* Gated RMSNorm of one fp32 head row of 128 (the fused shader's :182-224):
+ * out = fp16(fp16(w * o * r) * silu(z)), r = 1/sqrt(tree128(o^2)/128 + eps). */
+void orc_norm_gate_row(const float* o, const uint16_t* z, const float* norm_w,
+                       float eps, uint16_t* out);
+
+/* deltanet_norm_gate.comp:80-105 (unfused, fp16 input): io [nh][128] fp16 in
+ * place, z [nh][128] fp16, norm_w [128] fp32. */
+void orc_norm_gate_f16(size_t num_heads, float eps, uint16_t* io, const uint16_t* z,
+                       const float* norm_w);
+
 /* deltanet_recurrent.comp (unfused): g/beta read from the state tail
  * state[nh*128*128 + h] / state[nh*128*128 + nh + h]; output fp16 into V. */
 void orc_recurrent(size_t num_heads, float q_scale, uint16_t* qkv, float* state);

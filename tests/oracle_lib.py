@@ -53,6 +53,12 @@ def _load_oracle():
     lib.orc_conv_l2_qk.argtypes = [_sz] * 4 + [_p] * 3
     lib.orc_recurrent_gbeta_norm_gate.restype = None
     lib.orc_recurrent_gbeta_norm_gate.argtypes = [_sz, _sz, _c.c_float, _c.c_float] + [_p] * 8
+    lib.orc_gbeta.restype = None
+    lib.orc_gbeta.argtypes = [_c.c_float] * 4 + [_p, _p]
+    lib.orc_norm_gate_row.restype = None
+    lib.orc_norm_gate_row.argtypes = [_p, _p, _p, _c.c_float, _p]
+    lib.orc_norm_gate_f16.restype = None
+    lib.orc_norm_gate_f16.argtypes = [_sz, _c.c_float, _p, _p, _p]
     lib.orc_recurrent.restype = None
     lib.orc_recurrent.argtypes = [_sz, _c.c_float, _p, _p]
     lib.orc_decode_step.restype = None
@@ -207,6 +213,42 @@ def decode_step(inp: dict, layer_idx=0, q_scale=None, eps=1e-6):
                           _ptr(_f32(inp["a_log_bias"])), _ptr(st), st[0].size,
                           _ptr(_u16(inp["z"])), inp["z"].shape[1], _ptr(_f32(inp["norm_w"])))
     return qkv, cs, st
+
+
+def conv_l2_qk(qkv, conv_state, conv_w, nh=16):
+    """One deltanet_conv_l2_qk step on copies; returns (qkv, conv_state)."""
+    qkv = _u16(qkv).copy()
+    cs = _u16(conv_state).copy()
+    lib().orc_conv_l2_qk(qkv.size, 4, nh * 128, nh, _ptr(qkv), _ptr(cs), _ptr(_u16(conv_w)))
+    return qkv, cs
+
+
+def gbeta(a, b, a_log, dt_bias):
+    """(g, beta) per element of equally shaped fp32 arrays (orc_gbeta)."""
+    a, b, a_log, dt_bias = (np.broadcast_to(_f32(x), np.broadcast(a, b, a_log, dt_bias).shape).ravel()
+                            for x in (a, b, a_log, dt_bias))
+    g = np.empty(a.size, np.float32)
+    beta = np.empty(a.size, np.float32)
+    gp, bp = _c.c_float(), _c.c_float()
+    f = lib().orc_gbeta
+    for i in range(a.size):
+        f(float(a[i]), float(b[i]), float(a_log[i]), float(dt_bias[i]), _c.byref(gp), _c.byref(bp))
+        g[i], beta[i] = gp.value, bp.value
+    return g, beta
+
+
+def norm_gate_f16(core, z, norm_w, eps=1e-6):
+    """deltanet_norm_gate.comp over fp16 rows core [nh][128] (orc_norm_gate_f16)."""
+    io = _u16(core).copy()
+    lib().orc_norm_gate_f16(io.size // 128, float(eps), _ptr(io), _ptr(_u16(z)), _ptr(_f32(norm_w)))
+    return io
+
+
+def norm_gate_row(o, z, norm_w, eps=1e-6):
+    """The fused decode's gated RMSNorm of one fp32 row of 128 (orc_norm_gate_row)."""
+    out = np.empty(128, np.uint16)
+    lib().orc_norm_gate_row(_ptr(_f32(o)), _ptr(_u16(z)), _ptr(_f32(norm_w)), float(eps), _ptr(out))
+    return out
 
 
 def recurrent(qkv, state_with_tail, nh=16, q_scale=None):
