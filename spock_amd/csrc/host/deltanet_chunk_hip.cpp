@@ -80,7 +80,7 @@ DeltaNetChunkOutputs run_deltanet_chunk_rule(const DeltaNetChunkConfig& config,
   a.num_heads = static_cast<int32_t>(H);
   a.total_tokens = static_cast<int32_t>(T);
   a.key_dim = a.value_dim = static_cast<int32_t>(kDim);
-  a.chunk_size = 64;
+  a.chunk_size = 64;  // config.chunk_size only changes rounding (deltanet_chunk_hip.hpp)
   a.use_qk_l2norm = config.use_qk_l2norm ? 1 : 0;
   a.q_scale = 1.0f / std::sqrt(static_cast<float>(dk));  // deltanet_chunk.cpp:87
   a.input_dtype = SPK_F32;

@@ -8,9 +8,15 @@
 // final_state; std::runtime_error for a zero config field or a size mismatch.
 // The device kernels work on 128-wide heads and 64-token chunks: narrower
 // heads are zero-padded (zero key dims change no dot product or norm, zero
-// value dims give zero outputs, the q scale stays 1/sqrt(key_dim)), and the
-// chunk size is the kernel's blocking -- the chunk rule's result equals the
-// token recurrence for every chunk size, up to fp32 rounding.
+// value dims give zero outputs, the q scale stays 1/sqrt(key_dim)).
+//
+// chunk_size: validated (non-zero, as the reference requires) and then
+// replaced by the kernels' fixed 64-token blocking.  The chunk rule equals the
+// token recurrence for every chunk size, so this changes only fp32 rounding:
+// a call with chunk_size C returns exactly what the same call with 64 returns,
+// which is within 1e-5 of the reference rule at C (checked on the reference's
+// own unit case, C = 4).  Callers that need the reference's rounding order
+// for another C have no GPU path here.
 #pragma once
 
 #include <cstddef>

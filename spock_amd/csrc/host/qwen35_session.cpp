@@ -176,7 +176,8 @@ Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::u
   lm_ws_ = DeviceBuffer(spk_lm_head_workspace_size(static_cast<int32_t>(V)));
   tok_ = DeviceBuffer(256);
   pos_ = DeviceBuffer(256);
-  history_ = DeviceBuffer(std::size_t(kHistoryCap + 64) * 4);  // [count | pad | history]
+  history_cap_ = max_seq_;
+  history_ = DeviceBuffer(std::size_t(history_cap_ + 64) * 4);  // [count | pad | history]
   reset();
   if (verbose_)
     std::fprintf(stderr, "[spock-hip] session: %u layers (%u DeltaNet, %u attention), vocab %u, %.1f MiB weights, %.1f ms\n",
@@ -357,7 +358,7 @@ std::uint32_t Qwen35Session::prefill(const std::vector<std::uint32_t>& tokens) {
   hip_check(hipMemcpyAsync(history_.get(), &pos_count[1], 4, hipMemcpyHostToDevice, stream_), "history count");
   std::int32_t* hist = history_.get<std::int32_t>();
   spk_check(spk_record_token(tok_.get<std::int32_t>(), pos_.get<std::int32_t>(), hist, hist + 64,
-                             static_cast<int32_t>(kHistoryCap), S(stream_)),
+                             static_cast<int32_t>(history_cap_), S(stream_)),
             "record token");
   hip_check(hipEventRecord(ev.b, stream_), "hipEventRecord");
   std::int32_t first = 0;
@@ -461,7 +462,7 @@ void Qwen35Session::enqueue_decode_step() {
                                lm_ws_.bytes(), S(stream_)),
             "lm_head");
   std::int32_t* hist = history_.get<std::int32_t>();
-  spk_check(spk_record_token(tok, pos_.get<std::int32_t>(), hist, hist + 64, static_cast<int32_t>(kHistoryCap),
+  spk_check(spk_record_token(tok, pos_.get<std::int32_t>(), hist, hist + 64, static_cast<int32_t>(history_cap_),
                              S(stream_)),
             "record token");
 }
@@ -497,7 +498,7 @@ std::vector<std::uint32_t> Qwen35Session::decode_steps(std::uint32_t n) {
   if (std::size_t(pos_host_) + n > max_seq_)
     throw std::runtime_error("decode: position " + std::to_string(pos_host_ + n) + " exceeds max_seq " +
                              std::to_string(max_seq_));
-  if (std::size_t(history_len_) + n > kHistoryCap) throw std::runtime_error("decode: token history full");
+  if (std::size_t(history_len_) + n > history_cap_) throw std::runtime_error("decode: token history full");
   for (std::uint32_t i = 0; i < n; ++i) run_decode_step();
   std::vector<std::int32_t> out(n);
   hip_check(hipMemcpyAsync(out.data(), history_.get<std::int32_t>() + 64 + history_len_, n * 4, hipMemcpyDeviceToHost,
@@ -528,6 +529,7 @@ DecodeResult Qwen35Session::decode(const std::vector<std::uint32_t>& prompt_toke
     if (std::size_t(pos_host_) + n > max_seq_)
       throw std::runtime_error("decode: position " + std::to_string(pos_host_ + n) + " exceeds max_seq " +
                                std::to_string(max_seq_));
+    if (std::size_t(history_len_) + n > history_cap_) throw std::runtime_error("decode: token history full");
     for (std::uint32_t i = 0; i < n; ++i) run_decode_step();
     hip_check(hipEventRecord(ev.b, stream_), "hipEventRecord");
     std::vector<std::int32_t> out(n);

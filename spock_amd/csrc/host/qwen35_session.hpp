@@ -130,7 +130,7 @@ class Qwen35Session {
   // decode activations
   DeviceBuffer h_, hn_, qkv_, z_, a_, b_, qg_, k_, v_, attn_out_, gate_, up_, logits_;
   DeviceBuffer attn_ws_, lm_ws_, tok_, pos_, history_;
-  static constexpr std::uint32_t kHistoryCap = 8192;
+  std::uint32_t history_cap_ = 0;   // token history capacity (= max_seq_: one token per position)
   // prefill activations (capacity prefill_cap_ tokens)
   std::uint32_t prefill_cap_ = 0;
   DeviceBuffer p_tokens_, p_h_, p_xn_, p_qkv_, p_z_, p_a_, p_b_, p_qhm_, p_khm_, p_vhm_, p_g_, p_beta_, p_core_,

@@ -41,6 +41,26 @@ def _dev(t: torch.Tensor, dtype=None) -> torch.Tensor:
 # ----------------------------------------------------------------------------
 # chunk prefill
 # ----------------------------------------------------------------------------
+_CU_CHECKED: dict = {}
+
+
+def _check_cu_dev(cu_dev: torch.Tensor, cu_host: np.ndarray, dev) -> None:
+    """The kernels index sequences through the device copy and size the grid
+    from the host copy, so the two must agree.  The comparison reads the
+    device tensor back once per (buffer, version) and is cached, so repeated
+    calls with the same offsets stay asynchronous."""
+    if cu_dev.device != dev or cu_dev.dtype != torch.int32 or not cu_dev.is_contiguous():
+        raise _lib.SpockError("chunk_prefill: cu_seqlens_dev must be a contiguous int32 tensor on q's device")
+    if cu_dev.numel() != cu_host.size:
+        raise _lib.SpockError(f"chunk_prefill: cu_seqlens_dev has {cu_dev.numel()} entries, cu_seqlens {cu_host.size}")
+    key = (cu_dev.data_ptr(), cu_dev._version, cu_host.tobytes())
+    if key in _CU_CHECKED:
+        return
+    if not np.array_equal(cu_dev.cpu().numpy(), cu_host):
+        raise _lib.SpockError("chunk_prefill: cu_seqlens_dev differs from cu_seqlens")
+    if len(_CU_CHECKED) > 64:
+        _CU_CHECKED.clear()
+    _CU_CHECKED[key] = True
 def chunk_workspace_bytes(num_heads: int, total_tokens: int, num_seqs: int = 1) -> int:
     return int(lib().spk_chunk_prefill_workspace_size(num_heads, total_tokens, num_seqs, CHUNK))
 
@@ -59,9 +79,17 @@ def chunk_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     sequence; cu_seqlens_dev optionally holds the same offsets already on the
     device, int32).  Returns (core [H][N][128] f32, state [S][H][128][128] f32).
     """
+    if q.dim() != 3:
+        raise _lib.SpockError(f"chunk_prefill: q must be [H][N][128], got {tuple(q.shape)}")
     H, N, dk = q.shape
-    if dk != KEY_DIM or v.shape[-1] != VALUE_DIM:
+    if dk != KEY_DIM:
         raise _lib.SpockError("chunk_prefill: key_dim and value_dim must be 128")
+    for name, t in (("k", k), ("v", v)):
+        if tuple(t.shape) != (H, N, KEY_DIM):
+            raise _lib.SpockError(f"chunk_prefill: {name} shape {tuple(t.shape)} != q shape {(H, N, KEY_DIM)}")
+    for name, t in (("g", g), ("beta", beta)):
+        if tuple(t.shape) != (H, N):
+            raise _lib.SpockError(f"chunk_prefill: {name} shape {tuple(t.shape)} != {(H, N)}")
     dtype = q.dtype
     if dtype not in (torch.float32, torch.float16):
         raise _lib.SpockError("chunk_prefill: q/k/v must be float32 or float16")
@@ -74,14 +102,38 @@ def chunk_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         S = 1
         cu_dev = None
         cu_host = None
+        if cu_seqlens_dev is not None:
+            raise _lib.SpockError("chunk_prefill: cu_seqlens_dev given without cu_seqlens")
     else:
         cu_host = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
         S = len(cu_host) - 1
-        cu_dev = cu_seqlens_dev if cu_seqlens_dev is not None else torch.from_numpy(cu_host.copy()).to(dev)
+        if cu_seqlens_dev is not None:
+            _check_cu_dev(cu_seqlens_dev, cu_host, dev)
+            cu_dev = cu_seqlens_dev
+        else:
+            cu_dev = torch.from_numpy(cu_host.copy()).to(dev)
+    state_elems = S * H * KEY_DIM * VALUE_DIM
+    if initial_state is not None:
+        _dev(initial_state, torch.float32)
+        if initial_state.numel() != state_elems:
+            raise _lib.SpockError(f"chunk_prefill: initial_state must hold [S={S}][H={H}][128][128] "
+                                  f"= {state_elems} floats, got {initial_state.numel()}")
+    hs = core_head_stride or N
     if out_core is None:
+        if hs != N:
+            raise _lib.SpockError("chunk_prefill: core_head_stride needs an out_core buffer")
         out_core = torch.empty((H, N, VALUE_DIM), dtype=torch.float32, device=dev)
+    else:
+        _dev(out_core, torch.float32)
+        if hs < N or out_core.numel() < ((H - 1) * hs + N) * VALUE_DIM:
+            raise _lib.SpockError(f"chunk_prefill: out_core holds {out_core.numel()} floats, "
+                                  f"rows (h*{hs} + t) for H={H}, N={N} need {((H - 1) * hs + N) * VALUE_DIM}")
     if out_state is None:
         out_state = torch.empty((S, H, KEY_DIM, VALUE_DIM), dtype=torch.float32, device=dev)
+    else:
+        _dev(out_state, torch.float32)
+        if out_state.numel() < state_elems:
+            raise _lib.SpockError(f"chunk_prefill: out_state holds {out_state.numel()} floats, need {state_elems}")
     need = chunk_workspace_bytes(H, N, S)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)

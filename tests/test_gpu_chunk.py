@@ -173,3 +173,36 @@ def test_collect_and_last_to_fp16(dev, oracle):
     torch.cuda.synchronize()
     exp = oracle.chunk_last_to_fp16(src, H, 128, 100, 128)
     assert np.array_equal(out.cpu().numpy().view(np.uint16), exp)
+
+
+def test_chunk_prefill_rejects_inconsistent_arguments(dev):
+    """The Python mirror checks every operand the kernels index from N, S and
+    cu_seqlens before a launch (no kernel runs for these calls)."""
+    from spock_amd import ops
+    from spock_amd._lib import SpockError
+    H, N = 2, 100
+    f = lambda *s, dt=torch.float32: torch.zeros(*s, dtype=dt, device=dev)
+    q, k, v, g, b = f(H, N, 128), f(H, N, 128), f(H, N, 128), f(H, N), f(H, N)
+    cu = [0, 40, 100]
+    bad = [
+        dict(k=f(H, N - 1, 128)), dict(v=f(H + 1, N, 128)), dict(g=f(H, N + 1)), dict(beta=f(N)),
+        dict(initial_state=f(1, H, 128, 128), cu_seqlens=cu),
+        dict(initial_state=f(2, H, 128, 128, dt=torch.float16), cu_seqlens=cu),
+        dict(out_state=f(1, H, 128, 128), cu_seqlens=cu),
+        dict(out_core=f(H, N - 1, 128)),
+        dict(out_core=f(H, N, 128), core_head_stride=N + 5),
+        dict(cu_seqlens=cu, cu_seqlens_dev=torch.tensor(cu, dtype=torch.int64, device=dev)),
+        dict(cu_seqlens=cu, cu_seqlens_dev=torch.tensor([0, 50, 100], dtype=torch.int32, device=dev)),
+        dict(cu_seqlens=cu, cu_seqlens_dev=torch.tensor([0, 100], dtype=torch.int32, device=dev)),
+        dict(cu_seqlens_dev=torch.tensor(cu, dtype=torch.int32, device=dev)),
+    ]
+    for kw in bad:
+        args = dict(q=q, k=k, v=v, g=g, beta=b)
+        args.update(kw)
+        with pytest.raises(SpockError):
+            ops.chunk_prefill(**args)
+    torch.cuda.synchronize()
+    # the consistent call still runs
+    ops.chunk_prefill(q, k, v, g, b, cu_seqlens=cu,
+                      cu_seqlens_dev=torch.tensor(cu, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()

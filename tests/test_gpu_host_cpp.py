@@ -46,6 +46,23 @@ def test_chunk_cli_vs_oracle(dev, tmp_path, oracle, H, T, dk, dv, l2, init):
     assert max_rel(core, cc) <= 1e-5 and max_rel(state, cs) <= 1e-5
 
 
+def test_chunk_size_is_the_kernel_blocking(dev, tmp_path, oracle):
+    """run_deltanet_chunk_rule validates chunk_size and then runs the kernels'
+    64-token blocking: C = 4, 16 and 64 give the same bits, each within 1e-5
+    of the reference rule at its own C."""
+    inp = synth.chunk_inputs(2, 37, dk=128, dv=128, seed=17)
+    outs = []
+    for C in (4, 16, 64):
+        r = HC.run_chunk_cli(tmp_path, HC.chunk_fixture(**inp, chunk_size=C, l2=False))
+        assert r.returncode == 0, r.stderr
+        core, state = HC.parse_chunk_output(r.stdout, 2, 37, 128, 128)
+        cc, cs = oracle.chunk_rule(**inp, chunk=C, l2=False)
+        assert max_rel(core, cc) <= 1e-5 and max_rel(state, cs) <= 1e-5
+        outs.append((core, state))
+    for core, state in outs[1:]:
+        assert np.array_equal(core, outs[0][0]) and np.array_equal(state, outs[0][1])
+
+
 def _session_inputs(L, T, D, V, hidden, seed):
     CD, NH = 6144, 16
     pre_qkv = np.empty((L, T, CD), dtype=np.uint16)

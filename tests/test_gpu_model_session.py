@@ -114,3 +114,19 @@ def test_generate_api_and_errors(dev, small_artifact):
             s.generate(_prompt(60), 10)
         with pytest.raises(model.ModelError, match="vocab"):
             s.prefill([VOCAB + 1])
+
+
+def test_long_generation_past_8192_tokens(dev, small_artifact):
+    """The token history holds one entry per position (capacity max_seq), so
+    a session with max_seq > 8192 generates more than 8192 tokens; asking for
+    more than max_seq allows is a clean error, not an out-of-range copy."""
+    from spock_amd import model
+    print("[session 8300-token generation, max_seq 9000]", flush=True)
+    with model.Session(small_artifact, max_seq=9000) as s:
+        short = s.generate(_prompt(8), 24)
+        r = s.generate(_prompt(8), 8300)
+        assert len(r.tokens) == 8300 and r.decode_steps == 8299
+        assert r.tokens[:24].tolist() == short.tokens.tolist()
+        assert all(0 <= t < VOCAB for t in r.tokens)
+        with pytest.raises(model.ModelError, match="max_seq"):
+            s.generate(_prompt(8), 8994)

@@ -24,6 +24,10 @@ def _built():
 def test_chunk_cli_usage():
     r = subprocess.run([str(H.CHUNK_CLI)], capture_output=True, text=True)
     assert r.returncode == 2 and "--input is required" in r.stderr
+    r = subprocess.run([str(H.CHUNK_CLI), "--input"], capture_output=True, text=True)
+    assert r.returncode == 2 and "--input needs a FILE" in r.stderr
+    r = subprocess.run([str(H.CHUNK_CLI), "--bogus"], capture_output=True, text=True)
+    assert r.returncode == 2 and "unknown argument" in r.stderr
     r = subprocess.run([str(H.CHUNK_CLI), "--help"], capture_output=True, text=True)
     assert r.returncode == 0 and r.stdout.startswith("usage: spock-deltanet-chunk")
 
@@ -60,22 +64,29 @@ def test_chunk_zero_config_field(tmp_path, field):
 def test_chunk_json_errors(tmp_path):
     r = H.run_chunk_cli(tmp_path, '{"num_heads": 2, ')
     assert r.returncode == 1 and "JSON parse error" in r.stderr
+    r = H.run_chunk_cli(tmp_path, "[1, 2]")
+    assert r.returncode == 1 and "top-level JSON value is not an object" in r.stderr
+    cases = [
+        ("use_qk_l2norm", 1, 'field "use_qk_l2norm": expected true or false'),
+        ("beta", None, 'field "beta": required array of numbers is missing'),
+        ("query", {"a": 1}, 'field "query": expected an array of numbers'),
+        ("num_heads", None, 'field "num_heads": required integer is missing'),
+        ("key_dim", 2.5, 'field "key_dim": expected a non-negative integer'),
+        ("value_dim", -1, 'field "value_dim": expected a non-negative integer'),
+        ("chunk_size", "64", 'field "chunk_size": expected an integer'),
+    ]
+    for field, value, msg in cases:
+        fx = _small()
+        if value is None:
+            del fx[field]
+        else:
+            fx[field] = value
+        r = H.run_chunk_cli(tmp_path, fx)
+        assert r.returncode == 1 and msg in r.stderr, (field, r.stderr)
     fx = _small()
-    fx["use_qk_l2norm"] = 1
+    fx["g"][3] = "x"
     r = H.run_chunk_cli(tmp_path, fx)
-    assert r.returncode == 1 and "use_qk_l2norm must be a boolean" in r.stderr
-    fx = _small()
-    del fx["beta"]
-    r = H.run_chunk_cli(tmp_path, fx)
-    assert r.returncode == 1 and "missing array field: beta" in r.stderr
-    fx = _small()
-    fx["g"][0] = "x"
-    r = H.run_chunk_cli(tmp_path, fx)
-    assert r.returncode == 1 and "non-numeric value in field: g" in r.stderr
-    fx = _small()
-    del fx["num_heads"]
-    r = H.run_chunk_cli(tmp_path, fx)
-    assert r.returncode == 1 and "missing integer field: num_heads" in r.stderr
+    assert r.returncode == 1 and 'field "g": element 3 is not a number' in r.stderr
 
 
 def test_chunk_head_width_limit(tmp_path):
