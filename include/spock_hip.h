@@ -193,6 +193,19 @@ int spk_lm_head_argmax(const uint16_t* W, const uint16_t* x, int32_t vocab, int3
                        uint16_t* logits, uint32_t* out_index, void* workspace,
                        size_t workspace_bytes, spk_stream_t stream);
 
+/* spk_lm_head_argmax without a workspace argument.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * per-workgroup partial keys live in a static device array of
+ * SPK_LM_HEAD_NOALLOC_MAX_VOCAB / 32 keys (64 KiB), one copy per device held
+ * until the process ends; the call allocates nothing.  vocab above
+ * SPK_LM_HEAD_NOALLOC_MAX_VOCAB is rejected with SPK_ERR_SHAPE.  Calls that
+ * overlap on one device (concurrent streams or threads) race on that array:
+ * serialise them. */
+#define SPK_LM_HEAD_NOALLOC_MAX_VOCAB 262144
+int spk_lm_head_argmax_noalloc(const uint16_t* W, const uint16_t* x, int32_t vocab, int32_t hidden,
+                               uint16_t* logits, uint32_t* out_index, spk_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Qwen3.5 text model: the rest of the per-token decode loop and the prefill
  * element-wise operations (DecodeSession::decode, vk_session.cpp:2560-3400).

@@ -33,6 +33,7 @@ SIGNATURES = {
     "spk_argmax_f16": (C.c_int, [_p, _i32, _p, _p]),
     "spk_lm_head_workspace_size": (_sz, [_i32]),
     "spk_lm_head_argmax": (C.c_int, [_p, _p, _i32, _i32, _p, _p, _p, _sz, _p]),
+    "spk_lm_head_argmax_noalloc": (C.c_int, [_p, _p, _i32, _i32, _p, _p, _p]),
     "spk_selftest_numerics": (C.c_int, [_p, _i32, _p, _p]),
     "spk_selftest_mfma_peak": (C.c_int, [_i32, _i32, _p, _p]),
     "spk_selftest_stream_read": (C.c_int, [_p, _sz, _i32, _i32, _p, _p]),

@@ -20,6 +20,8 @@
 
 #include <float.h>
 
+#include <mutex>
+
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -432,22 +434,15 @@ extern "C" size_t spk_lm_head_workspace_size(int32_t vocab) {
   return ((blocks * sizeof(unsigned long long) + 255) / 256) * 256;
 }
 
-extern "C" int spk_lm_head_argmax(const uint16_t* W, const uint16_t* x, int32_t vocab,
-                                  int32_t hidden, uint16_t* logits, uint32_t* out_index,
-                                  void* workspace, size_t workspace_bytes, spk_stream_t stream) {
-  if (!W || !x || !out_index || !workspace) return spk::fail(SPK_ERR_NULL, "spk_lm_head_argmax: NULL pointer");
-  if (vocab <= 0 || hidden <= 0 || hidden % 512 != 0 || hidden > 8 * 512)
-    return spk::fail(SPK_ERR_SHAPE, "spk_lm_head_argmax: vocab %d hidden %d (hidden must be a multiple of 512, <= 4096)",
-                     vocab, hidden);
-  if (!spk::aligned(W, 16) || !spk::aligned(x, 16) || !spk::aligned(workspace, 8))
-    return spk::fail(SPK_ERR_ALIGN, "spk_lm_head_argmax: W/x must be 16-byte aligned");
-  if (workspace_bytes < spk_lm_head_workspace_size(vocab))
-    return spk::fail(SPK_ERR_ARG, "spk_lm_head_argmax: workspace %zu < %zu bytes", workspace_bytes,
-                     spk_lm_head_workspace_size(vocab));
-  hipStream_t s = spk::to_hip(stream);
+namespace {
+
+// Validation and the two launches shared by spk_lm_head_argmax and
+// spk_lm_head_argmax_noalloc; `partial` holds one 64-bit key per workgroup.
+int lm_head_argmax_launch(const char* name, const uint16_t* W, const uint16_t* x, int32_t vocab,
+                          int32_t hidden, uint16_t* logits, uint32_t* out_index,
+                          unsigned long long* partial, hipStream_t s) {
   const uint32_t E = (uint32_t)((vocab + 255) / 256);
   const int blocks = (vocab + 4 * kLmRows - 1) / (4 * kLmRows);
-  auto* partial = static_cast<unsigned long long*>(workspace);
 #define SPK_LM_CASE(n8)                                                                        \
   case n8:                                                                                     \
     hipLaunchKernelGGL((lm_head_kernel<n8, kLmRows>), dim3(blocks), dim3(256), 0, s, W, x,     \
@@ -463,11 +458,89 @@ extern "C" int spk_lm_head_argmax(const uint16_t* W, const uint16_t* x, int32_t 
     SPK_LM_CASE(7)
     SPK_LM_CASE(8)
     default:
-      return spk::fail(SPK_ERR_SHAPE, "spk_lm_head_argmax: hidden %d", hidden);
+      return spk::fail(SPK_ERR_SHAPE, "%s: hidden %d", name, hidden);
   }
 #undef SPK_LM_CASE
-  int rc = spk::check_launch("spk_lm_head_argmax (stream)");
+  int rc = spk::check_launch(name);
   if (rc) return rc;
   hipLaunchKernelGGL(argmax_partials_kernel, dim3(1), dim3(1024), 0, s, partial, blocks, E, out_index);
-  return spk::check_launch("spk_lm_head_argmax (reduce)");
+  return spk::check_launch(name);
+}
+
+int lm_head_check_args(const char* name, const uint16_t* W, const uint16_t* x, int32_t vocab,
+                       int32_t hidden, const uint32_t* out_index) {
+  if (!W || !x || !out_index) return spk::fail(SPK_ERR_NULL, "%s: NULL pointer", name);
+  if (vocab <= 0 || hidden <= 0 || hidden % 512 != 0 || hidden > 8 * 512)
+    return spk::fail(SPK_ERR_SHAPE, "%s: vocab %d hidden %d (hidden must be a multiple of 512, <= 4096)",
+                     name, vocab, hidden);
+  if (!spk::aligned(W, 16) || !spk::aligned(x, 16))
+    return spk::fail(SPK_ERR_ALIGN, "%s: W/x must be 16-byte aligned", name);
+  return SPK_OK;
+}
+
+}  // namespace
+
+extern "C" int spk_lm_head_argmax(const uint16_t* W, const uint16_t* x, int32_t vocab,
+                                  int32_t hidden, uint16_t* logits, uint32_t* out_index,
+                                  void* workspace, size_t workspace_bytes, spk_stream_t stream) {
+  const char* name = "spk_lm_head_argmax";
+  if (int rc = lm_head_check_args(name, W, x, vocab, hidden, out_index)) return rc;
+  if (!workspace) return spk::fail(SPK_ERR_NULL, "%s: workspace is NULL", name);
+  if (!spk::aligned(workspace, 8)) return spk::fail(SPK_ERR_ALIGN, "%s: workspace must be 8-byte aligned", name);
+  if (workspace_bytes < spk_lm_head_workspace_size(vocab))
+    return spk::fail(SPK_ERR_ARG, "%s: workspace %zu < %zu bytes", name, workspace_bytes,
+                     spk_lm_head_workspace_size(vocab));
+  return lm_head_argmax_launch(name, W, x, vocab, hidden, logits, out_index,
+                               static_cast<unsigned long long*>(workspace), spk::to_hip(stream));
+}
+
+// ---------------------------------------------------------------------------
+// spk_lm_head_argmax_noalloc: the same two kernels with their partial keys in
+// a file-scope device array instead of a caller workspace, for callers that
+// cannot allocate.  Every device holds its own copy of `scratch` for the life
+// of the process; its address on the current device is looked up once
+// (hipGetSymbolAddress) and kept per device.  Each call overwrites the keys
+// it uses before reading them, so nothing has to start at zero; two calls
+// that overlap on one device race on the array.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kNoAllocBlocks = (SPK_LM_HEAD_NOALLOC_MAX_VOCAB + 4 * kLmRows - 1) / (4 * kLmRows);
+}  // namespace
+
+static __device__ __align__(256) unsigned long long scratch[kNoAllocBlocks];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned long long* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(const char* name, unsigned long long** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return spk::fail(SPK_ERR_HIP, "%s: hipGetDevice: %s", name, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return spk::fail(SPK_ERR_ARG, "%s: device %d out of range", name, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return spk::fail(SPK_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", name, hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<unsigned long long*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return SPK_OK;
+}
+}  // namespace
+
+extern "C" int spk_lm_head_argmax_noalloc(const uint16_t* W, const uint16_t* x, int32_t vocab,
+                                          int32_t hidden, uint16_t* logits, uint32_t* out_index,
+                                          spk_stream_t stream) {
+  const char* name = "spk_lm_head_argmax_noalloc";
+  if (int rc = lm_head_check_args(name, W, x, vocab, hidden, out_index)) return rc;
+  if (vocab > SPK_LM_HEAD_NOALLOC_MAX_VOCAB)
+    return spk::fail(SPK_ERR_SHAPE, "%s: vocab %d exceeds the static scratch limit of %d rows", name, vocab,
+                     SPK_LM_HEAD_NOALLOC_MAX_VOCAB);
+  unsigned long long* partial = nullptr;
+  if (int rc = scratch_on_current_device(name, &partial)) return rc;
+  return lm_head_argmax_launch(name, W, x, vocab, hidden, logits, out_index, partial, spk::to_hip(stream));
 }
