@@ -312,8 +312,21 @@ def bench_lm_head(steps, warmup):
     avg = ms / 1e3
     nbytes = VOCAB * HIDDEN * 2
     gbs = nbytes / avg / 1e9
-    return {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    res = {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": 2}
+    # the one-launch form: device-atomic argmax key (+ the one-thread take)
+    key = torch.zeros(64, dtype=torch.int64, device=dev)  # SPK_ARGMAX_KEY_WORDS
+
+    def fn_key(i):
+        lib.spk_lm_head_argmax_key(Ws[i].data_ptr(), x.data_ptr(), None, VOCAB, HIDDEN, None, key.data_ptr(),
+                                   _stream())
+        lib.spk_argmax_key_take(key.data_ptr(), VOCAB, out.data_ptr(), None, None, None, 0, _stream())
+    ms = timed_graph(fn_key, steps, warmup, rotate=2)
+    avg = ms / 1e3
+    gbs = nbytes / avg / 1e9
+    res["atomic_key"] = {"launch_us": round(avg * 1e6, 2), "achieved_gbs": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": "1 + take"}
+    return res
 
 
 MODEL_SEED, MODEL_PROMPT, MODEL_NEW = 2026, 512, 128

@@ -281,6 +281,15 @@ size_t spk_attention_workspace_size(int32_t positions, int32_t tokens);
 /* One token at position *pos_dev (< max_seq; read on the device, so the call
  * can be recorded once and replayed); workspace for (max_seq, 1). */
 int spk_attention_decode(const SpkAttnArgs* args, spk_stream_t stream);
+/* spk_attention_decode followed by the o_proj projection (+ residual) with
+ * the second stage -- blocks combined in order, normalised, sigmoid-gated --
+ * computed inside the projection's prologue: attention_decode.comp,
+ * sigmoid_gate.comp, the o_proj matvec and residual_add.comp
+ * (vk_session.cpp:2676-2830) in two launches instead of three.  o_proj: W
+ * [out_dim][2048], y, residual as in spk_gemv_fused (W_up must be NULL);
+ * args->out is not written.  Same bits as spk_attention_decode then
+ * spk_gemv_fused (PLAIN input over args->out). */
+int spk_attention_decode_oproj(const SpkAttnArgs* args, const SpkGemvOutput* o_proj, spk_stream_t stream);
 /* `tokens` consecutive tokens at positions pos0.. (rows of qg/k/v/out are
  * per token); workspace for (pos0 + tokens, tokens). */
 int spk_attention_prefill(const SpkAttnArgs* args, int32_t pos0, int32_t tokens,
@@ -300,6 +309,24 @@ int spk_residual_add_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, int6
  * outside [0, vocab) give zero rows). */
 int spk_embedding_f16(const uint16_t* E, const int32_t* tokens, int32_t n_tokens, int32_t vocab,
                       uint16_t* y, spk_stream_t stream);
+/* Final RMSNorm(1+w) (rms_norm.comp; skipped when norm_w is NULL, else
+ * hidden == 1024), tied lm_head (lm_head_tiled.comp's order, as
+ * spk_lm_head_argmax) and argmax.comp's winner, in one launch: every
+ * workgroup folds its best 64-bit key into one of SPK_ARGMAX_KEY_WORDS device
+ * words with a device-scope atomic max.  key: SPK_ARGMAX_KEY_WORDS words
+ * (512 bytes) of device memory that hold 0 before the call;
+ * spk_argmax_key_take reduces them and sets them back to 0.  The final norm,
+ * lm_head, argmax and record-token dispatches of vk_session.cpp:3533-3563
+ * become this call and the take. */
+#define SPK_ARGMAX_KEY_WORDS 64
+int spk_lm_head_argmax_key(const uint16_t* W, const uint16_t* x, const uint16_t* norm_w, int32_t vocab,
+                           int32_t hidden, uint16_t* logits, uint64_t* key, spk_stream_t stream);
+/* *out_index = argmax.comp's index for the key words left by
+ * spk_lm_head_argmax_key over `vocab` rows; the words are set to 0.  With pos != NULL the token is also
+ * recorded as spk_record_token does (history[*count] = index when *count <
+ * capacity, *count += 1, *pos += 1). */
+int spk_argmax_key_take(uint64_t* key, int32_t vocab, uint32_t* out_index, int32_t* pos, int32_t* count,
+                        int32_t* history, int32_t capacity, spk_stream_t stream);
 /* *p += delta on the device (advances a device position counter). */
 int spk_add_i32(int32_t* p, int32_t delta, spk_stream_t stream);
 

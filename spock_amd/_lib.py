@@ -42,12 +42,15 @@ SIGNATURES = {
     "spk_attention_workspace_size": (_sz, [_i32, _i32]),
     "spk_attention_decode": (C.c_int, [_p, _p]),
     "spk_attention_prefill": (C.c_int, [_p, _i32, _i32, _p]),
+    "spk_attention_decode_oproj": (C.c_int, [_p, _p, _p]),
     "spk_rmsnorm_f16": (C.c_int, [_p, _p, _p, _i32, _i32, _p]),
     "spk_silu_gate_f16": (C.c_int, [_p, _p, _p, _i64, _p]),
     "spk_residual_add_f16": (C.c_int, [_p, _p, _p, _i64, _p]),
     "spk_embedding_f16": (C.c_int, [_p, _p, _i32, _i32, _p, _p]),
     "spk_add_i32": (C.c_int, [_p, _i32, _p]),
     "spk_record_token": (C.c_int, [_p, _p, _p, _p, _i32, _p]),
+    "spk_lm_head_argmax_key": (C.c_int, [_p, _p, _p, _i32, _i32, _p, _p, _p]),
+    "spk_argmax_key_take": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i32, _p]),
     "spk_gemm_f16": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _i32, _i32, _i32, _p]),
     "spk_deltanet_prefill_conv": (C.c_int, [_p, _i64, _p, _p, _i32, _p, _p, _p, _p]),
     "spk_deltanet_prefill_gbeta": (C.c_int, [_p, _p, _i64, _p, _i32, _i32, _p, _p, _p]),

@@ -1,22 +1,28 @@
 // decode.hip -- DeltaNet recurrent decode step for B independent sequences.
 //
-// One workgroup (256 lanes, 4 wavefronts) per (head, sequence).  The fused
-// variant performs, in one launch and with one read and one write of the
-// head's 64 KiB fp32 state:
+// One workgroup of 4, 8 or 16 wavefronts per (head, sequence): the launch
+// picks the width from the batch (16 wavefronts when a handful of heads must
+// carry the whole launch, 4 when thousands of workgroups fill the chip).  The
+// fused variant performs, in one launch and with one read and one write of
+// the head's 64 KiB fp32 state:
 //   deltanet_conv_l2_qk.comp:41-111              conv-state shift, depthwise
 //       conv (k=4) + SiLU, fp16 store, L2 of the Q and K head blocks;
 //   deltanet_recurrent_gbeta_norm_gate.comp:91-225  g/beta, decay, kv=S^T k,
 //       delta, rank-1 update, o=S^T q, RMSNorm, fp16(w*n)*SiLU(z).
-// The state stream is the cost (2 x 64 KiB per head): each lane owns a 16-row
-// x 4-column slice loaded as 16 float4 (global_load_dwordx4, row segments of
-// 512 B per 32 lanes).  Every global load is issued at the start, so no phase
-// after the conv waits on a memory round trip of its own.
+// The state stream is the cost (2 x 64 KiB per head): each lane owns
+// 16 / (WAVES / 4) consecutive rows x 4 columns, loaded as float4
+// (global_load_dwordx4, row segments of 512 B per 32 lanes).  Every global
+// load is issued at the start, so no phase after the conv waits on a memory
+// round trip of its own.  g/beta (a chain of exp/log) is evaluated by the
+// fourth wavefront while the first three run the conv.
 //
 // Reduction orders (fixed, and restated by the CPU oracle):
 //   conv taps summed i = 0..3; L2 / RMS sums use the shaders' 128-wide tree
 //   (s[l] += s[l+64], then 32..1: lane-local add, then wave shuffles);
 //   S^T x per column: 32 row groups of 4 rows, fma-accumulated from 0 in row
 //   order, then combined by a balanced pairwise tree (adjacent pairs first).
+#include <stdlib.h>
+
 #include "capi_common.hpp"
 #include "numerics.hpp"
 
@@ -59,8 +65,12 @@ __device__ __forceinline__ float tree32(const float (*part)[128], int col) {
 // CONV: run the conv/L2 phase.  REC: run the recurrence.  GB_TAIL: g/beta from
 // the state tail (deltanet_recurrent.comp) instead of a/b/A_log/dt_bias.
 // NORM_GATE: RMSNorm-gate the output (else fp16 of the raw output).
-template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE>
-__global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
+template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
+  // G row groups of 4 rows per lane: 32 row groups over WAVES*2 lanes per column
+  constexpr int G = 32 / (WAVES * 2);
+  constexpr int M = 4 * G;  // rows per lane
+  static_assert(WAVES == 4 || WAVES == 8 || WAVES == 16, "4, 8 or 16 wavefronts");
   const int h = blockIdx.x;
   const int seq = blockIdx.y;
   const int tid = threadIdx.x;
@@ -71,13 +81,31 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
 
   __shared__ float s_q[128], s_k[128], s_v[128], s_delta[128];
   __shared__ float s_part[32][128];
+  __shared__ float s_gb[2];
 
   const int c4 = tid & 31;  // owns columns 4*c4 .. 4*c4+3
-  const int rq = tid >> 5;  // owns row groups 4*rq .. 4*rq+3, i.e. rows 16*rq .. 16*rq+15
-  // The small g/beta and norm-gate operands are loaded first and without a
-  // branch (a branch around a load makes the compiler wait for the loads
-  // before it), then the state; the conv operands follow inside the conv
-  // branch.  No later phase waits on a memory round trip of its own.
+  const int rq = tid >> 5;  // owns row groups G*rq .. G*rq+G-1, i.e. rows M*rq .. M*rq+M-1
+  // Load order: the conv operands, then the small g/beta and norm-gate
+  // operands, then the state, all without a branch (a branch around a load
+  // makes the compiler wait for the loads before it).  A wave's loads return
+  // in issue order, so the conv waves start on their operands while the
+  // state stream is still in flight, and no later phase waits on a memory
+  // round trip of its own.  Waves 3.. load a copy of the V block's conv
+  // operands (cache hits, unused) so that the loads need no branch.
+  uint2 olds[2] = {}, wvs[2] = {};
+  uint16_t xs[2] = {0, 0};
+  const int conv_blk = wave < 3 ? wave : 2;  // wave 0: Q block, 1: K block, 2: V block
+  const int ch0 = conv_blk * nh * 128 + h * 128;
+  uint16_t* cs_seq = CONV ? p.conv_state + (long long)seq * p.conv_stride : nullptr;
+  if (CONV) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int ch = ch0 + lane + 64 * half;
+      olds[half] = *reinterpret_cast<const uint2*>(cs_seq + ch * 4);
+      wvs[half] = *reinterpret_cast<const uint2*>(p.conv_w + ch * 4);
+      xs[half] = qkv[ch];
+    }
+  }
   uint16_t a16 = 0, b16 = 0;
   float a_log = 0.0f, dt_bias = 0.0f, g_tail = 0.0f, beta_tail = 0.0f;
   uint16_t z16[2] = {0, 0};
@@ -101,30 +129,27 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
       nw[1] = p.norm_w[lane + 64];
     }
   }
-  float4 S[16];
+  float4 S[M];
   float* st_head = nullptr;
   if (REC) {
     st_head = p.state + (long long)seq * p.state_stride + (long long)h * 128 * 128;
 #pragma unroll
-    for (int m = 0; m < 16; ++m)
-      S[m] = *reinterpret_cast<const float4*>(st_head + (rq * 16 + m) * 128 + c4 * 4);
+    for (int m = 0; m < M; ++m)
+      S[m] = *reinterpret_cast<const float4*>(st_head + (rq * M + m) * 128 + c4 * 4);
   }
 
+  if (REC && !GB_TAIL && wave == 3) {
+    // g/beta while waves 0-2 run the conv (deltanet_recurrent_gbeta_norm_gate.comp:102-116)
+    if (lane == 0) {
+      const float av = spk::h2f(a16);
+      const float bv = spk::h2f(b16);
+      const float sp = spk::logf_det(1.0f + spk::expf_det(av + dt_bias));
+      s_gb[0] = -spk::expf_det(a_log) * sp;
+      s_gb[1] = 1.0f / (1.0f + spk::expf_det(-bv));
+    }
+  }
   if (CONV) {
     if (wave < 3) {
-      // wave 0: Q block of head h, wave 1: K block, wave 2: V block.
-      const int ch0 = wave * nh * 128 + h * 128;
-      uint16_t* cs_seq = p.conv_state + (long long)seq * p.conv_stride;
-      // both halves' operands are loaded before the first conv-state store
-      uint2 olds[2], wvs[2];
-      uint16_t xs[2];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int ch = ch0 + lane + 64 * half;
-        olds[half] = *reinterpret_cast<const uint2*>(cs_seq + ch * 4);
-        wvs[half] = *reinterpret_cast<const uint2*>(p.conv_w + ch * 4);
-        xs[half] = qkv[ch];
-      }
       uint16_t y[2];
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -180,27 +205,24 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
   }
   if (!REC) return;
 
+  __syncthreads();
   float g, beta;
   if (GB_TAIL) {
     g = g_tail;
     beta = beta_tail;
   } else {
-    const float av = spk::h2f(a16);
-    const float bv = spk::h2f(b16);
-    const float sp = spk::logf_det(1.0f + spk::expf_det(av + dt_bias));
-    g = -spk::expf_det(a_log) * sp;
-    beta = 1.0f / (1.0f + spk::expf_det(-bv));
+    g = s_gb[0];
+    beta = s_gb[1];
   }
-  __syncthreads();
 
   // decay + kv partials, one per 4-row group
   const float eg = spk::expf_det(g);
 #pragma unroll
-  for (int gq = 0; gq < 4; ++gq) {
+  for (int gq = 0; gq < G; ++gq) {
     float kp0 = 0.f, kp1 = 0.f, kp2 = 0.f, kp3 = 0.f;
 #pragma unroll
     for (int m = 4 * gq; m < 4 * gq + 4; ++m) {
-      const float ki = s_k[rq * 16 + m];
+      const float ki = s_k[rq * M + m];
       S[m].x = S[m].x * eg;
       S[m].y = S[m].y * eg;
       S[m].z = S[m].z * eg;
@@ -210,7 +232,7 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
       kp2 = __builtin_fmaf(S[m].z, ki, kp2);
       kp3 = __builtin_fmaf(S[m].w, ki, kp3);
     }
-    *reinterpret_cast<float4*>(&s_part[4 * rq + gq][c4 * 4]) = make_float4(kp0, kp1, kp2, kp3);
+    *reinterpret_cast<float4*>(&s_part[G * rq + gq][c4 * 4]) = make_float4(kp0, kp1, kp2, kp3);
   }
   __syncthreads();
   if (tid < 128) {
@@ -222,23 +244,23 @@ __global__ __launch_bounds__(256) void dn_decode_kernel(DecodeParams p) {
   // rank-1 update, state write-back, output partials per 4-row group
   const float4 d4 = *reinterpret_cast<const float4*>(&s_delta[c4 * 4]);
 #pragma unroll
-  for (int gq = 0; gq < 4; ++gq) {
+  for (int gq = 0; gq < G; ++gq) {
     float op0 = 0.f, op1 = 0.f, op2 = 0.f, op3 = 0.f;
 #pragma unroll
     for (int m = 4 * gq; m < 4 * gq + 4; ++m) {
-      const float ki = s_k[rq * 16 + m];
-      const float qi = s_q[rq * 16 + m];
+      const float ki = s_k[rq * M + m];
+      const float qi = s_q[rq * M + m];
       S[m].x = __builtin_fmaf(ki, d4.x, S[m].x);
       S[m].y = __builtin_fmaf(ki, d4.y, S[m].y);
       S[m].z = __builtin_fmaf(ki, d4.z, S[m].z);
       S[m].w = __builtin_fmaf(ki, d4.w, S[m].w);
-      *reinterpret_cast<float4*>(st_head + (rq * 16 + m) * 128 + c4 * 4) = S[m];
+      *reinterpret_cast<float4*>(st_head + (rq * M + m) * 128 + c4 * 4) = S[m];
       op0 = __builtin_fmaf(S[m].x, qi, op0);
       op1 = __builtin_fmaf(S[m].y, qi, op1);
       op2 = __builtin_fmaf(S[m].z, qi, op2);
       op3 = __builtin_fmaf(S[m].w, qi, op3);
     }
-    *reinterpret_cast<float4*>(&s_part[4 * rq + gq][c4 * 4]) = make_float4(op0, op1, op2, op3);
+    *reinterpret_cast<float4*>(&s_part[G * rq + gq][c4 * 4]) = make_float4(op0, op1, op2, op3);
   }
   __syncthreads();
 
@@ -325,14 +347,37 @@ DecodeParams make_params(const SpkDecodeArgs* a) {
   return p;
 }
 
+// Wavefronts per workgroup by the number of workgroups the launch has:
+// overridable with SPK_DECODE_WAVES=4|8|16 (measurement only).
+int decode_waves(int workgroups) {
+  static const int forced = [] {
+    const char* e = getenv("SPK_DECODE_WAVES");
+    const int v = e ? atoi(e) : 0;
+    return (v == 4 || v == 8 || v == 16) ? v : 0;
+  }();
+  if (forced) return forced;
+  if (workgroups <= 64) return 16;
+  if (workgroups <= 512) return 8;
+  return 4;
+}
+
 template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE>
 int launch(const SpkDecodeArgs* a, spk_stream_t stream, const char* name) {
   const int rc = validate(a, CONV, REC, REC && !GB_TAIL, REC && NORM_GATE);
   if (rc) return rc;
   if (a->batch == 0) return SPK_OK;
   dim3 grid(a->num_heads, a->batch);
-  hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE>), grid, dim3(256), 0,
-                     spk::to_hip(stream), make_params(a));
+  const int waves = decode_waves(a->num_heads * a->batch);
+  hipStream_t s = spk::to_hip(stream);
+  if (waves == 16)
+    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 16>), grid, dim3(1024), 0, s,
+                       make_params(a));
+  else if (waves == 8)
+    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 8>), grid, dim3(512), 0, s,
+                       make_params(a));
+  else
+    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 4>), grid, dim3(256), 0, s,
+                       make_params(a));
   return spk::check_launch(name);
 }
 

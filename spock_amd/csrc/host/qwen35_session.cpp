@@ -160,7 +160,6 @@ Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::u
   rope_.upload(rope.data(), rope.size() * 4);
 
   h_ = DeviceBuffer(H * 2);
-  hn_ = DeviceBuffer(H * 2);
   qkv_ = DeviceBuffer(CONV * 2);
   z_ = DeviceBuffer(VAL * 2);
   a_ = DeviceBuffer(256);
@@ -173,7 +172,8 @@ Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::u
   up_ = DeviceBuffer(INTER * 2);
   logits_ = DeviceBuffer(V * 2);
   attn_ws_ = DeviceBuffer(spk_attention_workspace_size(static_cast<int32_t>(max_seq_), 1));
-  lm_ws_ = DeviceBuffer(spk_lm_head_workspace_size(static_cast<int32_t>(V)));
+  argmax_key_ = DeviceBuffer(SPK_ARGMAX_KEY_WORDS * 8);
+  argmax_key_.zero(stream_);  // spk_argmax_key_take returns it to zero after every use
   tok_ = DeviceBuffer(256);
   pos_ = DeviceBuffer(256);
   history_cap_ = max_seq_;
@@ -348,18 +348,18 @@ std::uint32_t Qwen35Session::prefill(const std::vector<std::uint32_t>& tokens) {
   // Last token: final norm, lm_head + argmax, token bookkeeping on the device.
   const std::uint16_t* last = Hs + std::size_t(T - 1) * H;
   hip_check(hipMemcpyAsync(h_.get(), last, H * 2, hipMemcpyDeviceToDevice, stream_), "last hidden");
-  spk_check(spk_rmsnorm_f16(last, final_norm_, hn_.get<std::uint16_t>(), 1, H, S(stream_)), "final norm");
-  spk_check(spk_lm_head_argmax(embed_, hn_.get<std::uint16_t>(), static_cast<int32_t>(shape_.vocab), H,
-                               logits_.get<std::uint16_t>(), tok_.get<std::uint32_t>(), lm_ws_.get(), lm_ws_.bytes(),
-                               S(stream_)),
+  const int32_t vocab = static_cast<int32_t>(shape_.vocab);
+  spk_check(spk_lm_head_argmax_key(embed_, last, final_norm_, vocab, H, logits_.get<std::uint16_t>(),
+                                   argmax_key_.get<std::uint64_t>(), S(stream_)),
             "lm_head");
   const std::int32_t pos_count[2] = {p0 + Ti - 1, 0};
   hip_check(hipMemcpyAsync(pos_.get(), &pos_count[0], 4, hipMemcpyHostToDevice, stream_), "position");
   hip_check(hipMemcpyAsync(history_.get(), &pos_count[1], 4, hipMemcpyHostToDevice, stream_), "history count");
   std::int32_t* hist = history_.get<std::int32_t>();
-  spk_check(spk_record_token(tok_.get<std::int32_t>(), pos_.get<std::int32_t>(), hist, hist + 64,
-                             static_cast<int32_t>(history_cap_), S(stream_)),
-            "record token");
+  spk_check(spk_argmax_key_take(argmax_key_.get<std::uint64_t>(), vocab, tok_.get<std::uint32_t>(),
+                                pos_.get<std::int32_t>(), hist, hist + 64, static_cast<int32_t>(history_cap_),
+                                S(stream_)),
+            "argmax take");
   hip_check(hipEventRecord(ev.b, stream_), "hipEventRecord");
   std::int32_t first = 0;
   hip_check(hipMemcpyAsync(&first, hist + 64, 4, hipMemcpyDeviceToHost, stream_), "first token");
@@ -433,13 +433,10 @@ void Qwen35Session::enqueue_decode_step() {
       aa.out = attn_out_.get<std::uint16_t>();
       aa.workspace = attn_ws_.get();
       aa.workspace_bytes = attn_ws_.bytes();
-      spk_check(spk_attention_decode(&aa, S(stream_)), "attention decode");
-      SpkGemvInput oi{};
-      oi.kind = SPK_GEMV_IN_PLAIN;
-      oi.in_dim = 2048;
-      oi.x = attn_out_.get<std::uint16_t>();
+      // attention blocks, then o_proj + residual with the blocks' combine and
+      // sigmoid gate in its prologue
       const SpkGemvOutput oo{w.attn_o, h, h, static_cast<int32_t>(H), nullptr};
-      spk_check(spk_gemv_fused(&oi, &oo, 1, S(stream_)), "o_proj");
+      spk_check(spk_attention_decode_oproj(&aa, &oo, S(stream_)), "attention decode + o_proj");
     }
     SpkGemvInput mi{};
     mi.kind = SPK_GEMV_IN_RMSNORM;
@@ -456,15 +453,16 @@ void Qwen35Session::enqueue_decode_step() {
     const SpkGemvOutput dout{w.mlp_down, h, h, static_cast<int32_t>(H), nullptr};
     spk_check(spk_gemv_fused(&di, &dout, 1, S(stream_)), "down_proj");
   }
-  spk_check(spk_rmsnorm_f16(h, final_norm_, hn_.get<std::uint16_t>(), 1, H, S(stream_)), "final norm");
-  spk_check(spk_lm_head_argmax(embed_, hn_.get<std::uint16_t>(), static_cast<int32_t>(shape_.vocab), H,
-                               logits_.get<std::uint16_t>(), reinterpret_cast<std::uint32_t*>(tok), lm_ws_.get(),
-                               lm_ws_.bytes(), S(stream_)),
+  // final norm + lm_head + argmax key in one launch; the take records the token
+  const int32_t vocab = static_cast<int32_t>(shape_.vocab);
+  spk_check(spk_lm_head_argmax_key(embed_, h, final_norm_, vocab, H, logits_.get<std::uint16_t>(),
+                                   argmax_key_.get<std::uint64_t>(), S(stream_)),
             "lm_head");
   std::int32_t* hist = history_.get<std::int32_t>();
-  spk_check(spk_record_token(tok, pos_.get<std::int32_t>(), hist, hist + 64, static_cast<int32_t>(history_cap_),
-                             S(stream_)),
-            "record token");
+  spk_check(spk_argmax_key_take(argmax_key_.get<std::uint64_t>(), vocab, reinterpret_cast<std::uint32_t*>(tok),
+                                pos_.get<std::int32_t>(), hist, hist + 64, static_cast<int32_t>(history_cap_),
+                                S(stream_)),
+            "argmax take");
 }
 
 void Qwen35Session::ensure_graph() {

@@ -128,8 +128,8 @@ class Qwen35Session {
   // per-layer state
   DeviceBuffer dn_state_, conv_state_, kv_cache_, a_log_bias_, rope_;
   // decode activations
-  DeviceBuffer h_, hn_, qkv_, z_, a_, b_, qg_, k_, v_, attn_out_, gate_, up_, logits_;
-  DeviceBuffer attn_ws_, lm_ws_, tok_, pos_, history_;
+  DeviceBuffer h_, qkv_, z_, a_, b_, qg_, k_, v_, attn_out_, gate_, up_, logits_;
+  DeviceBuffer attn_ws_, argmax_key_, tok_, pos_, history_;
   std::uint32_t history_cap_ = 0;   // token history capacity (= max_seq_: one token per position)
   // prefill activations (capacity prefill_cap_ tokens)
   std::uint32_t prefill_cap_ = 0;

@@ -12,6 +12,7 @@
 //   GEMV: 64 lanes x contiguous spans, fma chains from 0, then the 32..1 tree
 //   attention: blocks of 64 positions; per block max, exp, 64-lane tree of the
 //     weights and fma chains over positions; blocks combined in order.
+#include "argmax_key.hpp"
 #include "capi_common.hpp"
 #include "numerics.hpp"
 
@@ -25,6 +26,7 @@ constexpr int kQHeads = 8;
 constexpr int kKvHeads = 2;
 constexpr int kKvRow = 1024;  // K 2x256 | V 2x256 halves per cached position
 constexpr int kAttnBlock = 64;
+constexpr int kPartFloats = 2 + kHeadDim;  // attention block partials: m, S, O[256]
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -93,7 +95,19 @@ struct FusedGemv {
   const uint16_t* res[kLaunchOut];
   int out_dim[kLaunchOut];
   int first_block[kLaunchOut + 1];
+  // input kind kInAttn: the attention blocks' partials (m, S, O[256]) per
+  // (query head, block of 64 positions), the position read on the device and
+  // the gate halves of the q projection (x = qg)
+  const float* part;
+  int max_blocks;
+  int max_seq;
+  const int32_t* pos_dev;
 };
+
+// Input kind of the o_proj GEMV fused behind attention decode (not in the C
+// ABI's SpkGemvInput: spk_attention_decode_oproj selects it).
+constexpr int kInAttn = 3;
+constexpr int kAttnPre = 16;  // blocks whose partials are loaded with the weight rows
 
 template <int N8, int R>
 __device__ __forceinline__ void load_rows(const uint16_t* __restrict__ W, int row0, int out_dim, int lane,
@@ -157,7 +171,30 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   static_assert(256 * PER * 8 <= kMaxIn, "x staging overruns xs");
   uint2 hv = make_uint2(0, 0), nwv = make_uint2(0, 0);
   uint4 xv[PER], uv[PER];
-  if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
+  // kInAttn: lane group (h = tid/32, j = tid%32) owns dims 8j..8j+7 of query
+  // head h; the first kAttnPre blocks' m, S and O are loaded here (their
+  // addresses do not depend on the position), clamped to the grid's blocks.
+  int apos = 0;
+  float am = 0.0f, as = 0.0f;
+  float4 aO[KIND == kInAttn ? kAttnPre : 1][2];
+  uint4 agate = make_uint4(0, 0, 0, 0);
+  if constexpr (KIND == kInAttn) {
+    const int h = tid >> 5, j = tid & 31;
+    // position and gate first: a wave's loads return in issue order, so the
+    // sigmoids start while the partials are still in flight
+    apos = a.pos_dev[0];
+    agate = *reinterpret_cast<const uint4*>(a.x + h * 512 + 256 + 8 * j);
+    const float* ph = a.part + (size_t)h * a.max_blocks * kPartFloats;
+    const int bj = min(j, a.max_blocks - 1);
+    am = ph[(size_t)bj * kPartFloats];
+    as = ph[(size_t)bj * kPartFloats + 1];
+#pragma unroll
+    for (int i = 0; i < kAttnPre; ++i) {
+      const float* po = ph + (size_t)min(i, a.max_blocks - 1) * kPartFloats + 2 + 8 * j;
+      aO[i][0] = *reinterpret_cast<const float4*>(po);
+      aO[i][1] = *reinterpret_cast<const float4*>(po + 4);
+    }
+  } else if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
     const uint16_t* h = a.x;
     if (a.token) {  // ids outside [0, token_rows) select row 0 instead of reading out of bounds
       const int id = a.token[0];
@@ -185,7 +222,73 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   load_rows<N8, R>(Wd, row0, out_dim, lane, wv);
   if (PAIR) load_rows<N8, PAIR ? R : 1>(W2d, row0, out_dim, lane, wv2);
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue
-  if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {
+  if constexpr (KIND == kInAttn) {
+    // attn_combine_kernel's arithmetic for the 2048 gated outputs: blocks
+    // combined in order (tot += S_b c_b, O += O_b c_b, c_b = e^{m_b - M}),
+    // normalised, fp16, times sigmoid(gate), fp16.  Lane j of the head's 32
+    // computes c_b and S_b of block b = j (+32 per chunk); the others take
+    // them by shuffle, so no barrier is needed.
+    const int h = tid >> 5, j = tid & 31;
+    const int gbase = tid & 32;  // this head's first lane in the wave
+    float sig[8];
+    {
+      float g[8];
+      unpack8(agate, g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sig[e] = 1.0f / (1.0f + spk::expf_det(-g[e]));
+    }
+    const float* ph = a.part + (size_t)h * a.max_blocks * kPartFloats;
+    const int nb = (apos >= 0 && apos < a.max_seq) ? (apos + kAttnBlock) / kAttnBlock : 0;
+    float M = j < nb ? am : -INFINITY;
+    for (int b = j + 32; b < nb; b += 32) M = fmaxf(M, ph[(size_t)b * kPartFloats]);
+#pragma unroll
+    for (int sh = 16; sh >= 1; sh >>= 1) M = fmaxf(M, __shfl_xor(M, sh, 64));
+    float tot = 0.0f;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nb; c0 += 32) {
+      float mj = am, sj = as;
+      if (c0 > 0 && c0 + j < nb) {
+        mj = ph[(size_t)(c0 + j) * kPartFloats];
+        sj = ph[(size_t)(c0 + j) * kPartFloats + 1];
+      }
+      const float cj = (c0 + j < nb) ? spk::expf_det(mj - M) : 0.0f;
+      const int n = min(32, nb - c0);
+#pragma unroll
+      for (int i0 = 0; i0 < 32; i0 += 8) {
+        if (i0 >= n) break;
+        float4 ov[8][2];
+        if (i0 < kAttnPre && c0 == 0) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            ov[i][0] = aO[i0 < kAttnPre ? i0 + i : 0][0];
+            ov[i][1] = aO[i0 < kAttnPre ? i0 + i : 0][1];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float* po = ph + (size_t)(c0 + min(i0 + i, n - 1)) * kPartFloats + 2 + 8 * j;
+            ov[i][0] = *reinterpret_cast<const float4*>(po);
+            ov[i][1] = *reinterpret_cast<const float4*>(po + 4);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float c = __shfl(cj, gbase + i0 + i, 64);
+          const float sb = __shfl(sj, gbase + i0 + i, 64);
+          if (i0 + i < n) {
+            tot = tot + sb * c;
+            const float vv[8] = {ov[i][0].x, ov[i][0].y, ov[i][0].z, ov[i][0].w,
+                                 ov[i][1].x, ov[i][1].y, ov[i][1].z, ov[i][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = o[e] + vv[e] * c;
+          }
+        }
+      }
+    }
+    const float inv = 1.0f / (tot + 1e-30f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xs[h * kHeadDim + 8 * j + e] = round16(round16(o[e] * inv) * sig[e]);
+  } else if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {
     const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
                         spk::h2f(hv.y >> 16)};
     const float w[4] = {spk::h2f(nwv.x & 0xffffu), spk::h2f(nwv.x >> 16), spk::h2f(nwv.y & 0xffffu),
@@ -258,7 +361,6 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
 // m_b, S_b, O_b[256].  Kernel 2: per query head, combine blocks in order,
 // normalise, sigmoid gate.
 // ---------------------------------------------------------------------------
-constexpr int kPartFloats = 2 + kHeadDim;  // m, S, O[256]
 
 // Per-head RMSNorm(1+w) of the 256 values a wave holds (lane l: d = 4l..4l+3),
 // in the s[t] += s[t+stride] (stride 128..1) order; returns fp16-rounded values.
@@ -778,6 +880,129 @@ __global__ __launch_bounds__(128) void embedding_kernel(const uint16_t* __restri
   reinterpret_cast<uint4*>(y + (size_t)t * kHidden)[threadIdx.x] = v;
 }
 
+// ---------------------------------------------------------------------------
+// Final norm + tied lm_head + argmax in one launch (rms_norm.comp,
+// lm_head_tiled.comp, argmax.comp): the RMSNorm(1+w) of h is recomputed by
+// every workgroup while its weight rows are in flight (the fused GEMV's
+// prologue), each wavefront streams R vocabulary rows with non-temporal
+// 16-byte loads, and the workgroup's argmax key is folded into one of 64
+// device words with a device-scope atomic max (posted: no return, no wait).
+// One word for all workgroups serialises the atomics (measured: 7,760 of them
+// add ~34 us to a 85 us stream); workgroup b uses word b % 64.  The take
+// kernel of the next launch reduces and clears the 64 words.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int N8, int R, bool NORM>
+__global__ __launch_bounds__(256) void lm_head_key_kernel(const uint16_t* __restrict__ W,
+                                                          const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ norm_w,
+                                                          uint16_t* __restrict__ logits, int vocab,
+                                                          uint32_t E, unsigned long long* key_out) {
+  __shared__ float xs[512 * N8];
+  __shared__ float red[257];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  constexpr int in_dim = 512 * N8;
+  constexpr int NV = in_dim / 8;  // 16-byte pieces of x
+  constexpr int PER = (NV + 255) / 256;
+  static_assert(!NORM || N8 == 2, "the norm prologue is rms_norm.comp's over 1024");
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  uint2 hv = make_uint2(0, 0), nwv = make_uint2(0, 0);
+  uint4 xv[PER];
+  if constexpr (NORM) {
+    hv = *reinterpret_cast<const uint2*>(x + 4 * tid);
+    nwv = *reinterpret_cast<const uint2*>(norm_w + 4 * tid);
+  } else {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) xv[c] = *reinterpret_cast<const uint4*>(x + 8 * min(tid + 256 * c, NV - 1));
+  }
+  uint4 wv[R][N8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row0 + r, vocab - 1);
+    const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
+#pragma unroll
+    for (int k = 0; k < N8; ++k) wv[r][k] = ld_stream(src + k);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every weight row in flight before the prologue
+  if constexpr (NORM) {
+    const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
+                        spk::h2f(hv.y >> 16)};
+    const float w[4] = {spk::h2f(nwv.x & 0xffffu), spk::h2f(nwv.x >> 16), spk::h2f(nwv.y & 0xffffu),
+                        spk::h2f(nwv.y >> 16)};
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p = __builtin_fmaf(v[i], v[i], p);
+    const float sum = block_tree256(p, red);
+    const float nf = 1.0f / __builtin_sqrtf(sum / 1024.0f + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[4 * tid + i] = round16((v[i] * nf) * (1.0f + w[i]));
+  } else {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = min(tid + 256 * c, NV - 1);
+      float f[8];
+      unpack8(xv[c], f);
+#pragma unroll
+      for (int e = 0; e < 8; e += 4) *reinterpret_cast<float4*>(&xs[8 * idx + e]) = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
+    }
+  }
+  __syncthreads();
+  float xf[8 * N8];
+#pragma unroll
+  for (int k = 0; k < 8 * N8; k += 4) {
+    const float4 t = *reinterpret_cast<const float4*>(&xs[lane * (8 * N8) + k]);
+    xf[k] = t.x;
+    xf[k + 1] = t.y;
+    xf[k + 2] = t.z;
+    xf[k + 3] = t.w;
+  }
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = lane_dot<N8>(wv[r], xf);
+  spk::tree64_rows<R>(acc);
+  unsigned long long key = 0ull;
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = row0 + r;
+      if (row < vocab) {
+        const uint16_t l16 = spk::f2h(acc[r]);
+        if (logits) logits[row] = l16;
+        key = spk::umax64(key, spk::argmax_key(spk::h2f(l16), (uint32_t)row, E));
+      }
+    }
+  }
+  key = spk::block_max_u64<256>(key);
+  if (tid == 0 && key != 0ull)
+    __hip_atomic_fetch_max(key_out + (blockIdx.x & (SPK_ARGMAX_KEY_WORDS - 1)), key, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// *out = index of the largest of the 64 key words (which are then zeroed);
+// with pos != NULL also the greedy loop's bookkeeping of record_token_kernel.
+// One wavefront: lane l takes word l.
+__global__ __launch_bounds__(64) void argmax_take_kernel(unsigned long long* key, uint32_t E, uint32_t* out,
+                                                         int32_t* pos, int32_t* count, int32_t* history, int cap) {
+  unsigned long long k = __hip_atomic_exchange(key + threadIdx.x, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  k = spk::wave_max_u64(k);
+  if (threadIdx.x == 0) {
+    const uint32_t idx = spk::key_to_index(k, E);
+    *out = idx;
+    if (pos) {
+      const int i = count[0];
+      if (i >= 0 && i < cap) history[i] = (int32_t)idx;
+      count[0] = i + 1;
+      pos[0] = pos[0] + 1;
+    }
+  }
+}
+
 __global__ void add_i32_kernel(int32_t* p, int32_t delta) {
   if (threadIdx.x == 0) p[0] += delta;
 }
@@ -830,6 +1055,10 @@ static int launch_fused_gemv(const SpkGemvInput* in, const SpkGemvOutput* outs, 
     a.first_block[i] = blocks;
   }
   a.first_block[kLaunchOut] = blocks;
+  a.part = nullptr;
+  a.max_blocks = 0;
+  a.max_seq = 0;
+  a.pos_dev = nullptr;
   hipStream_t s = spk::to_hip(stream);
   const bool pair = outs[0].W_up != nullptr;
 #define SPK_FGK(n8, r, kind)                                                                            \
@@ -912,17 +1141,19 @@ extern "C" size_t spk_attention_workspace_size(int32_t positions, int32_t tokens
   return (((size_t)tokens * kQHeads * nb * kPartFloats * sizeof(float)) + 255) / 256 * 256;
 }
 
-static int attention_common(const SpkAttnArgs* p, int T, int positions, const char* who, AttnArgs& a) {
+static int attention_common(const SpkAttnArgs* p, int T, int positions, const char* who, AttnArgs& a,
+                            bool need_out = true) {
   if (!p) return spk::fail(SPK_ERR_NULL, "%s: NULL args", who);
-  if (!p->qg || !p->k || !p->v || !p->q_norm_w || !p->k_norm_w || !p->rope || !p->kv_cache || !p->out ||
-      !p->workspace)
+  if (!p->qg || !p->k || !p->v || !p->q_norm_w || !p->k_norm_w || !p->rope || !p->kv_cache ||
+      (need_out && !p->out) || !p->workspace)
     return spk::fail(SPK_ERR_NULL, "%s: NULL pointer", who);
   if (p->max_seq <= 0 || p->max_seq > 65536 || T <= 0 || positions > 65536)
     return spk::fail(SPK_ERR_SHAPE, "%s: max_seq %d (at most 65536) tokens %d", who, p->max_seq, T);
   if (p->workspace_bytes < spk_attention_workspace_size(positions, T))
     return spk::fail(SPK_ERR_ARG, "%s: workspace %zu < %zu bytes", who, p->workspace_bytes,
                      spk_attention_workspace_size(positions, T));
-  const void* ptrs[] = {p->qg, p->k, p->v, p->q_norm_w, p->k_norm_w, p->kv_cache, p->out, p->workspace};
+  const void* ptrs[] = {p->qg, p->k, p->v, p->q_norm_w, p->k_norm_w, p->kv_cache, need_out ? p->out : p->qg,
+                        p->workspace};
   for (const void* q : ptrs)
     if (!spk::aligned(q, 16)) return spk::fail(SPK_ERR_ALIGN, "%s: buffers must be 16-byte aligned", who);
   a.qg = p->qg;
@@ -954,6 +1185,42 @@ extern "C" int spk_attention_decode(const SpkAttnArgs* p, spk_stream_t stream) {
   if (rc) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(kQHeads, 1), dim3(256), 0, s, a);
   return spk::check_launch("spk_attention_decode (combine)");
+}
+
+extern "C" int spk_attention_decode_oproj(const SpkAttnArgs* p, const SpkGemvOutput* o_proj, spk_stream_t stream) {
+  const char* name = "spk_attention_decode_oproj";
+  if (!o_proj || !o_proj->W || !o_proj->y) return spk::fail(SPK_ERR_NULL, "%s: NULL o_proj", name);
+  if (o_proj->W_up || o_proj->out_dim <= 0)
+    return spk::fail(SPK_ERR_SHAPE, "%s: o_proj out_dim %d (single projection)", name, o_proj->out_dim);
+  if (!spk::aligned(o_proj->W, 16)) return spk::fail(SPK_ERR_ALIGN, "%s: o_proj W must be 16-byte aligned", name);
+  AttnArgs a;
+  int rc = attention_common(p, 1, p ? p->max_seq : 0, name, a, false);
+  if (rc) return rc;
+  if (!p->pos_dev) return spk::fail(SPK_ERR_NULL, "%s: NULL pos_dev", name);
+  a.pos_dev = p->pos_dev;
+  a.pos0 = 0;
+  a.store_kv = 1;
+  hipStream_t s = spk::to_hip(stream);
+  hipLaunchKernelGGL(attn_blocks_kernel, dim3(a.max_blocks, kKvHeads, 1), dim3(256), 0, s, a);
+  rc = spk::check_launch(name);
+  if (rc) return rc;
+  FusedGemv g{};
+  g.kind = kInAttn;
+  g.in_dim = kQHeads * kHeadDim;
+  g.x = p->qg;
+  g.count = 1;
+  g.W[0] = o_proj->W;
+  g.y[0] = o_proj->y;
+  g.res[0] = o_proj->residual;
+  g.out_dim[0] = o_proj->out_dim;
+  const int blocks = (o_proj->out_dim + 3) / 4;  // R = 1 row per wave
+  for (int i = 1; i <= kLaunchOut; ++i) g.first_block[i] = blocks;
+  g.part = a.part;
+  g.max_blocks = a.max_blocks;
+  g.max_seq = a.max_seq;
+  g.pos_dev = p->pos_dev;
+  hipLaunchKernelGGL((fused_gemv_kernel<4, 1, false, kInAttn>), dim3(blocks), dim3(256), 0, s, g);
+  return spk::check_launch(name);
 }
 
 extern "C" int spk_attention_prefill(const SpkAttnArgs* p, int32_t pos0, int32_t tokens, spk_stream_t stream) {
@@ -1024,6 +1291,58 @@ extern "C" int spk_add_i32(int32_t* p, int32_t delta, spk_stream_t stream) {
   if (!p) return spk::fail(SPK_ERR_NULL, "spk_add_i32: NULL pointer");
   hipLaunchKernelGGL(add_i32_kernel, dim3(1), dim3(64), 0, spk::to_hip(stream), p, delta);
   return spk::check_launch("spk_add_i32");
+}
+
+extern "C" int spk_lm_head_argmax_key(const uint16_t* W, const uint16_t* x, const uint16_t* norm_w,
+                                      int32_t vocab, int32_t hidden, uint16_t* logits, uint64_t* key,
+                                      spk_stream_t stream) {
+  const char* name = "spk_lm_head_argmax_key";
+  if (!W || !x || !key) return spk::fail(SPK_ERR_NULL, "%s: NULL pointer", name);
+  if (vocab <= 0 || hidden <= 0 || hidden % 512 != 0 || hidden > 4096 || (norm_w && hidden != kHidden))
+    return spk::fail(SPK_ERR_SHAPE, "%s: vocab %d hidden %d (multiple of 512, <= 4096; 1024 with norm_w)", name,
+                     vocab, hidden);
+  if (!spk::aligned(W, 16) || !spk::aligned(x, 16) || !spk::aligned(key, 8) || (norm_w && !spk::aligned(norm_w, 8)))
+    return spk::fail(SPK_ERR_ALIGN, "%s: W/x must be 16-byte aligned, key and norm_w 8-byte", name);
+  constexpr int R = 8;
+  const uint32_t E = (uint32_t)((vocab + 255) / 256);
+  const int blocks = (vocab + 4 * R - 1) / (4 * R);
+  hipStream_t s = spk::to_hip(stream);
+  auto* k = reinterpret_cast<unsigned long long*>(key);
+  if (norm_w) {
+    hipLaunchKernelGGL((lm_head_key_kernel<2, R, true>), dim3(blocks), dim3(256), 0, s, W, x, norm_w, logits,
+                       vocab, E, k);
+    return spk::check_launch(name);
+  }
+#define SPK_LMK_CASE(n8)                                                                                      \
+  case n8:                                                                                                    \
+    hipLaunchKernelGGL((lm_head_key_kernel<n8, R, false>), dim3(blocks), dim3(256), 0, s, W, x, nullptr,   \
+                       logits, vocab, E, k);                                                                  \
+    break;
+  switch (hidden / 512) {
+    SPK_LMK_CASE(1)
+    SPK_LMK_CASE(2)
+    SPK_LMK_CASE(3)
+    SPK_LMK_CASE(4)
+    SPK_LMK_CASE(5)
+    SPK_LMK_CASE(6)
+    SPK_LMK_CASE(7)
+    SPK_LMK_CASE(8)
+    default:
+      return spk::fail(SPK_ERR_SHAPE, "%s: hidden %d", name, hidden);
+  }
+#undef SPK_LMK_CASE
+  return spk::check_launch(name);
+}
+
+extern "C" int spk_argmax_key_take(uint64_t* key, int32_t vocab, uint32_t* out_index, int32_t* pos,
+                                   int32_t* count, int32_t* history, int32_t capacity, spk_stream_t stream) {
+  if (!key || !out_index) return spk::fail(SPK_ERR_NULL, "spk_argmax_key_take: NULL pointer");
+  if (vocab <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_argmax_key_take: vocab %d", vocab);
+  if (pos && (!count || !history)) return spk::fail(SPK_ERR_NULL, "spk_argmax_key_take: count/history NULL with pos");
+  const uint32_t E = (uint32_t)((vocab + 255) / 256);
+  hipLaunchKernelGGL(argmax_take_kernel, dim3(1), dim3(64), 0, spk::to_hip(stream),
+                     reinterpret_cast<unsigned long long*>(key), E, out_index, pos, count, history, capacity);
+  return spk::check_launch("spk_argmax_key_take");
 }
 
 extern "C" int spk_record_token(const int32_t* token, int32_t* pos, int32_t* count, int32_t* history,

@@ -90,3 +90,58 @@ def test_argmax_tie_rule(dev, oracle, i):
     out = ops.argmax_f16(_t(dev, v.view(np.uint16)))
     torch.cuda.synchronize()
     assert int(out.cpu()[0]) == oracle.argmax_f16(v.view(np.uint16))
+
+
+def _key_path(dev, W, x, norm_w=None, logits=None):
+    """spk_lm_head_argmax_key + spk_argmax_key_take through the C ABI."""
+    from spock_amd import _lib
+    lib = _lib.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    vocab, hidden = W.shape
+    key = torch.zeros(64, dtype=torch.int64, device=dev)  # SPK_ARGMAX_KEY_WORDS
+    idx = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    rc = lib.spk_lm_head_argmax_key(W.data_ptr(), x.data_ptr(), None if norm_w is None else norm_w.data_ptr(),
+                                    vocab, hidden, None if logits is None else logits.data_ptr(), key.data_ptr(), s)
+    _lib.check(rc, "spk_lm_head_argmax_key")
+    _lib.check(lib.spk_argmax_key_take(key.data_ptr(), vocab, idx.data_ptr(), None, None, None, 0, s),
+               "spk_argmax_key_take")
+    torch.cuda.synchronize()
+    assert not key.cpu().numpy().any()  # the take leaves the key words at zero
+    return int(idx.cpu()[0])
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_lm_head_argmax_key_config3(dev, oracle, norm):
+    """Final norm + lm_head + argmax in one launch (device atomic max of the
+    argmax keys) against the oracle: bit-exact logits and index."""
+    import oracle_model
+    from spock_amd import synth
+    V, Hd = 248320, 1024
+    W = synth.gemv_weights(V, Hd, seed=41)
+    h = synth.gemv_input(Hd, seed=42)
+    x = h
+    nw = None
+    if norm:
+        nw = synth.f16(synth.normal(43, Hd, std=0.02))
+        x = np.empty(Hd, np.uint16)
+        oracle_model.lib().orc_rmsnorm1024(h.ctypes.data, nw.ctypes.data, x.ctypes.data)
+    e_idx, e_logits = oracle.lm_head_argmax(W, x)
+    logits = torch.empty(V, dtype=torch.float16, device=dev)
+    Wd = _t(dev, W)
+    got = _key_path(dev, Wd, _t(dev, h), None if nw is None else _t(dev, nw), logits)
+    assert np.array_equal(logits.cpu().numpy().view(np.uint16), e_logits)
+    assert got == e_idx
+    # again without logits (the key words were returned to zero by the take)
+    assert _key_path(dev, Wd, _t(dev, h), None if nw is None else _t(dev, nw)) == e_idx
+
+
+@pytest.mark.parametrize("vocab,hidden", [(1000, 512), (77777, 2048), (4096, 1024)])
+def test_lm_head_argmax_key_ties(dev, oracle, vocab, hidden):
+    """Rows repeated across the vocabulary make exact logit ties; the key path
+    keeps argmax.comp's tie rule (same index as the oracle)."""
+    from spock_amd import synth
+    base = synth.gemv_weights(37, hidden, seed=vocab)
+    W = np.ascontiguousarray(base[np.arange(vocab) % 37])
+    x = synth.gemv_input(hidden, seed=hidden)
+    e_idx, _ = oracle.lm_head_argmax(W, x)
+    assert _key_path(dev, _t(dev, W), _t(dev, x)) == e_idx

@@ -471,3 +471,39 @@ def test_gemv_silu_pair_bitexact(dev):
     exp = np.zeros(n, np.uint16)
     _om().orc_silu_gate(_p(g), _p(u), _p(exp), n)
     assert np.array_equal(_u16(y), exp)
+
+
+@pytest.mark.parametrize("pos", [0, 5, 64, 700, 1023, 1024, 2047, 2048, 3000, 4095])
+def test_attention_decode_oproj_equals_two_step(dev, pos):
+    """spk_attention_decode_oproj (blocks, then o_proj + residual with the
+    blocks' combine and sigmoid gate in its prologue) gives the bits of
+    spk_attention_decode followed by spk_gemv_fused over its output; past
+    1024 positions the prologue loads partials beyond its prefetch, past 2048
+    it runs more than one chunk of 32 blocks."""
+    from spock_amd import _lib
+    print(f"[attention decode + o_proj pos={pos}]", flush=True)
+    L = _lib.lib()
+    max_seq = 4096
+    rope, kv, qg, k, v, qn, kn = _attn_inputs(300 + pos, max_seq, pos)
+    Wo = _rand16(77, 1024 * 2048, 0.02)
+    res = _rand16(78, 1024)
+    dWo = _h(Wo, dev)
+    outs = []
+    for fused in (False, True):
+        a, d = _attn_args(dev, rope, kv, qg, k, v, qn, kn, max_seq, 1, max_seq)
+        dpos = torch.tensor([pos], dtype=torch.int32, device=dev)
+        a.pos_dev = dpos.data_ptr()
+        y = _h(res, dev)
+        o = _lib.SpkGemvOutput()
+        o.W, o.y, o.residual, o.out_dim, o.W_up = dWo.data_ptr(), y.data_ptr(), y.data_ptr(), 1024, None
+        if fused:
+            _lib.check(L.spk_attention_decode_oproj(C.byref(a), C.byref(o), _stream()), "spk_attention_decode_oproj")
+        else:
+            _lib.check(L.spk_attention_decode(C.byref(a), _stream()), "spk_attention_decode")
+            gi = _lib.SpkGemvInput()
+            gi.kind, gi.in_dim, gi.x = _lib.SPK_GEMV_IN_PLAIN, 2048, d["out"].data_ptr()
+            _lib.check(L.spk_gemv_fused(C.byref(gi), C.byref(o), 1, _stream()), "spk_gemv_fused")
+        torch.cuda.synchronize()
+        outs.append((_u16(y), _u16(d["kv"])))
+    assert np.array_equal(outs[1][1], outs[0][1])
+    assert np.array_equal(outs[1][0], outs[0][0])
