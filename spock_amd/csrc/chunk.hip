@@ -30,6 +30,8 @@
 // MFMA operand trick: the contraction index of a 16x16x4 step is a free
 // permutation, so lane (m = l%16, g = l/16) reads a float4 at k = 16u + 4g and
 // feeds its elements to 4 consecutive steps; the B operand uses the same map.
+#include <algorithm>
+
 #include "capi_common.hpp"
 #include "numerics.hpp"
 
@@ -69,6 +71,13 @@ __device__ __forceinline__ f4v mfma4(float a, float b, f4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Sequences of a launch: with up to kSelMax of them the host fills the
+// tables below from its copy of cu_seqlens, in the order the scan starts them
+// (longest first), so no workgroup searches cu_seqlens (measured: config 2
+// 1.01 -> 0.94 ms); with more (nsel == 0) the kernels find their sequence and
+// chunk from the device cu_seqlens.  Workspace records use the pack's global
+// chunk numbering.
+constexpr int kSelMax = 32;
 struct ChunkParams {
   int H;
   int N;
@@ -86,6 +95,12 @@ struct ChunkParams {
   float* state;
   const int* cu;
   float* ws;
+  int nsel;
+  int sel_seq[kSelMax];         // sequence index (row of initial/out state)
+  int sel_t0[kSelMax];          // its first token
+  int sel_len[kSelMax];         // its tokens
+  int sel_co[kSelMax];          // global index of its first chunk (workspace record)
+  int sel_chunk0[kSelMax + 1];  // prefix sums of chunks over the table (intra grid)
 };
 
 __device__ __forceinline__ float4 load4(const float* p, size_t i) {
@@ -299,10 +314,20 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   __shared__ __align__(16) float sBE[64];  // beta e^gcum ik
   __shared__ __align__(16) float sIK[64];  // inverse K norms (1 without L2 normalisation)
 
-  const int gchunk = blockIdx.x;
+  int gchunk = blockIdx.x;
   const int h = blockIdx.y;
   int seq, t0, len;
-  locate_chunk(p, gchunk, seq, t0, len);
+  if (p.nsel > 0) {  // local chunk id -> table entry (chunk prefix sums held in SGPRs)
+    int i = 0;
+    while (i + 1 < p.nsel && (int)blockIdx.x >= p.sel_chunk0[i + 1]) ++i;
+    const int c = blockIdx.x - p.sel_chunk0[i];
+    seq = p.sel_seq[i];
+    t0 = p.sel_t0[i] + c * kC;
+    len = min(kC, p.sel_len[i] - c * kC);
+    gchunk = p.sel_co[i] + c;
+  } else {
+    locate_chunk(p, gchunk, seq, t0, len);
+  }
   if (seq < 0) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -585,7 +610,7 @@ __global__ __launch_bounds__(256, 3) void chunk_state_kernel(ChunkParams p) {
   // (ids are dealt to the 8 XCDs round-robin) -- so they share one L2 for W,
   // Q, A and K^T.
   const int b = blockIdx.x;
-  const int groups = p.S * p.H;
+  const int groups = (p.nsel > 0 ? p.nsel : p.S) * p.H;
   int gi, tile;
   if ((groups & 7) == 0) {
     gi = (b >> 6) * 8 + (b & 7);
@@ -595,7 +620,8 @@ __global__ __launch_bounds__(256, 3) void chunk_state_kernel(ChunkParams p) {
     tile = b & 7;
   }
   const int h = gi % p.H;
-  const int seq = lpt_sequence(p, gi / p.H);
+  const int slot = gi / p.H;
+  const int seq = p.nsel > 0 ? p.sel_seq[slot] : lpt_sequence(p, slot);
   const int n0 = tile * 16;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -604,7 +630,11 @@ __global__ __launch_bounds__(256, 3) void chunk_state_kernel(ChunkParams p) {
   const int lg = lane >> 4;
 
   int t_begin = 0, L = p.N, co = 0;
-  if (p.cu) {
+  if (p.nsel > 0) {
+    t_begin = p.sel_t0[slot];
+    L = p.sel_len[slot];
+    co = p.sel_co[slot];
+  } else if (p.cu) {
     t_begin = p.cu[seq];
     L = p.cu[seq + 1] - t_begin;
     for (int s = 0; s < seq; ++s) co += (p.cu[s + 1] - p.cu[s] + kC - 1) / kC;
@@ -792,6 +822,42 @@ __global__ void last_to_fp16_kernel(const float* __restrict__ src, uint16_t* __r
 
 size_t ws_bytes_for(int H, long long chunks) { return (size_t)chunks * H * kWsStride * sizeof(float); }
 
+// ---- host side of the launches --------------------------------------------
+
+struct SeqEntry {
+  int seq, t0, len, chunks, co;
+};
+
+void fill_tables(ChunkParams& p, const SeqEntry* e, int n) {
+  p.nsel = n;
+  p.sel_chunk0[0] = 0;
+  for (int i = 0; i < n; ++i) {
+    p.sel_seq[i] = e[i].seq;
+    p.sel_t0[i] = e[i].t0;
+    p.sel_len[i] = e[i].len;
+    p.sel_co[i] = e[i].co;
+    p.sel_chunk0[i + 1] = p.sel_chunk0[i] + e[i].chunks;
+  }
+}
+
+int launch_intra(const ChunkParams& p, int chunks, bool f32, hipStream_t s) {
+  dim3 g((unsigned)chunks, (unsigned)p.H);
+  if (f32)
+    hipLaunchKernelGGL(chunk_intra_kernel<float>, g, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(chunk_intra_kernel<uint16_t>, g, dim3(256), 0, s, p);
+  return spk::check_launch("spk_chunk_prefill (intra)");
+}
+
+int launch_scan(const ChunkParams& p, int nseq, bool f32, hipStream_t s) {
+  dim3 g((unsigned)(kTiles * p.H * nseq));
+  if (f32)
+    hipLaunchKernelGGL(chunk_state_kernel<float>, g, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(chunk_state_kernel<uint16_t>, g, dim3(256), 0, s, p);
+  return spk::check_launch("spk_chunk_prefill (state)");
+}
+
 }  // namespace
 
 extern "C" size_t spk_chunk_prefill_workspace_size(int32_t num_heads, int32_t total_tokens,
@@ -855,22 +921,37 @@ extern "C" int spk_chunk_prefill(const SpkChunkArgs* a, spk_stream_t stream) {
   p.state = a->out_state;
   p.cu = a->cu_seqlens;
   p.ws = static_cast<float*>(a->workspace);
+  p.nsel = 0;
   hipStream_t s = spk::to_hip(stream);
-  if (chunks > 0) {
-    dim3 g1((unsigned)chunks, (unsigned)p.H);
-    if (a->input_dtype == SPK_F32)
-      hipLaunchKernelGGL(chunk_intra_kernel<float>, g1, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL(chunk_intra_kernel<uint16_t>, g1, dim3(256), 0, s, p);
-    const int rc = spk::check_launch("spk_chunk_prefill (intra)");
-    if (rc) return rc;
+  const bool f32 = a->input_dtype == SPK_F32;
+  if (!a->cu_seqlens || S > kSelMax) {  // one sequence, or more than the tables hold
+    if (chunks > 0) {
+      if (int rc = launch_intra(p, (int)chunks, f32, s)) return rc;
+    }
+    return launch_scan(p, S, f32, s);
   }
-  dim3 g2((unsigned)(kTiles * p.H * S));
-  if (a->input_dtype == SPK_F32)
-    hipLaunchKernelGGL(chunk_state_kernel<float>, g2, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL(chunk_state_kernel<uint16_t>, g2, dim3(256), 0, s, p);
-  return spk::check_launch("spk_chunk_prefill (state)");
+
+  // Sequences from the host copy of cu_seqlens, longest first (stable), in
+  // the kernels' tables.  (Splitting off the longest sequences so that their
+  // scan overlaps the others' intra work, on a second stream, measured slower
+  // for config 2 -- 1.08 vs 0.94 ms: the intra workgroups fill the CUs' LDS,
+  // so the early scan gets no slots until they drain.)
+  SeqEntry seqs[kSelMax];
+  {
+    int co = 0;
+    for (int i = 0; i < S; ++i) {
+      const int t0 = a->cu_seqlens_host[i], len = a->cu_seqlens_host[i + 1] - t0;
+      const int n = (len + kC - 1) / kC;
+      seqs[i] = {i, t0, len, n, co};
+      co += n;
+    }
+    std::stable_sort(seqs, seqs + S, [](const SeqEntry& x, const SeqEntry& y) { return x.len > y.len; });
+  }
+  fill_tables(p, seqs, S);
+  if (chunks > 0) {
+    if (int rc = launch_intra(p, p.sel_chunk0[p.nsel], f32, s)) return rc;
+  }
+  return launch_scan(p, p.nsel, f32, s);
 }
 
 extern "C" int spk_prefill_collect(const uint16_t* dn_qkv, const float* g_beta, float* q_out,
