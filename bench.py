@@ -125,7 +125,9 @@ def _stream():
     return torch.cuda.current_stream().cuda_stream
 
 
-def bench_prefill(steps, warmup):
+def bench_prefill(steps, warmup, before_timing=None):
+    """Config 2.  `before_timing`, if given, runs after the inputs are built
+    and immediately before the warm-up calls."""
     import torch
     from spock_amd import ops, synth
     dev = torch.device("cuda:0")
@@ -143,6 +145,8 @@ def bench_prefill(steps, warmup):
     cu_dev = torch.from_numpy(cu).to(dev)
     fn = lambda i: ops.chunk_prefill(q, k, v, g, beta, cu_seqlens=cu, out_core=core, out_state=state,
                                      workspace=ws, cu_seqlens_dev=cu_dev)
+    if before_timing is not None:
+        before_timing()
     wall, ms = timed_launches(fn, steps, warmup)
     chunks = int(sum(math.ceil(L / C) for L in lens))
     flops = chunks * H * FLOP_PER_HEAD_CHUNK
@@ -583,7 +587,19 @@ def main():
         print(json.dumps({"only": args.only, "result": r}, default=float), flush=True)
         return
 
-    pre = bench_prefill(args.steps, args.warmup)
+    # The ceilings leg (~70 ms of MFMA and HBM streaming) runs after the
+    # headline's inputs are built and right before its warm-up calls.  After
+    # the seconds of GPU idle that building the inputs takes, the GPU needs
+    # ~30 ms of work to return to its sustained clocks: with only the five
+    # warm-up calls in front, the timed calls run ~8% slower (same box: 1.02
+    # vs 0.94 ms per call), whatever ran before the idle period.
+    ceilings = {}
+
+    def run_ceilings():
+        ceilings.update(bench_ceilings(args.steps, args.warmup))
+        log(f"[bench] measured ceilings {ceilings}")
+
+    pre = bench_prefill(args.steps, args.warmup, before_timing=run_ceilings)
     value = pre["tokens"] * args.steps / pre["wall_s"]
     log(f"[bench] prefill {value:,.0f} tok/s, {pre['launch_ms']:.3f} ms per call, "
         f"{pre['roofline']['achieved']} TFLOP/s")
@@ -602,8 +618,7 @@ def main():
         log(f"[bench] lm_head {secondary['lm_head_argmax']}")
         secondary["config4_full_model"] = bench_model(args.steps, args.warmup, cpu=not args.no_cpu_baseline)
         log(f"[bench] full model {secondary['config4_full_model']}")
-        secondary["measured_ceilings"] = bench_ceilings(args.steps, args.warmup)
-        log(f"[bench] measured ceilings {secondary['measured_ceilings']}")
+        secondary["measured_ceilings"] = ceilings
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log(f"[bench] cpu baseline {cpu}")
@@ -627,7 +642,9 @@ def main():
                                "8 seqs L~U[512,8192] (seed 2024), H=16, dk=dv=128, C=64, "
                                "fp16 q/k/v in, fp32 compute and state",
                    "tokens": pre["tokens"], "lengths": pre["lengths"], "head_chunks": pre["head_chunks"],
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU",
+                   "timed_after": "inputs built, then the measured-ceilings leg (~70 ms of MFMA + HBM "
+                                  "work), then the warm-up calls: the timed calls run at sustained clocks"},
         "roofline": pre["roofline"],
         "cpu_baseline": cpu,
         "secondary": secondary,

@@ -457,33 +457,65 @@ struct AttnArgs {
 constexpr int kKLd = kHeadDim + 8;
 
 // One query-head wave over one block of positions [64b, 64b+64) of npos valid
-// ones, operands staged in LDS (K as Ks[p][d], V as Vs[p][d], q as fp16-rounded
-// floats): writes m_b, S_b, O_b.  Lane = position for the scores: each lane
-// reads its K row 8 dims at a time (ds_read_b128) and runs the d = 0..255 fma
-// chain; the weighted V sum visits positions j = 0..nvalid-1 in order, taking
-// w_j by readlane and prefetching 8 V rows at a time.
-__device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t (*Ks)[kKLd],
+// ones, operands staged in LDS (K as Ks[p][d], V as Vs[p][d], q as fp16: its
+// values are fp16-rounded, so this is exact): writes m_b, S_b, O_b.  Lane =
+// position for the scores: each lane reads its K row 8 dims at a time
+// (ds_read_b128) and runs the d = 0..255 fma chain, the reads one 32-dim stage
+// ahead of the chain; the weighted
+// V sum visits positions j = 0..nvalid-1 in order, taking w_j by readlane,
+// in whole groups of 8 positions with no per-position branch (the next
+// group's V rows are read while the current one accumulates), then the
+// block's last partial group.
+__device__ __forceinline__ void v_group(const uint2 (&vv)[8], int wbits, int j0, int n, float (&acc)[4]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i < n) {
+      const float wj = __int_as_float(__builtin_amdgcn_readlane(wbits, j0 + i));
+      const float vf[4] = {spk::h2f(vv[i].x & 0xffffu), spk::h2f(vv[i].x >> 16), spk::h2f(vv[i].y & 0xffffu),
+                           spk::h2f(vv[i].y >> 16)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(wj, vf[e], acc[e]);
+    }
+  }
+}
+
+__device__ __forceinline__ void attn_block_wave(const uint16_t* qs, const uint16_t (*Ks)[kKLd],
                                                 const uint16_t (*Vs)[kHeadDim], int b, int npos, int lane,
                                                 float* part) {
   const int p = kAttnBlock * b + lane;
   float sc = -INFINITY;
   if (p < npos) {
+    // 8 stages of 32 dims; stage s+1's K and q pieces are read while stage s
+    // runs its 32 chained fmas
     float dot = 0.0f;
-#pragma unroll 4
-    for (int d8 = 0; d8 < kHeadDim / 8; ++d8) {
-      const uint4 kk = *reinterpret_cast<const uint4*>(&Ks[lane][8 * d8]);
-      const float4 q0 = *reinterpret_cast<const float4*>(&qs[8 * d8]);
-      const float4 q1 = *reinterpret_cast<const float4*>(&qs[8 * d8 + 4]);
-      float kf[8];
-      unpack8(kk, kf);
-      dot = __builtin_fmaf(q0.x, kf[0], dot);
-      dot = __builtin_fmaf(q0.y, kf[1], dot);
-      dot = __builtin_fmaf(q0.z, kf[2], dot);
-      dot = __builtin_fmaf(q0.w, kf[3], dot);
-      dot = __builtin_fmaf(q1.x, kf[4], dot);
-      dot = __builtin_fmaf(q1.y, kf[5], dot);
-      dot = __builtin_fmaf(q1.z, kf[6], dot);
-      dot = __builtin_fmaf(q1.w, kf[7], dot);
+    uint4 kc[4], qc[4], kn[4], qn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kc[i] = *reinterpret_cast<const uint4*>(&Ks[lane][8 * i]);
+      qc[i] = *reinterpret_cast<const uint4*>(&qs[8 * i]);
+    }
+#pragma unroll
+    for (int st = 0; st < kHeadDim / 32; ++st) {
+      if (st + 1 < kHeadDim / 32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kn[i] = *reinterpret_cast<const uint4*>(&Ks[lane][32 * (st + 1) + 8 * i]);
+          qn[i] = *reinterpret_cast<const uint4*>(&qs[32 * (st + 1) + 8 * i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float kf[8], qf[8];
+        unpack8(kc[i], kf);
+        unpack8(qc[i], qf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(qf[e], kf[e], dot);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kc[i] = kn[i];
+        qc[i] = qn[i];
+      }
     }
     sc = dot * 0.0625f;
   }
@@ -494,22 +526,20 @@ __device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t 
   const float S = spk::tree64_to_lane0(w);
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int nvalid = min(kAttnBlock, npos - kAttnBlock * b);
+  const int nfull = nvalid & ~7;
   const int wbits = __float_as_int(w);
-  for (int j0 = 0; j0 < nvalid; j0 += 8) {
-    uint2 vv[8];
+  uint2 cur[8], nxt[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vv[i] = *reinterpret_cast<const uint2*>(&Vs[j0 + i][4 * lane]);
+  for (int i = 0; i < 8; ++i) cur[i] = *reinterpret_cast<const uint2*>(&Vs[i][4 * lane]);
+  for (int j0 = 0; j0 < nfull; j0 += 8) {
+    const int jn = min(j0 + 8, kAttnBlock - 8);  // rows of the next group (in bounds)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (j0 + i < nvalid) {
-        const float wj = __int_as_float(__builtin_amdgcn_readlane(wbits, j0 + i));
-        const float vf[4] = {spk::h2f(vv[i].x & 0xffffu), spk::h2f(vv[i].x >> 16), spk::h2f(vv[i].y & 0xffffu),
-                             spk::h2f(vv[i].y >> 16)};
+    for (int i = 0; i < 8; ++i) nxt[i] = *reinterpret_cast<const uint2*>(&Vs[jn + i][4 * lane]);
+    v_group(cur, wbits, j0, 8, acc);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(wj, vf[e], acc[e]);
-      }
-    }
+    for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
   }
+  if (nfull < nvalid) v_group(cur, wbits, nfull, nvalid - nfull, acc);  // cur holds rows nfull..nfull+7
   if (lane == 0) {
     part[0] = m;
     part[1] = S;
@@ -519,7 +549,7 @@ __device__ __forceinline__ void attn_block_wave(const float* qs, const uint16_t 
 
 // grid (max_blocks, kv_heads, T); block 256.
 __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
-  __shared__ __align__(16) float qs[4][kHeadDim];
+  __shared__ __align__(16) uint16_t qs[4][kHeadDim];  // fp16-rounded q, stored exactly as fp16
   __shared__ __align__(16) uint16_t Ks[kAttnBlock][kKLd];
   __shared__ __align__(16) uint16_t Vs[kAttnBlock][kHeadDim];
   const int b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
@@ -559,7 +589,7 @@ __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the q work below
   head_norm_wave(qv, qw);
   rope_wave(qv, c8, lane);
-  *reinterpret_cast<float4*>(&qs[wave][4 * lane]) = make_float4(qv[0], qv[1], qv[2], qv[3]);
+  *reinterpret_cast<uint2*>(&qs[wave][4 * lane]) = pack4h(qv);
   if (newrow) {  // new K row: norm + rope; V row as projected
     float nk[4] = {spk::h2f(nk16.x & 0xffffu), spk::h2f(nk16.x >> 16), spk::h2f(nk16.y & 0xffffu),
                    spk::h2f(nk16.y >> 16)};
