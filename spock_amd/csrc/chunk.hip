@@ -31,6 +31,7 @@
 // permutation, so lane (m = l%16, g = l/16) reads a float4 at k = 16u + 4g and
 // feeds its elements to 4 consecutive steps; the B operand uses the same map.
 #include <algorithm>
+#include <type_traits>
 
 #include "capi_common.hpp"
 #include "numerics.hpp"
@@ -265,7 +266,7 @@ __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, 
 template <int W>
 __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG, const float* sB,
                                            const float* sIK, float iq_scale, float* sL, float* ws,
-                                           int li, int lg, int lane) {
+                                           int li, int lg, int lane, bool store_a) {
   constexpr int Ik = 3 - W;
 #pragma unroll
   for (int t = 0; t < 5; ++t) {
@@ -290,18 +291,31 @@ __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG,
         const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
         o[r] = (j <= i) ? (acc[t][r] * (iq_scale * sIK[j])) * dec : 0.0f;
       }
-      *reinterpret_cast<float4*>(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4) = make_float4(o[0], o[1], o[2], o[3]);
+      if (store_a)
+        *reinterpret_cast<float4*>(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4) = make_float4(o[0], o[1], o[2], o[3]);
     }
   }
   // blocks above the diagonal of this query block are zero
+  if (store_a) {
 #pragma unroll
-  for (int J = W + 1; J < 4; ++J)
-    *reinterpret_cast<float4*>(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int J = W + 1; J < 4; ++J)
+      *reinterpret_cast<float4*>(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
 }
 
 // fp16 inputs: 3 workgroups per CU (50 KB of LDS each), so at most 168 VGPRs;
 // fp32 inputs stage 83 KB and run one workgroup per CU.
-template <typename TIn>
+//
+// PARTS workgroups per (chunk, head) (blockIdx.z = part), for launches with
+// too few (chunk, head) pairs to fill the chip: every part loads the chunk,
+// forms the Gram tiles and T (the serial part), then computes and stores only
+// its share of the record: U / W column tiles 2*part, 2*part+1 (PARTS 4; its
+// four wavefronts split the two tiles' row blocks as {0,3} / {1,2}, 40 MFMA
+// each instead of 160) or 4*part..4*part+3 (PARTS 2), and the A, raw Q and K^T
+// blocks of the wavefronts w with w % PARTS == part.  Each value is computed
+// by the same operation sequence whatever PARTS is, so the record is
+// bit-identical.
+template <typename TIn, int PARTS>
 __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_kernel(ChunkParams p) {
   typedef RawOf<TIn> R;
   typedef RowStage<TIn> RS;
@@ -329,11 +343,13 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
     locate_chunk(p, gchunk, seq, t0, len);
   }
   if (seq < 0) return;
+  const int part = PARTS > 1 ? (int)blockIdx.z : 0;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int li = lane & 15;
   const int lg = lane >> 4;
+  const bool own_block = (wave % PARTS) == part;  // this wave's A / raw Q / K^T block
   const TIn* q = static_cast<const TIn*>(p.q);
   const TIn* k = static_cast<const TIn*>(p.k);
   const TIn* v = static_cast<const TIn*>(p.v);
@@ -389,7 +405,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   __syncthreads();
 
   // ---- raw Q rows of block `wave` in the scan's fragment order
-  {
+  if (own_block) {
     typename RS::T* qf = reinterpret_cast<typename RS::T*>(ws + kWsQ);
 #pragma unroll
     for (int u = 0; u < 8; ++u) RS::store_raw4(qf + ((wave * 8 + u) * 64 + lane) * 4, qa[u]);
@@ -435,19 +451,19 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   // ---- epilogue: L into LDS, A into the workspace; per-token scales
   const float iq_scale = iq * p.q_scale;  // lane li of any group: row 16*wave + li
   switch (wave) {
-    case 0: gram_store<0>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane); break;
-    case 1: gram_store<1>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane); break;
-    case 2: gram_store<2>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane); break;
-    default: gram_store<3>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane); break;
+    case 0: gram_store<0>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane, own_block); break;
+    case 1: gram_store<1>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane, own_block); break;
+    case 2: gram_store<2>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane, own_block); break;
+    default: gram_store<3>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane, own_block); break;
   }
   const float gL = sG[63];
-  if (lg == 0) ws[kWsQs + 16 * wave + li] = iq_scale * expf(sG[16 * wave + li]);  // the scan re-reads Q raw
+  if (lg == 0 && own_block) ws[kWsQs + 16 * wave + li] = iq_scale * expf(sG[16 * wave + li]);  // the scan re-reads Q raw
   if (tid < 64) {
     const float eg = expf(sG[tid]);
     sBE[tid] = sB[tid] * eg * sIK[tid];
-    ws[kWsKs + tid] = expf(gL - sG[tid]) * sIK[tid];
+    if (part == 0) ws[kWsKs + tid] = expf(gL - sG[tid]) * sIK[tid];
   }
-  if (tid == 0) ws[kWsMisc] = expf(gL);
+  if (tid == 0 && part == 0) ws[kWsMisc] = expf(gL);
   __syncthreads();
 
   // ---- diagonal blocks of T by forward substitution, lane j < 16 of wave w
@@ -493,18 +509,24 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   }
 
   // ---- U = T diag(beta) V and W^T = K^T diag(beta e^g ik) T^T, row blocks
-  // I = 0..3 of two 16-column tiles per wavefront accumulated together; the
-  // per-token factors are applied to the V / K operand as it is read.  W is
-  // produced transposed so that each lane holds four consecutive key dims of
-  // one token: the A-operand fragment of the state scan.
+  // I = 0..3 of 16-column tiles (two per wavefront without a split),
+  // accumulated together; the per-token factors are applied to the V / K
+  // operand as it is read.  W is produced transposed so that each lane holds
+  // four consecutive key dims of one token: the A-operand fragment of the
+  // state scan.
+  constexpr int kTilesPerWave = PARTS == 1 ? 2 : 1;
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    const int n = 16 * (2 * wave + jj) + li;
+  for (int jj = 0; jj < kTilesPerWave; ++jj) {
+    const int ct = PARTS == 1 ? 2 * wave + jj : PARTS == 2 ? 4 * part + wave : 2 * part + (wave & 1);
+    const unsigned imask = PARTS == 4 ? ((wave >> 1) ? 0x6u : 0x9u) : 0xFu;  // row blocks I of this wave
+    const int umax = PARTS == 4 ? ((wave >> 1) ? 2 : 3) : 3;
+    const int n = 16 * ct + li;
     f4v au[4], aw[4];
 #pragma unroll
     for (int I = 0; I < 4; ++I) au[I] = aw[I] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
+      if (u > umax) break;
       const int t = 16 * u + 4 * lg;
       const float4 bb = *reinterpret_cast<const float4*>(&sB[t]);
       const float4 be = *reinterpret_cast<const float4*>(&sBE[t]);
@@ -516,6 +538,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
       }
 #pragma unroll
       for (int I = u; I < 4; ++I) {
+        if (!((imask >> I) & 1u)) continue;
         const float* tp = (I == u) ? sL + blk(I, I) : sT + offblk(I, u);
         const float4 a4 = *reinterpret_cast<const float4*>(&tp[li * 16 + 4 * lg]);
 #pragma unroll
@@ -525,10 +548,10 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
         }
       }
     }
-    // U: lane (li, lg) holds U[16I+4lg+r][n]; W^T: W[16I+li][16(2w+jj)+4lg+r]
-    const int ct = 2 * wave + jj;
+    // U: lane (li, lg) holds U[16I+4lg+r][n]; W^T: W[16I+li][16 ct+4lg+r]
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
+      if (!((imask >> I) & 1u)) continue;
       *reinterpret_cast<float4*>(ws + kWsU + ((ct * 4 + I) * 64 + lane) * 4) = make_float4(au[I][0], au[I][1], au[I][2], au[I][3]);
       *reinterpret_cast<float4*>(ws + kWsW + ((I * 8 + ct) * 64 + lane) * 4) = make_float4(aw[I][0], aw[I][1], aw[I][2], aw[I][3]);
     }
@@ -540,6 +563,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   typename RS::T* kt = reinterpret_cast<typename RS::T*>(ws + kWsKT);
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
+    if (((it >> 1) % PARTS) != part) continue;  // fragment block M = it / 2
     const int f = tid + 256 * it;  // [M][v][lane]
     const int l = f & 63;
     const int v8 = (f >> 6) & 7;
@@ -591,11 +615,17 @@ struct ScanLate {
 //   C  o = qs (Q S) + A v_new -> core
 //   D  S rows 32M..32M+31 <- e^{gL} S + K^T diag(Ks) v_new
 // 112 MFMA per wavefront per chunk.
-// Three workgroups per CU (168 VGPRs; the fp16 instance spills a few): more
-// resident wavefronts measured faster than two workgroups holding both operand
-// sets double-buffered.
-template <typename TIn>
-__global__ __launch_bounds__(256, 3) void chunk_state_kernel(ChunkParams p) {
+// MINB workgroups per CU.  fp16 inputs, large launches: three (168 VGPRs;
+// the instance spills a few): more resident wavefronts measured faster than
+// two workgroups holding both operand sets double-buffered.  fp32 inputs hold
+// twice the Q and K^T operand registers: at 168 VGPRs they spilled 236 bytes
+// per lane inside the chunk loop (6.5-9 us per chunk step against 3.1 for
+// fp16), so they run two workgroups per CU without spilling, as do small
+// fp16 launches.
+// ZERO_INIT (no initial state): S is zero entering each sequence's first
+// chunk, so that chunk's W S and Q S are exactly zero and stage A is skipped.
+template <typename TIn, bool ZERO_INIT, int MINB>
+__global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   typedef RawOf<TIn> R;
   // S tile and v_new stored transposed ([column][contraction index]) so one
   // ds_read_b128 feeds four consecutive MFMA steps; strides 132 and 68 keep
@@ -676,32 +706,35 @@ __global__ __launch_bounds__(256, 3) void chunk_state_kernel(ChunkParams p) {
     l.gle = ws[kWsMisc];
   };
 
-  auto step = [&](const ScanEarly& e, const ScanLate& l, int c) {
+  // zero_s: S is zero (first chunk without an initial state)
+  auto step = [&](const ScanEarly& e, const ScanLate& l, int c, auto zero_s) {
     const int tok0 = t_begin + c * kC;
     const int len = min(kC, L - c * kC);
 
     // ---- stage A: W_M S and Q_M S share the B operand (S); the per-row Q
     // scale is applied to the product
     f4v aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (!decltype(zero_s)::value) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float4 sb = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * u + 4 * lg]);
-      const float4 x = R::cvt4(e.q[u]);
+      for (int u = 0; u < 8; ++u) {
+        const float4 sb = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * u + 4 * lg]);
+        const float4 x = R::cvt4(e.q[u]);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        aw = mfma4(elem(e.w[u], k), elem(sb, k), aw);
-        aq = mfma4(elem(x, k), elem(sb, k), aq);
+        for (int k = 0; k < 4; ++k) {
+          aw = mfma4(elem(e.w[u], k), elem(sb, k), aw);
+          aq = mfma4(elem(x, k), elem(sb, k), aq);
+        }
       }
-    }
-    // The loads issued just before this stage (same scheduling region) are
-    // spread over the MFMA stream rather than issued as one burst, which
-    // would queue in the CU's vector-memory pipe behind the other
-    // wavefronts' bursts.  (sched_group_barrier masks: 0x020 VMEM read,
-    // 0x008 MFMA.)
+      // The loads issued just before this stage (same scheduling region) are
+      // spread over the MFMA stream rather than issued as one burst, which
+      // would queue in the CU's vector-memory pipe behind the other
+      // wavefronts' bursts.  (sched_group_barrier masks: 0x020 VMEM read,
+      // 0x008 MFMA.)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      }
     }
 
     // ---- stage B: v_new = U - W S, and v_new scaled by Ks for the update
@@ -772,19 +805,40 @@ __global__ __launch_bounds__(256, 3) void chunk_state_kernel(ChunkParams p) {
 
   // Stage-A operands double-buffered (the loads of chunk c+1 are in flight
   // while chunk c computes); stage B-D operands of chunk c are loaded at the
-  // start of its own step and arrive during stage A.
+  // start of its own step and arrive during stage A.  ZERO_INIT peels the
+  // first chunk to drop its stage A at compile time (a run-time flag, or the
+  // peeled loop for every launch, made the fp16 instance spill more).
+  using NZ = std::integral_constant<bool, false>;
   ScanEarly ea, eb;
   ScanLate lt;
-  if (nchunks > 0) load_early(ea, 0);
-  __syncthreads();
-  for (int c = 0; c < nchunks; c += 2) {
-    load_late(lt, c);
-    load_early(eb, min(c + 1, nchunks - 1));
-    step(ea, lt, c);
-    if (c + 1 >= nchunks) break;
-    load_late(lt, c + 1);
-    load_early(ea, min(c + 2, nchunks - 1));
-    step(eb, lt, c + 1);
+  if constexpr (ZERO_INIT) {
+    __syncthreads();
+    if (nchunks > 0) {
+      load_late(lt, 0);
+      load_early(eb, min(1, nchunks - 1));
+      step(ea, lt, 0, std::integral_constant<bool, true>{});
+    }
+    for (int c = 1; c < nchunks; c += 2) {
+      load_late(lt, c);
+      load_early(ea, min(c + 1, nchunks - 1));
+      step(eb, lt, c, NZ{});
+      if (c + 1 >= nchunks) break;
+      load_late(lt, c + 1);
+      load_early(eb, min(c + 2, nchunks - 1));
+      step(ea, lt, c + 1, NZ{});
+    }
+  } else {
+    if (nchunks > 0) load_early(ea, 0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; c += 2) {
+      load_late(lt, c);
+      load_early(eb, min(c + 1, nchunks - 1));
+      step(ea, lt, c, NZ{});
+      if (c + 1 >= nchunks) break;
+      load_late(lt, c + 1);
+      load_early(ea, min(c + 2, nchunks - 1));
+      step(eb, lt, c + 1, NZ{});
+    }
   }
 
   float* outs = p.state + ((size_t)seq * p.H + h) * kD * kD;
@@ -840,21 +894,56 @@ void fill_tables(ChunkParams& p, const SeqEntry* e, int n) {
   }
 }
 
-int launch_intra(const ChunkParams& p, int chunks, bool f32, hipStream_t s) {
-  dim3 g((unsigned)chunks, (unsigned)p.H);
-  if (f32)
-    hipLaunchKernelGGL(chunk_intra_kernel<float>, g, dim3(256), 0, s, p);
+// Workgroups per (chunk, head): split while the split launch still has at
+// most one workgroup per CU (256 CUs).  Past that the parts' repeated Gram
+// and T work costs more than the split saves (fp16, 8 chunks x 16 heads: 4
+// parts 23.9 us, 1 part 20.2 us).
+int intra_parts(long long pairs) {
+  if (pairs * 4 <= 256) return 4;
+  if (pairs * 2 <= 256) return 2;
+  return 1;
+}
+
+template <typename TIn>
+void launch_intra_t(const ChunkParams& p, int chunks, int parts, hipStream_t s) {
+  dim3 g((unsigned)chunks, (unsigned)p.H, (unsigned)parts);
+  if (parts == 4)
+    hipLaunchKernelGGL((chunk_intra_kernel<TIn, 4>), g, dim3(256), 0, s, p);
+  else if (parts == 2)
+    hipLaunchKernelGGL((chunk_intra_kernel<TIn, 2>), g, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(chunk_intra_kernel<uint16_t>, g, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((chunk_intra_kernel<TIn, 1>), g, dim3(256), 0, s, p);
+}
+
+int launch_intra(const ChunkParams& p, int chunks, bool f32, hipStream_t s) {
+  const int parts = intra_parts((long long)chunks * p.H);
+  if (f32)
+    launch_intra_t<float>(p, chunks, parts, s);
+  else
+    launch_intra_t<uint16_t>(p, chunks, parts, s);
   return spk::check_launch("spk_chunk_prefill (intra)");
 }
 
 int launch_scan(const ChunkParams& p, int nseq, bool f32, hipStream_t s) {
   dim3 g((unsigned)(kTiles * p.H * nseq));
-  if (f32)
-    hipLaunchKernelGGL(chunk_state_kernel<float>, g, dim3(256), 0, s, p);
+  // Three fp16 workgroups per CU (168 VGPRs, a 56-byte spill) only when the
+  // launch has that many workgroups to keep resident; otherwise two per CU
+  // without spilling, with the first-chunk skip when there is no initial
+  // state (that instance's peeled loop spilled more at 168 VGPRs).  Measured,
+  // fp16, 16 heads: one 104-token sequence 9.0 -> 8.0 us; config 2 (1024
+  // workgroups) unchanged either way within noise, so it keeps the old path.
+  const bool z = p.init == nullptr;
+  const bool big = g.x > 2u * 256u;
+  if (f32 && z)
+    hipLaunchKernelGGL((chunk_state_kernel<float, true, 2>), g, dim3(256), 0, s, p);
+  else if (f32)
+    hipLaunchKernelGGL((chunk_state_kernel<float, false, 2>), g, dim3(256), 0, s, p);
+  else if (big)
+    hipLaunchKernelGGL((chunk_state_kernel<uint16_t, false, 3>), g, dim3(256), 0, s, p);
+  else if (z)
+    hipLaunchKernelGGL((chunk_state_kernel<uint16_t, true, 2>), g, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(chunk_state_kernel<uint16_t>, g, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((chunk_state_kernel<uint16_t, false, 2>), g, dim3(256), 0, s, p);
   return spk::check_launch("spk_chunk_prefill (state)");
 }
 
