@@ -40,6 +40,20 @@ namespace {
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+// Workspace record stores are non-temporal: the record is read back by the
+// scan (a later launch, mostly on other XCDs), so keeping it dirty in the
+// writer's L2 only adds to the end-of-launch write-back (config 2: 0.956 ->
+// 0.949 ms per call).
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void ws_store(float* p, float a, float b, float c, float d) {
+  const f4v v = {a, b, c, d};
+  __builtin_nontemporal_store(v, reinterpret_cast<f4v*>(p));
+}
+__device__ __forceinline__ void ws_store(void* p, uint32_t a, uint32_t b) {
+  const u32x2v v = {a, b};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x2v*>(p));
+}
+
 constexpr int kC = 64;
 constexpr int kD = 128;
 // Workspace record per (chunk, head), in floats.  The matrices are stored in
@@ -50,16 +64,17 @@ constexpr int kD = 128;
 // pipe several times more per byte.  Lane l = 16*lg + li.
 //   W   [M 4][u 8][lane][4]   W[16M+li][16u+4lg+e]                 fp32
 //   U   [tile 8][M 4][lane][4] U[16M+4lg+e][16 tile+li]             fp32
-//   A   [M 4][J 4][lane][4]   A[16M+li][16J+4lg+e] (0 above diag)  fp32
+//   A   [M 4][J 4][lane][4]   A[16M+li][16J+4lg+e], blocks J <= M   fp32
 //   KT  [M 4][v 8][lane][4]   K[16(v%4)+4lg+e][32M+16(v/4)+li]     input type
-//   Q   [M 4][u 8][lane][4]   Q[16M+li][16u+4lg+e] (raw)            input type
 //   Qs  [64] Q scale (q_scale iq e^gcum)   Ks [64] e^{gL - gcum} ik
 //   Misc[0] e^{gL}
+// A's blocks above the diagonal (zero) are neither stored nor multiplied, and
+// the scan reads raw Q from the input rows rather than from a record copy:
+// 22 of the record's ~115 KB (fp16 inputs) less for the intra kernel to write.
 constexpr int kWsW = 0;
 constexpr int kWsU = 8192;
 constexpr int kWsA = 16384;
 constexpr int kWsKT = 20480;
-constexpr int kWsQ = 28672;
 constexpr int kWsQs = 36864;
 constexpr int kWsKs = 36928;
 constexpr int kWsMisc = 36992;
@@ -184,14 +199,11 @@ template <> struct RowStage<uint16_t> {
                        spk::h2f((uint16_t)(u.y & 0xffffu)), spk::h2f((uint16_t)(u.y >> 16)));
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return spk::h2f(s[r * kLd + c]); }
-  static __device__ __forceinline__ void store_raw4(T* dst, const float4& raw) {
-    *reinterpret_cast<uint2*>(dst) = make_uint2(__float_as_uint(raw.x), __float_as_uint(raw.y));
-  }
   // rows r..r+3 of column c, stored as 4 consecutive elements at dst
   static __device__ __forceinline__ void col4_to(const T* s, int r, int c, T* dst) {
     const uint32_t a = s[r * kLd + c], b = s[(r + 1) * kLd + c];
     const uint32_t x = s[(r + 2) * kLd + c], y = s[(r + 3) * kLd + c];
-    *reinterpret_cast<uint2*>(dst) = make_uint2(a | (b << 16), x | (y << 16));
+    ws_store(dst, a | (b << 16), x | (y << 16));
   }
 };
 template <> struct RowStage<float> {
@@ -204,12 +216,8 @@ template <> struct RowStage<float> {
     return *reinterpret_cast<const float4*>(s + r * kLd + c);
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return s[r * kLd + c]; }
-  static __device__ __forceinline__ void store_raw4(T* dst, const float4& raw) {
-    *reinterpret_cast<float4*>(dst) = raw;
-  }
   static __device__ __forceinline__ void col4_to(const T* s, int r, int c, T* dst) {
-    *reinterpret_cast<float4*>(dst) =
-        make_float4(s[r * kLd + c], s[(r + 1) * kLd + c], s[(r + 2) * kLd + c], s[(r + 3) * kLd + c]);
+    ws_store(dst, s[r * kLd + c], s[(r + 1) * kLd + c], s[(r + 2) * kLd + c], s[(r + 3) * kLd + c]);
   }
 };
 
@@ -292,14 +300,8 @@ __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG,
         o[r] = (j <= i) ? (acc[t][r] * (iq_scale * sIK[j])) * dec : 0.0f;
       }
       if (store_a)
-        *reinterpret_cast<float4*>(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4) = make_float4(o[0], o[1], o[2], o[3]);
+        ws_store(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4, o[0], o[1], o[2], o[3]);
     }
-  }
-  // blocks above the diagonal of this query block are zero
-  if (store_a) {
-#pragma unroll
-    for (int J = W + 1; J < 4; ++J)
-      *reinterpret_cast<float4*>(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
 
@@ -403,13 +405,6 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
     RS::put4(sV, r, c4, vx);
   }
   __syncthreads();
-
-  // ---- raw Q rows of block `wave` in the scan's fragment order
-  if (own_block) {
-    typename RS::T* qf = reinterpret_cast<typename RS::T*>(ws + kWsQ);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) RS::store_raw4(qf + ((wave * 8 + u) * 64 + lane) * 4, qa[u]);
-  }
 
   // ---- inverse L2 norms (eps inside the sqrt, deltanet_chunk.cpp:27-39):
   // K rows from LDS, 4 threads per row; Q rows from this lane's registers
@@ -552,8 +547,8 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       if (!((imask >> I) & 1u)) continue;
-      *reinterpret_cast<float4*>(ws + kWsU + ((ct * 4 + I) * 64 + lane) * 4) = make_float4(au[I][0], au[I][1], au[I][2], au[I][3]);
-      *reinterpret_cast<float4*>(ws + kWsW + ((I * 8 + ct) * 64 + lane) * 4) = make_float4(aw[I][0], aw[I][1], aw[I][2], aw[I][3]);
+      ws_store(ws + kWsU + ((ct * 4 + I) * 64 + lane) * 4, au[I][0], au[I][1], au[I][2], au[I][3]);
+      ws_store(ws + kWsW + ((I * 8 + ct) * 64 + lane) * 4, aw[I][0], aw[I][1], aw[I][2], aw[I][3]);
     }
     __builtin_amdgcn_sched_barrier(0);  // one column tile's operands live at a time
   }
@@ -614,7 +609,7 @@ struct ScanLate {
 //   B  v_new = U - W S  -> LDS, also scaled by Ks
 //   C  o = qs (Q S) + A v_new -> core
 //   D  S rows 32M..32M+31 <- e^{gL} S + K^T diag(Ks) v_new
-// 112 MFMA per wavefront per chunk.
+// 100-112 MFMA per wavefront per chunk (stage C: 4 (M+1)).
 // MINB workgroups per CU.  fp16 inputs, large launches: three (168 VGPRs;
 // the instance spills a few): more resident wavefronts measured faster than
 // two workgroups holding both operand sets double-buffered.  fp32 inputs hold
@@ -683,13 +678,17 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   // rather than guarded), so the compiler's vmcnt bookkeeping stays exact.
   // Each load instruction reads one contiguous fragment.
   auto record = [&](int c) { return p.ws + ((size_t)(co + c) * p.H + h) * kWsStride; };
+  // raw Q row 16M+li of chunk c from the input (padding rows read the
+  // chunk's row 0, as the intra kernel's Q operand does; qs zeroes them)
+  const TIn* qin = static_cast<const TIn*>(p.q) + ((size_t)h * p.N + t_begin) * kD + 4 * lg;
   auto load_early = [&](ScanEarly& e, int c) {
     const float* ws = record(c);
-    const TIn* qf = reinterpret_cast<const TIn*>(ws + kWsQ);
+    const int row = 16 * M + li;
+    const TIn* qrow = qin + (size_t)(c * kC + (row < L - c * kC ? row : 0)) * kD;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       e.w[u] = *reinterpret_cast<const float4*>(ws + kWsW + ((M * 8 + u) * 64 + lane) * 4);
-      e.q[u] = R::ld4(qf, ((M * 8 + u) * 64 + lane) * 4);
+      e.q[u] = R::ld4(qrow, 16 * u);
     }
   };
   auto load_late = [&](ScanLate& l, int c) {
@@ -747,8 +746,8 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     }
     __syncthreads();
 
-    // ---- stage C: o = qs (Q S) + A v_new (all four blocks of A's row
-    // block, the ones above the diagonal being zero; two accumulator chains)
+    // ---- stage C: o = qs (Q S) + A v_new over the blocks J <= M of A's row
+    // block (two accumulator chains: J = 0, 1 and J = 2, 3)
     {
       float4 vb[4];
 #pragma unroll
@@ -757,10 +756,13 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
       f4v ad = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
+        if (u <= M) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          ac = mfma4(elem(l.a[u], k), elem(vb[u], k), ac);
-          ad = mfma4(elem(l.a[u + 2], k), elem(vb[u + 2], k), ad);
+          for (int k = 0; k < 4; ++k) ac = mfma4(elem(l.a[u], k), elem(vb[u], k), ac);
+        }
+        if (u + 2 <= M) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) ad = mfma4(elem(l.a[u + 2], k), elem(vb[u + 2], k), ad);
         }
       }
       aq = ac + ad;
