@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "numerics.hpp"
+
 namespace spk {
 
 __device__ __forceinline__ uint32_t ordered_f32(float v) {
@@ -44,13 +46,19 @@ __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsig
   return a > b ? a : b;
 }
 
+// Maximum over the wave, in every lane: lane swaps across the halves and
+// rows, then DPP rotations inside each 16-lane row (max is exact, so any
+// complete pattern gives the same key).  Every lane must be active.
+__device__ __forceinline__ unsigned long long join64(uint32_t hi, uint32_t lo) {
+  return ((unsigned long long)hi << 32) | lo;
+}
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, d, 64);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), d, 64);
-    v = umax64(v, ((unsigned long long)hi << 32) | lo);
-  }
+  v = umax64(v, join64(lane_xor32_u((uint32_t)(v >> 32)), lane_xor32_u((uint32_t)v)));
+  v = umax64(v, join64(lane_xor16_u((uint32_t)(v >> 32)), lane_xor16_u((uint32_t)v)));
+  v = umax64(v, join64(row_ror_u<8>((uint32_t)(v >> 32)), row_ror_u<8>((uint32_t)v)));
+  v = umax64(v, join64(row_ror_u<4>((uint32_t)(v >> 32)), row_ror_u<4>((uint32_t)v)));
+  v = umax64(v, join64(row_ror_u<2>((uint32_t)(v >> 32)), row_ror_u<2>((uint32_t)v)));
+  v = umax64(v, join64(row_ror_u<1>((uint32_t)(v >> 32)), row_ror_u<1>((uint32_t)v)));
   return v;
 }
 

@@ -386,11 +386,14 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   // gcum (running sum in token order, deltanet_chunk.cpp:137-142): lane t adds
   // g_0 .. g_t left to right (adding +0 past t), so every lane's sum is
   // rounded exactly as the reference's running sum
+  // (g_j taken by v_readlane: with __shfl the 64 reads became a serial chain
+  // of LDS permutes)
   if (wave == 0) {
     float run = 0.0f;
+    const int gbits = __float_as_int(gv);
 #pragma unroll
     for (int j = 0; j < 64; ++j) {
-      const float gj = __shfl(gv, j);
+      const float gj = __int_as_float(__builtin_amdgcn_readlane(gbits, j));
       run = run + (j <= lane ? gj : 0.0f);
     }
     sG[lane] = run;
@@ -416,8 +419,8 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
       const float4 x = R::cvt4(qa[u]);
       ssq = ssq + x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
     }
-    ssq = ssq + __shfl_xor(ssq, 16);
-    ssq = ssq + __shfl_xor(ssq, 32);
+    ssq = ssq + spk::lane_xor16(ssq);
+    ssq = ssq + spk::lane_xor32(ssq);
     iq = 1.0f / sqrtf(ssq + 1e-6f);
     const int r = tid >> 2, part = tid & 3;
     float sk = 0.0f;
@@ -426,8 +429,8 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
       const float4 x = RS::get4(sK, r, 32 * part + c);
       sk = sk + x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
     }
-    sk = sk + __shfl_xor(sk, 1);
-    sk = sk + __shfl_xor(sk, 2);
+    sk = sk + spk::lane_xor1(sk);
+    sk = sk + spk::lane_xor2(sk);
     if (part == 0) sIK[r] = 1.0f / sqrtf(sk + 1e-6f);
   } else if (tid < 64) {
     sIK[tid] = 1.0f;

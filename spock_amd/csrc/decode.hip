@@ -176,7 +176,7 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
         const float yb = spk::h2f(y[1]);
         float v = ya * ya + yb * yb;          // tree step stride 64
         v = spk::tree64_to_lane0(v);          // strides 32..1
-        const float tot = __shfl(v, 0, 64);
+        const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));  // lane 0 broadcast, no LDS
         const float inv = spk::rsqrt_det(tot + 1e-6f);
         y[0] = spk::f2h(ya * inv);
         y[1] = spk::f2h(yb * inv);
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
     if (NORM_GATE) {
       float v = oa * oa + ob * ob;
       v = spk::tree64_to_lane0(v);
-      const float tot = __shfl(v, 0, 64);
+      const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));  // lane 0 broadcast, no LDS
       const float r = spk::rsqrt_det(tot / 128.0f + p.eps);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {

@@ -46,7 +46,7 @@ __global__ __launch_bounds__(64) void dn_prefill_conv_kernel(const uint16_t* __r
   if (blk < 2 * kHeads) {  // L2 of the Q / K head block: 128-wide tree, eps inside the sqrt
     float v = y[0] * y[0] + y[1] * y[1];
     v = spk::tree64_to_lane0(v);
-    const float tot = __shfl(v, 0, 64);
+    const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));  // lane 0 broadcast, no LDS
     const float inv = spk::rsqrt_det(tot + 1e-6f);
     y[0] = y[0] * inv;
     y[1] = y[1] * inv;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(64) void dn_norm_gate_kernel(const float* __restric
   const float oa = o[lane], ob = o[lane + 64];
   float v = oa * oa + ob * ob;
   v = spk::tree64_to_lane0(v);
-  const float tot = __shfl(v, 0, 64);
+  const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));  // lane 0 broadcast, no LDS
   const float r = spk::rsqrt_det(tot / 128.0f + eps);
   const uint16_t* zr = z + (long long)t * zld + h * kDim;
   uint16_t* orow = out + (long long)t * old + h * kDim;

@@ -227,9 +227,9 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
     // combined in order (tot += S_b c_b, O += O_b c_b, c_b = e^{m_b - M}),
     // normalised, fp16, times sigmoid(gate), fp16.  Lane j of the head's 32
     // computes c_b and S_b of block b = j (+32 per chunk); the others take
-    // them by shuffle, so no barrier is needed.
+    // them by readlane, so no barrier is needed.
     const int h = tid >> 5, j = tid & 31;
-    const int gbase = tid & 32;  // this head's first lane in the wave
+    const bool hi_half = (tid & 32) != 0;  // this head's lanes are 32-63 of the wave
     float sig[8];
     {
       float g[8];
@@ -241,8 +241,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
     const int nb = (apos >= 0 && apos < a.max_seq) ? (apos + kAttnBlock) / kAttnBlock : 0;
     float M = j < nb ? am : -INFINITY;
     for (int b = j + 32; b < nb; b += 32) M = fmaxf(M, ph[(size_t)b * kPartFloats]);
-#pragma unroll
-    for (int sh = 16; sh >= 1; sh >>= 1) M = fmaxf(M, __shfl_xor(M, sh, 64));
+    M = spk::half_wave_max(M);
     float tot = 0.0f;
     float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int c0 = 0; c0 < nb; c0 += 32) {
@@ -252,6 +251,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
         sj = ph[(size_t)(c0 + j) * kPartFloats + 1];
       }
       const float cj = (c0 + j < nb) ? spk::expf_det(mj - M) : 0.0f;
+      const int cjb = __float_as_int(cj), sjb = __float_as_int(sj);
       const int n = min(32, nb - c0);
 #pragma unroll
       for (int i0 = 0; i0 < 32; i0 += 8) {
@@ -273,8 +273,11 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float c = __shfl(cj, gbase + i0 + i, 64);
-          const float sb = __shfl(sj, gbase + i0 + i, 64);
+          // lane i0+i of this head's half wave (lanes 0-31: head 2w, 32-63: 2w+1)
+          const float c = __int_as_float(hi_half ? __builtin_amdgcn_readlane(cjb, 32 + i0 + i)
+                                                 : __builtin_amdgcn_readlane(cjb, i0 + i));
+          const float sb = __int_as_float(hi_half ? __builtin_amdgcn_readlane(sjb, 32 + i0 + i)
+                                                  : __builtin_amdgcn_readlane(sjb, i0 + i));
           if (i0 + i < n) {
             tot = tot + sb * c;
             const float vv[8] = {ov[i][0].x, ov[i][0].y, ov[i][0].z, ov[i][0].w,
@@ -369,13 +372,9 @@ __device__ __forceinline__ void head_norm_wave(float (&v)[4], const float (&wf)[
   float s[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) s[i] = v[i] * v[i];
-#pragma unroll
-  for (int sh = 32; sh >= 1; sh >>= 1) {  // strides 128, 64, ..., 4 (lane distance sh)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = s[i] + __shfl_down(s[i], sh, 64);
-  }
+  spk::tree64_rows<4>(s);  // strides 128, 64, ..., 4 (lane distance 32..1), sums in lane 0
   float sum = (s[0] + s[2]) + (s[1] + s[3]);  // strides 2 then 1 inside lane 0
-  sum = __shfl(sum, 0, 64);
+  sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sum), 0));  // lane 0 broadcast, no LDS
   const float nf = 1.0f / __builtin_sqrtf(sum / 256.0f + 1e-6f);
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = round16((v[i] * nf) * (1.0f + wf[i]));
@@ -401,7 +400,7 @@ __device__ __forceinline__ void load_rope(const float* cs, int lane, float (&c)[
 __device__ __forceinline__ void rope_wave(float (&v)[4], const float (&c8)[8], int lane) {
   float o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = __shfl_xor(v[i], 8, 64);
+  for (int i = 0; i < 4; ++i) o[i] = spk::lane_xor8(v[i]);
   if (lane < 16) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -520,8 +519,7 @@ __device__ __forceinline__ void attn_block_wave(const uint16_t* qs, const uint16
     sc = dot * 0.0625f;
   }
   float m = sc;
-#pragma unroll
-  for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh, 64));
+  m = spk::wave_max(m);
   const float w = (p < npos) ? spk::expf_det(sc - m) : 0.0f;
   const float S = spk::tree64_to_lane0(w);
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -709,9 +707,7 @@ __global__ __launch_bounds__(256) void attn_prefill_blocks_kernel(AttnArgs a) {
     m[i] = (tok && pp < npos0 + i) ? dot[i] * 0.0625f : -INFINITY;
   }
 #pragma unroll
-  for (int sh = 32; sh >= 1; sh >>= 1)
-#pragma unroll
-    for (int i = 0; i < kAttnGroup; ++i) m[i] = fmaxf(m[i], __shfl_xor(m[i], sh, 64));
+  for (int i = 0; i < kAttnGroup; ++i) m[i] = spk::wave_max(m[i]);
 #pragma unroll
   for (int i = 0; i < kAttnGroup; ++i)
     w[i] = (lane < nvalid[i]) ? spk::expf_det(dot[i] * 0.0625f - m[i]) : 0.0f;
@@ -812,8 +808,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   __syncthreads();
   if (d < 64) {
     float m = fmaxf(fmaxf(red[d], red[d + 64]), fmaxf(red[d + 128], red[d + 192]));
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh, 64));
+    m = spk::wave_max(m);
     if (d == 0) red[256] = m;
   }
   __syncthreads();

@@ -98,22 +98,6 @@ __device__ __forceinline__ float rsqrt_det(float x) { return 1.0f / __builtin_sq
 
 __device__ __forceinline__ float silu_det(float x) { return x / (1.0f + expf_det(-x)); }
 
-// Wave-wide (64 lanes) shuffle-down; lanes >= 64-delta read their own value.
-__device__ __forceinline__ float shfl_down64(float v, int delta) {
-  return __shfl_down(v, delta, 64);
-}
-
-// 64-lane tree s[l] += s[l+stride], stride 32..1; the sum ends in lane 0.
-__device__ __forceinline__ float tree64_to_lane0(float v) {
-  v = v + shfl_down64(v, 32);
-  v = v + shfl_down64(v, 16);
-  v = v + shfl_down64(v, 8);
-  v = v + shfl_down64(v, 4);
-  v = v + shfl_down64(v, 2);
-  v = v + shfl_down64(v, 1);
-  return v;
-}
-
 // v <- v + (v of lane l + S), for lanes whose partner lies in the same row of
 // 16 lanes (DPP row_shl:S); other lanes receive values no later level reads.
 template <int S>
@@ -121,19 +105,92 @@ __device__ __forceinline__ float add_row_shl(float v) {
   return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + S, 0xF, 0xF, true));
 }
 
+// Lanes 0..31 receive lane l+32's value (v_permlane32_swap of v with itself:
+// a VALU lane exchange, no LDS round trip); lanes 32..63 keep their own.
+__device__ __forceinline__ float lanes_down32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[1]);
+}
+
+// Lanes 0..15 (and 32..47) receive lane l+16's value (v_permlane16_swap);
+// lanes 16..31 and 48..63 keep their own.
+__device__ __forceinline__ float lanes_down16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[1]);
+}
+
+// Exact xor exchanges without LDS: lane l receives lane (l ^ m)'s value.
+// 32 and 16 from the permlane swaps (r[1] is the lower half's / even rows'
+// partner value, r[0] the upper half's / odd rows'), 8 as a DPP rotation by 8
+// within the 16-lane row, 2 and 1 as DPP quad permutations.
+__device__ __forceinline__ uint32_t lane_xor32_u(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t lane_xor16_u(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (threadIdx.x & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t lane_xor8_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+}
+__device__ __forceinline__ uint32_t lane_xor2_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ uint32_t lane_xor1_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ float lane_xor32(float v) { return __uint_as_float(lane_xor32_u(__float_as_uint(v))); }
+__device__ __forceinline__ float lane_xor16(float v) { return __uint_as_float(lane_xor16_u(__float_as_uint(v))); }
+__device__ __forceinline__ float lane_xor8(float v) { return __uint_as_float(lane_xor8_u(__float_as_uint(v))); }
+__device__ __forceinline__ float lane_xor2(float v) { return __uint_as_float(lane_xor2_u(__float_as_uint(v))); }
+__device__ __forceinline__ float lane_xor1(float v) { return __uint_as_float(lane_xor1_u(__float_as_uint(v))); }
+
+// Lane l receives the value of lane (l - S) mod 16 of its row (DPP row_ror:S).
+template <int S>
+__device__ __forceinline__ uint32_t row_ror_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + S, 0xF, 0xF, false);
+}
+
+// Maximum over the 16 lanes of each row, in every lane (max is exact, so the
+// rotation pattern gives the same value as any other complete reduction).
+__device__ __forceinline__ float row_max16(float m) {
+  m = fmaxf(m, __uint_as_float(row_ror_u<8>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(row_ror_u<4>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(row_ror_u<2>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(row_ror_u<1>(__float_as_uint(m))));
+  return m;
+}
+// ... over each half wave (32 lanes) and over the whole wave, in every lane.
+__device__ __forceinline__ float half_wave_max(float m) { return row_max16(fmaxf(m, lane_xor16(m))); }
+__device__ __forceinline__ float wave_max(float m) { return half_wave_max(fmaxf(m, lane_xor32(m))); }
+
+// 64-lane tree s[l] += s[l+stride], stride 32..1; the sum ends in lane 0
+// (other lanes hold partial sums no caller reads).  Strides 32 and 16 by lane
+// swaps, 8..1 as DPP row shifts: no LDS permute on the chain.  Every lane of
+// the wave must be active.
+__device__ __forceinline__ float tree64_to_lane0(float v) {
+  v = v + lanes_down32(v);
+  v = v + lanes_down16(v);
+  v = add_row_shl<8>(v);
+  v = add_row_shl<4>(v);
+  v = add_row_shl<2>(v);
+  v = add_row_shl<1>(v);
+  return v;
+}
+
 // N independent 64-lane trees s[l] += s[l+stride], stride 32..1 (the order of
-// tree64_to_lane0), interleaved so each level's cross-lane moves are in
-// flight together: strides 32 and 16 through the LDS permute, 8..1 as DPP
-// row shifts.  Sums end in lane 0.
+// tree64_to_lane0), interleaved level by level.  Sums end in lane 0; every
+// lane of the wave must be active.
 template <int N>
 __device__ __forceinline__ void tree64_rows(float (&v)[N]) {
   float t[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) t[i] = __shfl_down(v[i], 32, 64);
+  for (int i = 0; i < N; ++i) t[i] = lanes_down32(v[i]);
 #pragma unroll
   for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
 #pragma unroll
-  for (int i = 0; i < N; ++i) t[i] = __shfl_down(v[i], 16, 64);
+  for (int i = 0; i < N; ++i) t[i] = lanes_down16(v[i]);
 #pragma unroll
   for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
 #pragma unroll
