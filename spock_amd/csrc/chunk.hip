@@ -311,12 +311,13 @@ __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG,
 // PARTS workgroups per (chunk, head) (blockIdx.z = part), for launches with
 // too few (chunk, head) pairs to fill the chip: every part loads the chunk,
 // forms the Gram tiles and T (the serial part), then computes and stores only
-// its share of the record: U / W column tiles 2*part, 2*part+1 (PARTS 4; its
-// four wavefronts split the two tiles' row blocks as {0,3} / {1,2}, 40 MFMA
-// each instead of 160) or 4*part..4*part+3 (PARTS 2), and the A, raw Q and K^T
-// blocks of the wavefronts w with w % PARTS == part.  Each value is computed
-// by the same operation sequence whatever PARTS is, so the record is
-// bit-identical.
+// its share of the record: U / W column tiles 4*part..4*part+3 (PARTS 2),
+// 2*part and 2*part+1 (PARTS 4: its four wavefronts split the two tiles' row
+// blocks as {0,3} / {1,2}, 40 MFMA each instead of 160) or tile `part`
+// (PARTS 8: waves 0-1 form U, 2-3 form W, row blocks {0,3} / {1,2}, 20 MFMA
+// each), and the A and K^T blocks of the wavefronts w with w % PARTS == part.
+// Each value is computed by the same operation sequence whatever PARTS is, so
+// the record is bit-identical.
 template <typename TIn, int PARTS>
 __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_kernel(ChunkParams p) {
   typedef RawOf<TIn> R;
@@ -515,9 +516,17 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   constexpr int kTilesPerWave = PARTS == 1 ? 2 : 1;
 #pragma unroll
   for (int jj = 0; jj < kTilesPerWave; ++jj) {
-    const int ct = PARTS == 1 ? 2 * wave + jj : PARTS == 2 ? 4 * part + wave : 2 * part + (wave & 1);
-    const unsigned imask = PARTS == 4 ? ((wave >> 1) ? 0x6u : 0x9u) : 0xFu;  // row blocks I of this wave
-    const int umax = PARTS == 4 ? ((wave >> 1) ? 2 : 3) : 3;
+    const int ct = PARTS == 1   ? 2 * wave + jj
+                   : PARTS == 2 ? 4 * part + wave
+                   : PARTS == 4 ? 2 * part + (wave & 1)
+                                : part;
+    // row blocks I of this wave: {0,3} or {1,2} (4 parts: by wave / 2; 8
+    // parts: by wave % 2, waves 0-1 forming U and 2-3 forming W)
+    const bool odd_rows = PARTS == 4 ? (wave >> 1) != 0 : (wave & 1) != 0;
+    const unsigned imask = PARTS >= 4 ? (odd_rows ? 0x6u : 0x9u) : 0xFu;
+    const int umax = PARTS >= 4 ? (odd_rows ? 2 : 3) : 3;
+    const bool do_u = PARTS < 8 || wave < 2;
+    const bool do_w = PARTS < 8 || wave >= 2;
     const int n = 16 * ct + li;
     f4v au[4], aw[4];
 #pragma unroll
@@ -539,10 +548,13 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
         if (!((imask >> I) & 1u)) continue;
         const float* tp = (I == u) ? sL + blk(I, I) : sT + offblk(I, u);
         const float4 a4 = *reinterpret_cast<const float4*>(&tp[li * 16 + 4 * lg]);
+        if (do_u) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          au[I] = mfma4(elem(a4, s), vb[s], au[I]);
-          aw[I] = mfma4(kb[s], elem(a4, s), aw[I]);
+          for (int s = 0; s < 4; ++s) au[I] = mfma4(elem(a4, s), vb[s], au[I]);
+        }
+        if (do_w) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) aw[I] = mfma4(kb[s], elem(a4, s), aw[I]);
         }
       }
     }
@@ -550,8 +562,8 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       if (!((imask >> I) & 1u)) continue;
-      ws_store(ws + kWsU + ((ct * 4 + I) * 64 + lane) * 4, au[I][0], au[I][1], au[I][2], au[I][3]);
-      ws_store(ws + kWsW + ((I * 8 + ct) * 64 + lane) * 4, aw[I][0], aw[I][1], aw[I][2], aw[I][3]);
+      if (do_u) ws_store(ws + kWsU + ((ct * 4 + I) * 64 + lane) * 4, au[I][0], au[I][1], au[I][2], au[I][3]);
+      if (do_w) ws_store(ws + kWsW + ((I * 8 + ct) * 64 + lane) * 4, aw[I][0], aw[I][1], aw[I][2], aw[I][3]);
     }
     __builtin_amdgcn_sched_barrier(0);  // one column tile's operands live at a time
   }
@@ -904,6 +916,7 @@ void fill_tables(ChunkParams& p, const SeqEntry* e, int n) {
 // and T work costs more than the split saves (fp16, 8 chunks x 16 heads: 4
 // parts 23.9 us, 1 part 20.2 us).
 int intra_parts(long long pairs) {
+  if (pairs * 8 <= 256) return 8;
   if (pairs * 4 <= 256) return 4;
   if (pairs * 2 <= 256) return 2;
   return 1;
@@ -912,7 +925,9 @@ int intra_parts(long long pairs) {
 template <typename TIn>
 void launch_intra_t(const ChunkParams& p, int chunks, int parts, hipStream_t s) {
   dim3 g((unsigned)chunks, (unsigned)p.H, (unsigned)parts);
-  if (parts == 4)
+  if (parts == 8)
+    hipLaunchKernelGGL((chunk_intra_kernel<TIn, 8>), g, dim3(256), 0, s, p);
+  else if (parts == 4)
     hipLaunchKernelGGL((chunk_intra_kernel<TIn, 4>), g, dim3(256), 0, s, p);
   else if (parts == 2)
     hipLaunchKernelGGL((chunk_intra_kernel<TIn, 2>), g, dim3(256), 0, s, p);

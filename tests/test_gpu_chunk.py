@@ -154,20 +154,20 @@ def test_config2_full_size_properties(dev, oracle):
 @pytest.mark.parametrize("half", [False, True])
 def test_small_launch_paths_equal_packed(dev, half):
     """Alone, a 104-token sequence (2 chunks x 16 heads) runs the intra kernel
-    as 4 workgroups per (chunk, head) and a 300-token one (5 chunks) as 2; the
-    scan runs two workgroups per CU and skips the first chunk's S products (no
-    initial state).  Packed with longer sequences the same sequences run one
-    workgroup per (chunk, head) and, for fp16, the three-per-CU scan.  Every
-    output must be the same bits."""
+    as 8 workgroups per (chunk, head), a 192-token one (3 chunks) as 4 and a
+    300-token one (5 chunks) as 2; the scan runs two workgroups per CU and
+    skips the first chunk's S products (no initial state).  Packed with longer
+    sequences the same sequences run one workgroup per (chunk, head) and, for
+    fp16, the three-per-CU scan.  Every output must be the same bits."""
     from spock_amd import synth
-    lens = np.array([104, 300, 300, 300, 4096])
+    lens = np.array([104, 192, 300, 300, 4096])
     cu = synth.cu_seqlens_from(lens)
     inp = synth.chunk_inputs(16, int(cu[-1]), seed=11)
     if half:
         for n in ("q", "k", "v"):
             inp[n] = inp[n].astype(np.float16).astype(np.float32)
     gc, gs = _run(dev, inp, cu=cu, half=half)
-    for s in (0, 1):
+    for s in (0, 1, 2):
         t0, L = int(cu[s]), int(lens[s])
         c1, s1 = _run(dev, {k_: v_[:, t0:t0 + L] for k_, v_ in inp.items()}, half=half)
         assert np.array_equal(c1, gc[:, t0:t0 + L]) and np.array_equal(s1[0], gs[s])
