@@ -729,9 +729,12 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     // scale is applied to the product
     f4v aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
     if constexpr (!decltype(zero_s)::value) {
+      // the S piece of step u+1 is read while step u's MFMAs run
+      float4 sb_next = *reinterpret_cast<const float4*>(&sST[li * kLdST + 4 * lg]);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float4 sb = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * u + 4 * lg]);
+        const float4 sb = sb_next;
+        if (u + 1 < 8) sb_next = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * (u + 1) + 4 * lg]);
         const float4 x = R::cvt4(e.q[u]);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -744,10 +747,16 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
       // would queue in the CU's vector-memory pipe behind the other
       // wavefronts' bursts.  (sched_group_barrier masks: 0x020 VMEM read,
       // 0x008 MFMA.)
+      // (masks: 0x100 LDS read, 0x020 VMEM read, 0x008 MFMA) -- the S piece
+      // of step u+1 goes out before step u's 8 MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        if (i < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     }
 
