@@ -388,6 +388,21 @@ def bench_model(steps, warmup, use_graph=True, cpu=False):
             mism = [i for i, (a, b) in enumerate(zip(best.tokens.tolist(), golden)) if a != b]
             r["first_token_mismatch"] = mism[0] if mism else None
         res[mode] = r
+    # Per-region GPU time of the decode step (the reference's gpu_region_us),
+    # from a separate untimed run: HIP events between the regions, so the
+    # step's kernels are launched one by one instead of replayed as a graph.
+    with model.Session(art, gpu_timestamps=2) as s:
+        s.generate(prompt[:64], 4)
+        rr = s.generate(prompt, MODEL_NEW)
+    per = {k: v / rr.decode_steps for k, v in rr.gpu_region_us.items()}
+    layer_us = [per[f"layer_{i}"] for i in range(24)]
+    attn = [u for i, u in enumerate(layer_us) if i % 4 == 3]
+    dn = [u for i, u in enumerate(layer_us) if i % 4 != 3]
+    res["gpu_regions_us_per_token"] = {
+        "deltanet_layer_mean": round(float(np.mean(dn)), 2), "attention_layer_mean": round(float(np.mean(attn)), 2),
+        "lm_head": round(per["lm_head"], 2), "argmax": round(per["argmax"], 2),
+        "step": round(float(np.mean(rr.per_token_gpu_us)), 2), "layers": [round(u, 2) for u in layer_us],
+        "launches": "one by one (events between regions)"}
     nbytes = model_decode_bytes()
     per_tok = res["ordered_prefill"]["decode_us_per_token"] / 1e6
     res["decode_bytes_per_token"] = nbytes

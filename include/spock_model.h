@@ -43,10 +43,18 @@ const char* spk_model_last_error(void);
 
 /* spk_model_open flags */
 enum {
-  SPK_MODEL_NO_GRAPH = 1,       /* launch the decode step's kernels one by one */
-  SPK_MODEL_MATRIX_PREFILL = 2  /* prompt on the matrix cores (spk_gemm_f16, MFMA
-                                   chunk rule) instead of the default order of
-                                   the CPU restatement (bit-identical prefill) */
+  SPK_MODEL_NO_GRAPH = 1,        /* launch the decode step's kernels one by one */
+  SPK_MODEL_MATRIX_PREFILL = 2,  /* prompt on the matrix cores (spk_gemm_f16, MFMA
+                                    chunk rule) instead of the default order of
+                                    the CPU restatement (bit-identical prefill) */
+  SPK_MODEL_GPU_TIMESTAMPS = 4,  /* GPU time of every decode step (the reference's
+                                    SPOCK_GPU_TIMESTAMPS, vk_session.cpp:2188-2201):
+                                    a HIP event before each step, graph kept */
+  SPK_MODEL_GPU_REGIONS = 8      /* also GPU time per region of the step
+                                    (SPOCK_GPU_BLOCK_TIMESTAMPS, vk_session.cpp:
+                                    2204-2218): events after each layer, lm_head and
+                                    argmax; the step's kernels are then launched one
+                                    by one, since a recorded graph holds no events */
 };
 
 /* Opens <repack_dir>, uploads every tensor, allocates the per-layer state for
@@ -66,6 +74,21 @@ int spk_model_reset(SpkModel* m);
  * max_new tokens (the first from the prefill logits).  out_tokens[max_new]. */
 int spk_model_generate(SpkModel* m, const int32_t* prompt, int32_t prompt_len, int32_t max_new,
                        int32_t* out_tokens, SpkGenerateStats* stats);
+
+/* GPU timings of the last spk_model_generate call's decode steps (sessions
+ * opened with SPK_MODEL_GPU_TIMESTAMPS or SPK_MODEL_GPU_REGIONS; otherwise
+ * empty).  DecodeResult::per_token_gpu_us (vk_decode.hpp:19): writes
+ * min(*count, capacity) microseconds, one per step; *count = steps. */
+int spk_model_gpu_token_us(const SpkModel* m, double* us, int32_t capacity, int32_t* count);
+/* DecodeResult::gpu_region_us (vk_decode.hpp:20, filled at vk_session.cpp:
+ * 4139-4176), SPK_MODEL_GPU_REGIONS only: microseconds per region summed over
+ * the steps, in step order: "layer_0" .. "layer_<n-1>" ("layer_0" includes the
+ * embedding gather, which its input norm reads directly, so there is no
+ * "embedding" region), "lm_head" (final norm, lm_head and the argmax key in one
+ * launch, so no separate "final_norm"), "argmax" (the take that records the
+ * token).  *name stays valid until the next spk_model_generate call. */
+int spk_model_gpu_region_count(const SpkModel* m, int32_t* count);
+int spk_model_gpu_region(const SpkModel* m, int32_t index, const char** name, double* us);
 
 /* Lower-level steps (the same work as spk_model_generate):
  * prefill at the current position (no reset) -> greedy token;

@@ -92,8 +92,12 @@ std::vector<float> rope_table(std::uint32_t max_seq) {
 }
 
 Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::uint32_t max_seq, bool use_graph,
-                             bool ordered_prefill)
-    : verbose_(verbose), use_graph_(use_graph), ordered_prefill_(ordered_prefill), max_seq_(max_seq ? max_seq : MAX_SEQ) {
+                             bool ordered_prefill, GpuTimestamps gpu_timestamps)
+    : verbose_(verbose),
+      use_graph_(use_graph),
+      ordered_prefill_(ordered_prefill),
+      max_seq_(max_seq ? max_seq : MAX_SEQ),
+      gpu_ts_(gpu_timestamps) {
   if (max_seq_ > 65536) throw std::runtime_error("max_seq must be <= 65536");
   const auto t0 = std::chrono::steady_clock::now();
   WeightArtifact art = WeightArtifact::load(repack_dir);
@@ -191,6 +195,19 @@ Qwen35Session::~Qwen35Session() {
     (void)hipStreamSynchronize(stream_);
     (void)hipStreamDestroy(stream_);
   }
+  for (hipEvent_t e : ts_events_) (void)hipEventDestroy(e);
+}
+
+void Qwen35Session::ensure_ts_events(std::size_t n) {
+  while (ts_events_.size() < n) {
+    hipEvent_t e = nullptr;
+    hip_check(hipEventCreate(&e), "hipEventCreate");
+    ts_events_.push_back(e);
+  }
+}
+
+void Qwen35Session::mark(std::size_t k) {
+  if (marks_) hip_check(hipEventRecord(marks_[k], stream_), "hipEventRecord (region)");
 }
 
 void Qwen35Session::reset() {
@@ -373,7 +390,9 @@ std::uint32_t Qwen35Session::prefill(const std::vector<std::uint32_t>& tokens) {
 void Qwen35Session::enqueue_decode_step() {
   std::int32_t* tok = tok_.get<std::int32_t>();
   std::uint16_t* h = h_.get<std::uint16_t>();
-  for (std::size_t L = 0; L < layers_.size(); ++L) {
+  const std::size_t NL = layers_.size();
+  mark(0);
+  for (std::size_t L = 0; L < NL; ++L) {
     const LayerW& w = layers_[L];
     SpkGemvInput in{};
     in.kind = SPK_GEMV_IN_RMSNORM;
@@ -452,17 +471,20 @@ void Qwen35Session::enqueue_decode_step() {
     di.x = gate_.get<std::uint16_t>();
     const SpkGemvOutput dout{w.mlp_down, h, h, static_cast<int32_t>(H), nullptr};
     spk_check(spk_gemv_fused(&di, &dout, 1, S(stream_)), "down_proj");
+    mark(L + 1);
   }
   // final norm + lm_head + argmax key in one launch; the take records the token
   const int32_t vocab = static_cast<int32_t>(shape_.vocab);
   spk_check(spk_lm_head_argmax_key(embed_, h, final_norm_, vocab, H, logits_.get<std::uint16_t>(),
                                    argmax_key_.get<std::uint64_t>(), S(stream_)),
             "lm_head");
+  mark(NL + 1);
   std::int32_t* hist = history_.get<std::int32_t>();
   spk_check(spk_argmax_key_take(argmax_key_.get<std::uint64_t>(), vocab, reinterpret_cast<std::uint32_t*>(tok),
                                 pos_.get<std::int32_t>(), hist, hist + 64, static_cast<int32_t>(history_cap_),
                                 S(stream_)),
             "argmax take");
+  mark(NL + 2);
 }
 
 void Qwen35Session::ensure_graph() {
@@ -519,16 +541,32 @@ DecodeResult Qwen35Session::decode(const std::vector<std::uint32_t>& prompt_toke
   r.gpu_prefill_us = last_gpu_prefill_ms_ * 1000.0;
   r.generated_tokens.push_back(first);
   if (max_new_tokens > 1) {
-    ensure_graph();  // recorded outside the timed region
-    EventTimer ev;
-    const auto t1 = std::chrono::steady_clock::now();
-    hip_check(hipEventRecord(ev.a, stream_), "hipEventRecord");
     const std::uint32_t n = max_new_tokens - 1;
     if (std::size_t(pos_host_) + n > max_seq_)
       throw std::runtime_error("decode: position " + std::to_string(pos_host_ + n) + " exceeds max_seq " +
                                std::to_string(max_seq_));
     if (std::size_t(history_len_) + n > history_cap_) throw std::runtime_error("decode: token history full");
-    for (std::uint32_t i = 0; i < n; ++i) run_decode_step();
+    const bool regions = gpu_ts_ == GpuTimestamps::per_region;
+    const std::size_t NL = layers_.size(), per_step = NL + 3;  // events of one step: start, layers, lm_head, argmax
+    if (regions)
+      ensure_ts_events(std::size_t(n) * per_step);
+    else if (gpu_ts_ == GpuTimestamps::per_token)
+      ensure_ts_events(std::size_t(n) + 1);
+    if (!regions) ensure_graph();  // recorded outside the timed region
+    EventTimer ev;
+    const auto t1 = std::chrono::steady_clock::now();
+    hip_check(hipEventRecord(ev.a, stream_), "hipEventRecord");
+    for (std::uint32_t i = 0; i < n; ++i) {
+      if (regions) {
+        marks_ = &ts_events_[std::size_t(i) * per_step];
+        enqueue_decode_step();
+        marks_ = nullptr;
+      } else {
+        if (gpu_ts_ == GpuTimestamps::per_token) hip_check(hipEventRecord(ts_events_[i], stream_), "hipEventRecord");
+        run_decode_step();
+      }
+    }
+    if (gpu_ts_ == GpuTimestamps::per_token) hip_check(hipEventRecord(ts_events_[n], stream_), "hipEventRecord");
     hip_check(hipEventRecord(ev.b, stream_), "hipEventRecord");
     std::vector<std::int32_t> out(n);
     hip_check(hipMemcpyAsync(out.data(), history_.get<std::int32_t>() + 64 + history_len_, n * 4,
@@ -537,12 +575,29 @@ DecodeResult Qwen35Session::decode(const std::vector<std::uint32_t>& prompt_toke
     hip_check(hipStreamSynchronize(stream_), "decode");
     r.decode_ms = ms_since(t1);
     r.gpu_decode_us = ev.ms() * 1000.0;
+    auto us = [&](std::size_t a, std::size_t b) {
+      float v = 0.0f;
+      hip_check(hipEventElapsedTime(&v, ts_events_[a], ts_events_[b]), "hipEventElapsedTime");
+      return double(v) * 1000.0;
+    };
+    if (gpu_ts_ == GpuTimestamps::per_token) {
+      for (std::uint32_t i = 0; i < n; ++i) r.per_token_gpu_us.push_back(us(i, i + 1));
+    } else if (regions) {
+      for (std::size_t L = 0; L < NL; ++L) r.gpu_region_us.emplace_back("layer_" + std::to_string(L), 0.0);
+      r.gpu_region_us.emplace_back("lm_head", 0.0);
+      r.gpu_region_us.emplace_back("argmax", 0.0);
+      for (std::uint32_t i = 0; i < n; ++i) {
+        const std::size_t b = std::size_t(i) * per_step;
+        r.per_token_gpu_us.push_back(us(b, b + NL + 2));
+        for (std::size_t k = 0; k < NL + 2; ++k) r.gpu_region_us[k].second += us(b + k, b + k + 1);
+      }
+    }
     pos_host_ += static_cast<std::int32_t>(n);
     history_len_ += n;
     for (auto t : out) r.generated_tokens.push_back(static_cast<std::uint32_t>(t));
     r.decode_steps = n;
   }
-  r.used_graph = use_graph_;
+  r.used_graph = use_graph_ && gpu_ts_ != GpuTimestamps::per_region;
   r.elapsed_ms = ms_since(t0);
   return r;
 }
@@ -594,6 +649,7 @@ void Qwen35Session::last_output(std::uint16_t* logits, std::uint16_t* hidden) {
 
 struct SpkModel {
   std::unique_ptr<spock::hip::Qwen35Session> s;
+  spock::hip::DecodeResult last;  // timings of the last spk_model_generate call
 };
 
 namespace {
@@ -617,12 +673,17 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
   SpkModel* m = nullptr;
   const int rc = guarded([&] {
     if (!repack_dir) throw std::runtime_error("spk_model_open: NULL directory");
-    if (flags & ~(SPK_MODEL_NO_GRAPH | SPK_MODEL_MATRIX_PREFILL)) throw std::runtime_error("spk_model_open: unknown flags");
+    if (flags & ~(SPK_MODEL_NO_GRAPH | SPK_MODEL_MATRIX_PREFILL | SPK_MODEL_GPU_TIMESTAMPS | SPK_MODEL_GPU_REGIONS))
+      throw std::runtime_error("spk_model_open: unknown flags");
+    using spock::hip::GpuTimestamps;
+    const GpuTimestamps ts = (flags & SPK_MODEL_GPU_REGIONS)      ? GpuTimestamps::per_region
+                             : (flags & SPK_MODEL_GPU_TIMESTAMPS) ? GpuTimestamps::per_token
+                                                                  : GpuTimestamps::off;
     auto s = std::make_unique<spock::hip::Qwen35Session>(repack_dir, false,
                                                          max_seq > 0 ? static_cast<std::uint32_t>(max_seq) : 0u,
                                                          (flags & SPK_MODEL_NO_GRAPH) == 0,
-                                                         (flags & SPK_MODEL_MATRIX_PREFILL) == 0);
-    m = new SpkModel{std::move(s)};
+                                                         (flags & SPK_MODEL_MATRIX_PREFILL) == 0, ts);
+    m = new SpkModel{std::move(s), {}};
   });
   return rc == 0 ? m : nullptr;
 }
@@ -655,7 +716,8 @@ extern "C" int spk_model_generate(SpkModel* m, const int32_t* prompt, int32_t pr
       if (prompt[i] < 0) throw std::runtime_error("spk_model_generate: negative token id");
       p.push_back(static_cast<std::uint32_t>(prompt[i]));
     }
-    const spock::hip::DecodeResult r = m->s->decode(p, static_cast<std::uint32_t>(max_new));
+    m->last = m->s->decode(p, static_cast<std::uint32_t>(max_new));
+    const spock::hip::DecodeResult& r = m->last;
     for (std::size_t i = 0; i < r.generated_tokens.size(); ++i) out_tokens[i] = static_cast<int32_t>(r.generated_tokens[i]);
     if (stats) {
       stats->prefill_ms = r.prefill_ms;
@@ -665,6 +727,34 @@ extern "C" int spk_model_generate(SpkModel* m, const int32_t* prompt, int32_t pr
       stats->decode_steps = static_cast<int32_t>(r.decode_steps);
       stats->used_graph = r.used_graph ? 1 : 0;
     }
+  });
+}
+
+extern "C" int spk_model_gpu_token_us(const SpkModel* m, double* us, int32_t capacity, int32_t* count) {
+  return guarded([&] {
+    if (!m || !count || (capacity > 0 && !us)) throw std::runtime_error("spk_model_gpu_token_us: NULL argument");
+    const auto& v = m->last.per_token_gpu_us;
+    *count = static_cast<int32_t>(v.size());
+    for (std::size_t i = 0; i < v.size() && i < std::size_t(capacity > 0 ? capacity : 0); ++i) us[i] = v[i];
+  });
+}
+
+extern "C" int spk_model_gpu_region_count(const SpkModel* m, int32_t* count) {
+  return guarded([&] {
+    if (!m || !count) throw std::runtime_error("spk_model_gpu_region_count: NULL argument");
+    *count = static_cast<int32_t>(m->last.gpu_region_us.size());
+  });
+}
+
+extern "C" int spk_model_gpu_region(const SpkModel* m, int32_t index, const char** name, double* us) {
+  return guarded([&] {
+    if (!m || !name || !us) throw std::runtime_error("spk_model_gpu_region: NULL argument");
+    const auto& v = m->last.gpu_region_us;
+    if (index < 0 || std::size_t(index) >= v.size())
+      throw std::runtime_error("spk_model_gpu_region: index " + std::to_string(index) + " of " +
+                               std::to_string(v.size()) + " regions");
+    *name = v[index].first.c_str();
+    *us = v[index].second;
   });
 }
 

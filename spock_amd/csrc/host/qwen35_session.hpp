@@ -25,6 +25,7 @@
 
 #include <cstdint>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "hip_buffer.hpp"
@@ -43,8 +44,19 @@ struct DecodeResult {
   double gpu_decode_us = 0.0;
   std::uint32_t decode_steps = 0;
   bool used_graph = false;
+  // With GPU timestamps on (vk_decode.hpp:16-21): GPU microseconds of each
+  // decode step, and per region of the step summed over the steps, in step
+  // order: layer_0 .. layer_{n-1} (layer_0 includes the embedding gather,
+  // which its input norm reads directly), lm_head (final norm, lm_head and
+  // the argmax key in one launch), argmax (the take that records the token).
+  std::vector<double> per_token_gpu_us;
+  std::vector<std::pair<std::string, double>> gpu_region_us;
   std::string error;
 };
+
+// GPU timestamp levels of a session (SPOCK_GPU_TIMESTAMPS and
+// SPOCK_GPU_BLOCK_TIMESTAMPS, vk_session.cpp:2188-2218).
+enum class GpuTimestamps { off = 0, per_token = 1, per_region = 2 };
 
 class Qwen35Session {
  public:
@@ -54,8 +66,13 @@ class Qwen35Session {
   // ordered_prefill: prompt projections and chunk rule in the CPU
   // restatement's operation order (bit-identical prefill, the reference's
   // default CPU chunk path, vk_session.cpp:4840-4868); false: matrix cores.
+  // gpu_timestamps: per_token records a HIP event before every decode step;
+  // per_region also records one after each layer, lm_head and argmax inside
+  // the step, whose kernels are then launched one by one (a recorded graph
+  // holds no timing events).
   explicit Qwen35Session(const std::string& repack_dir, bool verbose = false, std::uint32_t max_seq = MAX_SEQ,
-                         bool use_graph = true, bool ordered_prefill = true);
+                         bool use_graph = true, bool ordered_prefill = true,
+                         GpuTimestamps gpu_timestamps = GpuTimestamps::off);
   ~Qwen35Session();
   Qwen35Session(const Qwen35Session&) = delete;
   Qwen35Session& operator=(const Qwen35Session&) = delete;
@@ -101,6 +118,8 @@ class Qwen35Session {
   void enqueue_decode_step();
   void ensure_graph();
   void run_decode_step();
+  void ensure_ts_events(std::size_t n);
+  void mark(std::size_t k);
   float* dn_state_layer(std::uint32_t i) const { return dn_state_.get<float>() + std::size_t(i) * kStateFloats; }
   std::uint16_t* conv_layer(std::uint32_t i) const { return conv_state_.get<std::uint16_t>() + std::size_t(i) * 6144 * 4; }
   std::uint16_t* kv_layer(std::uint32_t i) const {
@@ -116,6 +135,9 @@ class Qwen35Session {
   hipStream_t stream_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
   hipGraph_t graph_ = nullptr;
+  GpuTimestamps gpu_ts_ = GpuTimestamps::off;
+  std::vector<hipEvent_t> ts_events_;  // timing events, reused across calls
+  hipEvent_t* marks_ = nullptr;        // this step's region events (eager steps only)
   std::int32_t pos_host_ = 0;       // host mirror of the next position
   std::uint32_t history_len_ = 0;   // tokens recorded so far
   double last_gpu_prefill_ms_ = 0.0;

@@ -22,6 +22,8 @@ _sz = C.c_size_t
 
 SPK_MODEL_NO_GRAPH = 1
 SPK_MODEL_MATRIX_PREFILL = 2
+SPK_MODEL_GPU_TIMESTAMPS = 4
+SPK_MODEL_GPU_REGIONS = 8
 
 
 class SpkGenerateStats(C.Structure):
@@ -36,6 +38,9 @@ SIGNATURES = {
     "spk_model_info": (C.c_int, [_p, _p, _p, _p]),
     "spk_model_reset": (C.c_int, [_p]),
     "spk_model_generate": (C.c_int, [_p, _p, _i32, _i32, _p, _p]),
+    "spk_model_gpu_token_us": (C.c_int, [_p, _p, _i32, _p]),
+    "spk_model_gpu_region_count": (C.c_int, [_p, _p]),
+    "spk_model_gpu_region": (C.c_int, [_p, _i32, _p, _p]),
     "spk_model_prefill": (C.c_int, [_p, _p, _i32, _p]),
     "spk_model_decode": (C.c_int, [_p, _i32, _p]),
     "spk_model_state_sizes": (C.c_int, [_p, _p, _p, _p]),
@@ -89,16 +94,25 @@ class GenerateResult:
     gpu_decode_ms: float
     decode_steps: int
     used_graph: bool
+    # with gpu_timestamps (DecodeResult::per_token_gpu_us / gpu_region_us)
+    per_token_gpu_us: Optional[np.ndarray] = None
+    gpu_region_us: Optional[dict] = None
 
 
 class Session:
     """DecodeSession on one MI355X: construct from a repack directory, then
     generate(prompt, max_new) (= decode()), reset(), prefill/decode steps.
     matrix_prefill=True runs the prompt on the matrix cores; the default runs
-    it in the CPU restatement's order (bit-identical)."""
+    it in the CPU restatement's order (bit-identical).  gpu_timestamps: 0 off,
+    1 GPU time per decode step, 2 also per region of the step (layer_i,
+    lm_head, argmax; the step's kernels are then launched one by one)."""
 
-    def __init__(self, repack_dir, max_seq: int = 2048, use_graph: bool = True, matrix_prefill: bool = False):
+    def __init__(self, repack_dir, max_seq: int = 2048, use_graph: bool = True, matrix_prefill: bool = False,
+                 gpu_timestamps: int = 0):
+        if gpu_timestamps not in (0, 1, 2):
+            raise ModelError(f"gpu_timestamps must be 0, 1 or 2, got {gpu_timestamps}")
         flags = (0 if use_graph else SPK_MODEL_NO_GRAPH) | (SPK_MODEL_MATRIX_PREFILL if matrix_prefill else 0)
+        flags |= (0, SPK_MODEL_GPU_TIMESTAMPS, SPK_MODEL_GPU_REGIONS)[gpu_timestamps]
         self._h = lib().spk_model_open(str(repack_dir).encode(), max_seq, flags)
         if not self._h:
             raise ModelError(f"spk_model_open: {lib().spk_model_last_error().decode(errors='replace')}")
@@ -132,8 +146,24 @@ class Session:
         st = SpkGenerateStats()
         _check(lib().spk_model_generate(self._h, p.ctypes.data, len(p), max_new, out.ctypes.data, C.byref(st)),
                "spk_model_generate")
-        return GenerateResult(out[:max_new].copy(), st.prefill_ms, st.decode_ms, st.gpu_prefill_ms,
-                              st.gpu_decode_ms, st.decode_steps, bool(st.used_graph))
+        res = GenerateResult(out[:max_new].copy(), st.prefill_ms, st.decode_ms, st.gpu_prefill_ms,
+                             st.gpu_decode_ms, st.decode_steps, bool(st.used_graph))
+        n = _i32()
+        _check(lib().spk_model_gpu_token_us(self._h, None, 0, C.byref(n)), "spk_model_gpu_token_us")
+        if n.value:
+            us = np.zeros(n.value, dtype=np.float64)
+            _check(lib().spk_model_gpu_token_us(self._h, us.ctypes.data, n.value, C.byref(n)),
+                   "spk_model_gpu_token_us")
+            res.per_token_gpu_us = us
+        _check(lib().spk_model_gpu_region_count(self._h, C.byref(n)), "spk_model_gpu_region_count")
+        if n.value:
+            regions = {}
+            name, us1 = C.c_char_p(), C.c_double()
+            for i in range(n.value):
+                _check(lib().spk_model_gpu_region(self._h, i, C.byref(name), C.byref(us1)), "spk_model_gpu_region")
+                regions[name.value.decode()] = us1.value
+            res.gpu_region_us = regions
+        return res
 
     def prefill(self, prompt: Sequence[int]) -> int:
         p = np.ascontiguousarray(prompt, dtype=np.int32)

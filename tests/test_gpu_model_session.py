@@ -130,3 +130,37 @@ def test_long_generation_past_8192_tokens(dev, small_artifact):
         assert all(0 <= t < VOCAB for t in r.tokens)
         with pytest.raises(model.ModelError, match="max_seq"):
             s.generate(_prompt(8), 8994)
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_gpu_timestamps(dev, small_artifact, use_graph):
+    """Per-step and per-region GPU times (DecodeResult::per_token_gpu_us and
+    gpu_region_us, vk_decode.hpp:19-20): same tokens as an untimed session;
+    one time per decode step; the regions of a step tile it exactly, in step
+    order, so their sums equal the per-step sum."""
+    from spock_amd import model
+    print(f"[session gpu timestamps graph={use_graph}]", flush=True)
+    prompt, n = _prompt(20), 12
+    with model.Session(small_artifact, max_seq=64, use_graph=use_graph) as s:
+        base = s.generate(prompt, n)
+        assert base.per_token_gpu_us is None and base.gpu_region_us is None
+    with model.Session(small_artifact, max_seq=64, use_graph=use_graph, gpu_timestamps=1) as s:
+        r = s.generate(prompt, n)
+    assert r.tokens.tolist() == base.tokens.tolist() and r.used_graph == use_graph
+    assert r.gpu_region_us is None
+    t = r.per_token_gpu_us
+    assert t is not None and len(t) == n - 1 and (t > 0).all()
+    assert 0.5 * r.gpu_decode_ms * 1e3 <= t.sum() <= r.gpu_decode_ms * 1e3 * (1 + 1e-6) + 1.0
+    with model.Session(small_artifact, max_seq=64, use_graph=use_graph, gpu_timestamps=2) as s:
+        r2 = s.generate(prompt, n)
+        assert r2.tokens.tolist() == base.tokens.tolist() and not r2.used_graph
+        t2, reg = r2.per_token_gpu_us, r2.gpu_region_us
+        assert t2 is not None and len(t2) == n - 1 and (t2 > 0).all()
+        assert list(reg) == [f"layer_{i}" for i in range(LAYERS)] + ["lm_head", "argmax"]
+        assert all(v > 0 for v in reg.values())
+        assert abs(sum(reg.values()) - t2.sum()) <= 1e-3 * t2.sum() + 0.05
+        # a call without decode steps leaves no timings
+        r3 = s.generate(prompt, 1)
+        assert r3.per_token_gpu_us is None and r3.gpu_region_us is None
+    with pytest.raises(model.ModelError, match="gpu_timestamps"):
+        model.Session(small_artifact, max_seq=64, gpu_timestamps=3)
