@@ -231,19 +231,53 @@ __device__ __forceinline__ int offblk(int I, int J) { return ((I - 1) * I / 2 + 
 
 constexpr float kLog2e = 1.44269504f;
 
-// The five Gram tiles of wavefront W: K K^T row block 3-W (tiles J = 0..3-W)
-// and (Q K^T)^T = K Q^T for query block W (tiles J = 0..W), accumulated
-// together so that the MFMA stream carries five independent chains.  The K
-// rows of block J are read once for both products.  A is produced transposed
-// so that each lane holds four consecutive key positions of one query row:
-// the A-operand fragment of the state scan.
-template <typename TIn, int W>
+// Gram tiles of one wavefront: the K K^T row blocks I in KMASK (tiles J =
+// 0..I each, rows 16I.., L's strict lower triangle) and, when QB >= 0, the
+// K Q^T tiles of query block QB (J = 0..QB), which must be the wavefront's own
+// Q rows (qa).  Without a split, wavefront W takes row block 3-W and query
+// block W: five tiles each.  Each tile is one MFMA chain over the 128 key
+// dims, the same whichever wavefront runs it and in whatever order, so the
+// assignment never changes a value.  The chains are accumulated together so
+// that the MFMA stream carries up to five independent ones, and the K rows of
+// block J are read once for all of them.  A is produced transposed so that
+// each lane holds four consecutive key positions of one query row: the
+// A-operand fragment of the state scan.
+struct GramTile {
+  int I, J;
+  bool q;  // K Q^T tile (query block I) rather than K K^T
+};
+template <unsigned KMASK, int QB>
+__host__ __device__ constexpr int gram_ntiles() {
+  int n = QB >= 0 ? QB + 1 : 0;
+  for (int I = 0; I < 4; ++I)
+    if ((KMASK >> I) & 1u) n += I + 1;
+  return n;
+}
+template <unsigned KMASK, int QB>
+__host__ __device__ constexpr GramTile gram_tile(int t) {
+  for (int I = 3; I >= 0; --I)
+    if ((KMASK >> I) & 1u) {
+      if (t <= I) return GramTile{I, t, false};
+      t -= I + 1;
+    }
+  return GramTile{QB, t, true};
+}
+template <unsigned KMASK, int QB>
+__host__ __device__ constexpr int gram_nj() {  // K row blocks read: 0 .. nJ-1
+  int m = QB;
+  for (int I = 0; I < 4; ++I)
+    if ((KMASK >> I) & 1u) m = I > m ? I : m;
+  return m + 1;
+}
+
+template <typename TIn, unsigned KMASK, int QB>
 __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, const float4 (&qa)[8],
                                            int li, int lg, f4v (&acc)[5]) {
   typedef RowStage<TIn> RS;
   typedef RawOf<TIn> R;
-  constexpr int Ik = 3 - W;
-  constexpr int nJ = (Ik > W ? Ik : W) + 1;
+  constexpr int NT = gram_ntiles<KMASK, QB>();
+  constexpr int nJ = gram_nj<KMASK, QB>();
+  static_assert(NT <= 5, "at most five Gram tiles per wavefront");
 #pragma unroll
   for (int t = 0; t < 5; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -255,13 +289,12 @@ __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, 
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
 #pragma unroll
-      for (int t = 0; t < 5; ++t) {
-        const bool isq = t > Ik;
-        const int J = isq ? t - Ik - 1 : t;
-        if (isq)
-          acc[t] = mfma4(elem(kb[J], e), elem(qf, e), acc[t]);
+      for (int t = 0; t < NT; ++t) {
+        const GramTile g = gram_tile<KMASK, QB>(t);
+        if (g.q)
+          acc[t] = mfma4(elem(kb[g.J], e), elem(qf, e), acc[t]);
         else
-          acc[t] = mfma4(elem(kb[Ik], e), elem(kb[J], e), acc[t]);
+          acc[t] = mfma4(elem(kb[g.I], e), elem(kb[g.J], e), acc[t]);
       }
     }
   }
@@ -270,17 +303,17 @@ __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, 
 // Epilogue of the Gram tiles: L = strict_lower(beta_i k_i.k_j Gamma_ij) into
 // LDS, A = lower(q_i.k_j scale Gamma_ij) into the workspace in fragment order
 // (with the inverse L2 norms when requested; 1 otherwise).  iq_scale is the
-// scale of query row 16W + li.
-template <int W>
+// scale of query row 16 QB + li.
+template <unsigned KMASK, int QB>
 __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG, const float* sB,
                                            const float* sIK, float iq_scale, float* sL, float* ws,
-                                           int li, int lg, int lane, bool store_a) {
-  constexpr int Ik = 3 - W;
+                                           int li, int lg, int lane) {
+  constexpr int NT = gram_ntiles<KMASK, QB>();
 #pragma unroll
-  for (int t = 0; t < 5; ++t) {
-    const bool isq = t > Ik;
-    const int J = isq ? t - Ik - 1 : t;
-    if (!isq) {
+  for (int t = 0; t < NT; ++t) {
+    const GramTile g = gram_tile<KMASK, QB>(t);
+    if (!g.q) {
+      const int Ik = g.I, J = g.J;
       const int j = 16 * J + li;
       const float ikj = sIK[j];
 #pragma unroll
@@ -290,7 +323,8 @@ __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG,
         sL[blk(Ik, J) + (4 * lg + r) * 16 + li] = (j < i) ? sB[i] * (acc[t][r] * (sIK[i] * ikj)) * dec : 0.0f;
       }
     } else {
-      // lane (li, lg) holds A[i][j], i = 16W + li, j = 16J + 4lg + r
+      // lane (li, lg) holds A[i][j], i = 16QB + li, j = 16J + 4lg + r
+      const int W = g.I, J = g.J;
       const int i = 16 * W + li;
       float o[4];
 #pragma unroll
@@ -299,8 +333,88 @@ __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG,
         const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
         o[r] = (j <= i) ? (acc[t][r] * (iq_scale * sIK[j])) * dec : 0.0f;
       }
-      if (store_a)
-        ws_store(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4, o[0], o[1], o[2], o[3]);
+      ws_store(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4, o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// Gram work of wavefront `wave` in part `part` of PARTS, dispatched to the
+// instance (KMASK, QB) that holds it.  Without a split: row block 3-w and
+// query block w (five tiles).  With one, only the wavefronts that own their
+// A block (w % PARTS == part) form K Q^T tiles, and the ten K K^T tiles are
+// spread so that no wavefront runs more than four:
+//   4 / 8 parts, owner o: o takes query block o alone; the others, in
+//     wavefront order, take row blocks {3}, {2}, {1,0}; (8 parts without an
+//     owner: {3}, {2}, {1}, {0});
+//   2 parts: part 0 -> w0 {2}+q0, w1 {3}, w2 {0}+q2, w3 {1};
+//            part 1 -> w0 {3}, w1 {1}+q1, w2 {2,0}, w3 q3.
+template <typename TIn>
+struct GramTilesOp {
+  const typename RowStage<TIn>::T* sK;
+  const float4 (&qa)[8];
+  int li, lg;
+  f4v (&acc)[5];
+  template <unsigned KM, int QB>
+  __device__ __forceinline__ void run() const {
+    gram_tiles<TIn, KM, QB>(sK, qa, li, lg, acc);
+  }
+};
+struct GramStoreOp {
+  const f4v (&acc)[5];
+  const float *sG, *sB, *sIK;
+  float iq_scale;
+  float *sL, *ws;
+  int li, lg, lane;
+  template <unsigned KM, int QB>
+  __device__ __forceinline__ void run() const {
+    gram_store<KM, QB>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane);
+  }
+};
+
+template <int PARTS, typename F>
+__device__ __forceinline__ void gram_dispatch(int part, int wave, const F& f) {
+  if constexpr (PARTS == 1) {
+    switch (wave) {
+      case 0: f.template run<8u, 0>(); break;
+      case 1: f.template run<4u, 1>(); break;
+      case 2: f.template run<2u, 2>(); break;
+      default: f.template run<1u, 3>(); break;
+    }
+  } else if constexpr (PARTS == 2) {
+    switch (part * 4 + wave) {
+      case 0: f.template run<4u, 0>(); break;
+      case 1: f.template run<8u, -1>(); break;
+      case 2: f.template run<1u, 2>(); break;
+      case 3: f.template run<2u, -1>(); break;
+      case 4: f.template run<8u, -1>(); break;
+      case 5: f.template run<2u, 1>(); break;
+      case 6: f.template run<5u, -1>(); break;
+      default: f.template run<0u, 3>(); break;
+    }
+  } else {
+    if (part < 4 && wave == part) {
+      switch (wave) {
+        case 0: f.template run<0u, 0>(); break;
+        case 1: f.template run<0u, 1>(); break;
+        case 2: f.template run<0u, 2>(); break;
+        default: f.template run<0u, 3>(); break;
+      }
+    } else {
+      const int rank = part < 4 ? wave - (wave > part ? 1 : 0) : wave;  // among the non-owners
+      if (part < 4) {
+        switch (rank) {
+          case 0: f.template run<8u, -1>(); break;
+          case 1: f.template run<4u, -1>(); break;
+          default: f.template run<3u, -1>(); break;
+        }
+      } else {
+        switch (rank) {
+          case 0: f.template run<8u, -1>(); break;
+          case 1: f.template run<4u, -1>(); break;
+          case 2: f.template run<2u, -1>(); break;
+          default: f.template run<1u, -1>(); break;
+        }
+      }
     }
   }
 }
@@ -309,9 +423,9 @@ __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG,
 // fp32 inputs stage 83 KB and run one workgroup per CU.
 //
 // PARTS workgroups per (chunk, head) (blockIdx.z = part), for launches with
-// too few (chunk, head) pairs to fill the chip: every part loads the chunk,
-// forms the Gram tiles and T (the serial part), then computes and stores only
-// its share of the record: U / W column tiles 4*part..4*part+3 (PARTS 2),
+// too few (chunk, head) pairs to fill the chip: every part loads K and the
+// value columns it needs, forms L's Gram tiles and T (the serial part), then
+// computes and stores only its share of the record: U / W column tiles 4*part..4*part+3 (PARTS 2),
 // 2*part and 2*part+1 (PARTS 4: its four wavefronts split the two tiles' row
 // blocks as {0,3} / {1,2}, 40 MFMA each instead of 160) or tile `part`
 // (PARTS 8: waves 0-1 form U, 2-3 form W, row blocks {0,3} / {1,2}, 20 MFMA
@@ -368,21 +482,31 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
     bv = p.beta[(size_t)h * p.N + t0 + tt];
     if (lane >= len) gv = bv = 0.0f;
   }
+  // Only the wavefronts that form K Q^T tiles (their own A block) need their
+  // Q rows; the others read row 0 (one cached row) so no load sits under a
+  // branch.  A split launch's part needs the value columns of its own U
+  // tiles only: 128 / PARTS of them.
   float4 qa[8];
   {
     const int row = 16 * wave + li;
-    const int rr = row < len ? row : 0;
+    const int rr = (own_block && row < len) ? row : 0;
 #pragma unroll
     for (int u = 0; u < 8; ++u) qa[u] = R::ld4(q, ((size_t)h * p.N + t0 + rr) * kD + 16 * u + 4 * lg);
   }
-  float4 kr[8], vr[8];
+  constexpr int kVCols = 128 / PARTS;
+  constexpr int kVIt = kVCols / 16;  // 16-byte V loads per thread
+  constexpr int kVq = kVCols / 4;    // threads per V row
+  float4 kr[8], vr[kVIt];
   const int c4 = (tid & 31) * 4;
+  const int vc4 = kVCols * part + (tid % kVq) * 4;
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int r = (tid >> 5) + 8 * it;
-    const size_t off = ((size_t)h * p.N + t0 + (r < len ? r : 0)) * kD + c4;
-    kr[it] = R::ld4(k, off);
-    vr[it] = R::ld4(v, off);
+    kr[it] = R::ld4(k, ((size_t)h * p.N + t0 + (r < len ? r : 0)) * kD + c4);
+    if (it < kVIt) {
+      const int rv = tid / kVq + (256 / kVq) * it;
+      vr[it < kVIt ? it : 0] = R::ld4(v, ((size_t)h * p.N + t0 + (rv < len ? rv : 0)) * kD + vc4);
+    }
   }
   // gcum (running sum in token order, deltanet_chunk.cpp:137-142): lane t adds
   // g_0 .. g_t left to right (adding +0 past t), so every lane's sum is
@@ -403,10 +527,15 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int r = (tid >> 5) + 8 * it;
-    float4 kx = kr[it], vx = vr[it];
-    if (r >= len) kx = vx = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 kx = kr[it];
+    if (r >= len) kx = make_float4(0.f, 0.f, 0.f, 0.f);
     RS::put4(sK, r, c4, kx);
-    RS::put4(sV, r, c4, vx);
+    if (it < kVIt) {
+      const int rv = tid / kVq + (256 / kVq) * it;
+      float4 vx = vr[it < kVIt ? it : 0];
+      if (rv >= len) vx = make_float4(0.f, 0.f, 0.f, 0.f);
+      RS::put4(sV, rv, vc4, vx);
+    }
   }
   __syncthreads();
 
@@ -439,22 +568,12 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
 
   // ---- Gram tiles (raw dot products; decays and scales in the epilogue)
   f4v acc[5];
-  switch (wave) {
-    case 0: gram_tiles<TIn, 0>(sK, qa, li, lg, acc); break;
-    case 1: gram_tiles<TIn, 1>(sK, qa, li, lg, acc); break;
-    case 2: gram_tiles<TIn, 2>(sK, qa, li, lg, acc); break;
-    default: gram_tiles<TIn, 3>(sK, qa, li, lg, acc); break;
-  }
+  gram_dispatch<PARTS>(part, wave, GramTilesOp<TIn>{sK, qa, li, lg, acc});
   __syncthreads();
 
   // ---- epilogue: L into LDS, A into the workspace; per-token scales
   const float iq_scale = iq * p.q_scale;  // lane li of any group: row 16*wave + li
-  switch (wave) {
-    case 0: gram_store<0>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane, own_block); break;
-    case 1: gram_store<1>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane, own_block); break;
-    case 2: gram_store<2>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane, own_block); break;
-    default: gram_store<3>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane, own_block); break;
-  }
+  gram_dispatch<PARTS>(part, wave, GramStoreOp{acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane});
   const float gL = sG[63];
   if (lg == 0 && own_block) ws[kWsQs + 16 * wave + li] = iq_scale * expf(sG[16 * wave + li]);  // the scan re-reads Q raw
   if (tid < 64) {
