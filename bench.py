@@ -286,18 +286,18 @@ def read_floor_us(stage_bytes, steps, warmup):
     sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
     offs = [sum(stage_bytes[:j]) for j in range(len(stage_bytes))]
     best = None
-    for cached in (1, 0):
+    for mode in (0, 1, 2, 3):  # bit 0: cached loads, bit 1: grid-stride walk
         for rounds in (1, 2):
             blocks = [max(1, -(-(b // 16) // (256 * 4 * rounds))) for b in stage_bytes]
 
-            def fn(i, cached=cached, blocks=blocks):
+            def fn(i, mode=mode, blocks=blocks):
                 stream = _stream()
                 for b, off, nb in zip(stage_bytes, offs, blocks):
-                    lib.spk_selftest_stream_read(bufs[i].data_ptr() + off, b, nb, cached, sink.data_ptr(), stream)
+                    lib.spk_selftest_stream_read(bufs[i].data_ptr() + off, b, nb, mode, sink.data_ptr(), stream)
             us = timed_graph(fn, steps, warmup, rotate=copies) * 1e3
             if best is None or us < best["us"]:
-                best = {"us": round(us, 2), "cached": bool(cached), "loads_per_thread": 4 * rounds,
-                        "launches": len(stage_bytes), "bytes": total}
+                best = {"us": round(us, 2), "cached": bool(mode & 1), "grid_stride": bool(mode & 2),
+                        "loads_per_thread": 4 * rounds, "launches": len(stage_bytes), "bytes": total}
     del bufs
     return best
 
@@ -450,7 +450,9 @@ def bench_copy(steps, warmup):
 def bench_ceilings(steps, warmup):
     """Measured ceilings beside the datasheet peaks: dense fp32 MFMA issue
     (8 independent v_mfma_f32_16x16x4_f32 chains per wavefront, 4 workgroups
-    per CU) and a read-only non-temporal stream over 2 GiB of HBM."""
+    per CU) and the fastest read-only stream over 2 GiB of HBM (non-temporal
+    loads; contiguous per-workgroup shares or a grid-stride walk, 32768 or
+    65536 workgroups)."""
     import torch
     from spock_amd import _lib
     lib = _lib.lib()
@@ -463,10 +465,12 @@ def bench_ceilings(steps, warmup):
     flop = blocks * 4 * 8 * iters * 2.0 * 16 * 16 * 4
     nbytes = 2 << 30
     buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
-    sink = torch.empty(32768, dtype=torch.int32, device=dev)
-    # 32768 workgroups (16 loads of 16 B per thread): the best of a 1k..32k sweep
-    _, ms_r = timed_launches(lambda i: lib.spk_selftest_stream_read(buf.data_ptr(), nbytes, 32768, 0, sink.data_ptr(),
-                                                                    stream), steps, warmup)
+    sink = torch.empty(65536, dtype=torch.int32, device=dev)
+    # mode 0: contiguous shares, 2: grid-stride walk (both non-temporal); the
+    # best of a 1k..64k workgroup sweep sits at 32k-64k for either
+    ms_r = min(timed_launches(lambda i: lib.spk_selftest_stream_read(buf.data_ptr(), nbytes, nb, mode, sink.data_ptr(),
+                                                                     stream), steps, warmup)[1]
+               for mode in (0, 2) for nb in (32768, 65536))
     return {"fp32_mfma_tflops": round(flop / (ms / 1e3) / 1e12, 1), "fp32_mfma_datasheet_tflops": FP32_MFMA_PEAK_TFLOPS,
             "hbm_read_gbs": round(nbytes / (ms_r / 1e3) / 1e9, 1), "hbm_datasheet_gbs": HBM_PEAK_GBS}
 

@@ -405,11 +405,12 @@ int spk_selftest_numerics(const float* x, int32_t n, float* out, spk_stream_t st
  * `blocks` workgroups of 4 wavefronts, each issuing 8 independent chains of
  * `iters` v_mfma_f32_16x16x4_f32 (2048 FLOP each); out holds blocks * 256
  * floats.  spk_selftest_stream_read reads `bytes` (16-byte multiple, 16-byte
- * aligned) once with `blocks` workgroups of 256 threads, with plain cached
- * loads when `cached` is nonzero, else non-temporal loads; out holds `blocks`
- * words (almost never written). */
+ * aligned) once with `blocks` workgroups of 256 threads; mode bit 0: plain
+ * cached loads (else non-temporal), bit 1: the grid walks the whole buffer in
+ * strides (else each workgroup reads its own contiguous share); out holds
+ * `blocks` words (almost never written). */
 int spk_selftest_mfma_peak(int32_t blocks, int32_t iters, float* out, spk_stream_t stream);
-int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, int32_t cached, uint32_t* out,
+int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, int32_t mode, uint32_t* out,
                              spk_stream_t stream);
 
 #ifdef __cplusplus

@@ -53,20 +53,38 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* __rest
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-// Grid-stride 16-byte reads of the whole buffer, non-temporal (NT) or plain
-// cached loads.  Each thread's XOR of what it read is stored only if it equals
-// a fixed constant, so the reads cannot be dropped and (almost) nothing is
-// written.
-template <bool NT>
+// 16-byte reads of the whole buffer, non-temporal (NT) or plain cached
+// loads, four per thread per round.  STRIDE: the grid walks the whole buffer
+// in steps of grid x 256 x 16 bytes; otherwise workgroup b reads its own
+// contiguous share.  Measured on MI355X: over 2 GiB, contiguous shares reach
+// 6.8-7.1 TB/s with non-temporal loads against 6.0-6.9 TB/s for the
+// grid-stride walk (cached loads 5.5-6.5); for reads of a few MB in one
+// launch the grid-stride walk is the faster one.  Each thread's XOR of what
+// it read is stored only if it equals a fixed constant, so the reads cannot
+// be dropped and (almost) nothing is written.
+template <bool NT, bool STRIDE>
 __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, long long n16,
                                                           uint32_t* __restrict__ out) {
+  long long lo, hi, step, lane_step;
+  if (STRIDE) {
+    lo = 0;
+    hi = n16;
+    lane_step = (long long)gridDim.x * blockDim.x;
+    step = 4 * lane_step;
+  } else {
+    const long long per = (n16 + gridDim.x - 1) / gridDim.x;
+    lo = (long long)blockIdx.x * per;
+    hi = min(lo + per, n16);
+    lane_step = 256;
+    step = 4 * 256;
+  }
+  const long long first = STRIDE ? (long long)blockIdx.x * blockDim.x + threadIdx.x : lo + threadIdx.x;
   uint32_t acc = 0;
-  const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += 4 * stride) {
+  for (long long i = first; i < hi; i += step) {
     u32x4 v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const long long j = min(i + u * stride, n16 - 1);
+      const long long j = min(i + u * lane_step, hi - 1);
       v[u] = NT ? __builtin_nontemporal_load(p + j) : p[j];
     }
 #pragma unroll
@@ -84,18 +102,20 @@ extern "C" int spk_selftest_mfma_peak(int32_t blocks, int32_t iters, float* out,
   return spk::check_launch("spk_selftest_mfma_peak");
 }
 
-extern "C" int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, int32_t cached,
+extern "C" int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, int32_t mode,
                                         uint32_t* out, spk_stream_t stream) {
   if (!p || !out) return spk::fail(SPK_ERR_NULL, "spk_selftest_stream_read: NULL pointer");
-  if (bytes < 16 || bytes % 16 || blocks <= 0 || !spk::aligned(p, 16))
-    return spk::fail(SPK_ERR_SHAPE, "spk_selftest_stream_read: bytes %zu blocks %d (16-byte multiple and alignment)",
-                     bytes, blocks);
+  if (bytes < 16 || bytes % 16 || blocks <= 0 || !spk::aligned(p, 16) || mode < 0 || mode > 3)
+    return spk::fail(SPK_ERR_SHAPE, "spk_selftest_stream_read: bytes %zu blocks %d mode %d (16-byte multiple and alignment)",
+                     bytes, blocks, mode);
   const u32x4* src = static_cast<const u32x4*>(p);
-  if (cached)
-    hipLaunchKernelGGL(stream_read_kernel<false>, dim3(blocks), dim3(256), 0, spk::to_hip(stream), src,
-                       (long long)(bytes / 16), out);
-  else
-    hipLaunchKernelGGL(stream_read_kernel<true>, dim3(blocks), dim3(256), 0, spk::to_hip(stream), src,
-                       (long long)(bytes / 16), out);
+  const long long n16 = (long long)(bytes / 16);
+  hipStream_t s = spk::to_hip(stream);
+  switch (mode) {
+    case 0: hipLaunchKernelGGL((stream_read_kernel<true, false>), dim3(blocks), dim3(256), 0, s, src, n16, out); break;
+    case 1: hipLaunchKernelGGL((stream_read_kernel<false, false>), dim3(blocks), dim3(256), 0, s, src, n16, out); break;
+    case 2: hipLaunchKernelGGL((stream_read_kernel<true, true>), dim3(blocks), dim3(256), 0, s, src, n16, out); break;
+    default: hipLaunchKernelGGL((stream_read_kernel<false, true>), dim3(blocks), dim3(256), 0, s, src, n16, out); break;
+  }
   return spk::check_launch("spk_selftest_stream_read");
 }
