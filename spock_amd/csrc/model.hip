@@ -30,8 +30,10 @@ constexpr int kPartFloats = 2 + kHeadDim;  // attention block partials: m, S, O[
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Weight loads are plain (cached) 16-byte loads: non-temporal loads measured
-// up to 2x slower for decode-sized matrices (a few MB) on MI355X.
+// Weight loads are plain (cached) 16-byte loads: for decode-sized matrices (a
+// few MB per launch) non-temporal loads measured slower on MI355X, up to 2x for
+// a single GEMV and 689.4 vs 684.7 us per config-4 token, although they stream
+// faster over hundreds of MB.
 __device__ __forceinline__ uint4 ld_w(const uint4* p) { return *p; }
 
 __device__ __forceinline__ void unpack8(const uint4& u, float* f) {
