@@ -547,26 +547,55 @@ DecodeResult Qwen35Session::decode(const std::vector<std::uint32_t>& prompt_toke
                                std::to_string(max_seq_));
     if (std::size_t(history_len_) + n > history_cap_) throw std::runtime_error("decode: token history full");
     const bool regions = gpu_ts_ == GpuTimestamps::per_region;
-    const std::size_t NL = layers_.size(), per_step = NL + 3;  // events of one step: start, layers, lm_head, argmax
-    if (regions)
-      ensure_ts_events(std::size_t(n) * per_step);
-    else if (gpu_ts_ == GpuTimestamps::per_token)
-      ensure_ts_events(std::size_t(n) + 1);
+    const bool timed = gpu_ts_ != GpuTimestamps::off;
+    // Events of one step: per region, start + one after each layer, lm_head
+    // and argmax; per token, start and end.  Steps are timed in batches of
+    // kTsBatch over two alternating event sets: the host reads batch k (its
+    // last event completed) while the GPU runs batch k+1, so the pool stays
+    // at 2 x kTsBatch steps' events however many tokens are generated.
+    const std::size_t NL = layers_.size();
+    const std::size_t per_step = regions ? NL + 3 : 2;
+    constexpr std::uint32_t kTsBatch = 64;
+    if (timed) ensure_ts_events(2 * kTsBatch * per_step);
+    if (regions) {
+      for (std::size_t L = 0; L < NL; ++L) r.gpu_region_us.emplace_back("layer_" + std::to_string(L), 0.0);
+      r.gpu_region_us.emplace_back("lm_head", 0.0);
+      r.gpu_region_us.emplace_back("argmax", 0.0);
+    }
+    auto step_events = [&](std::uint32_t i) { return &ts_events_[(((i / kTsBatch) & 1u) * kTsBatch + i % kTsBatch) * per_step]; };
+    auto us = [&](hipEvent_t a, hipEvent_t b) {
+      float v = 0.0f;
+      hip_check(hipEventElapsedTime(&v, a, b), "hipEventElapsedTime");
+      return double(v) * 1000.0;
+    };
+    std::uint32_t collected = 0;  // steps whose times have been read
+    auto collect = [&](std::uint32_t upto) {  // reads steps [collected, upto), in order
+      if (collected >= upto) return;
+      hip_check(hipEventSynchronize(step_events(upto - 1)[per_step - 1]), "hipEventSynchronize");
+      for (; collected < upto; ++collected) {
+        hipEvent_t* e = step_events(collected);
+        r.per_token_gpu_us.push_back(us(e[0], e[per_step - 1]));
+        if (regions)
+          for (std::size_t k = 0; k < NL + 2; ++k) r.gpu_region_us[k].second += us(e[k], e[k + 1]);
+      }
+    };
     if (!regions) ensure_graph();  // recorded outside the timed region
     EventTimer ev;
     const auto t1 = std::chrono::steady_clock::now();
     hip_check(hipEventRecord(ev.a, stream_), "hipEventRecord");
     for (std::uint32_t i = 0; i < n; ++i) {
+      // this step reuses the event set of step i - 2 kTsBatch: read that batch first
+      if (timed && i % kTsBatch == 0 && i >= 2 * kTsBatch) collect(i - kTsBatch);
       if (regions) {
-        marks_ = &ts_events_[std::size_t(i) * per_step];
+        marks_ = step_events(i);
         enqueue_decode_step();
         marks_ = nullptr;
       } else {
-        if (gpu_ts_ == GpuTimestamps::per_token) hip_check(hipEventRecord(ts_events_[i], stream_), "hipEventRecord");
+        if (timed) hip_check(hipEventRecord(step_events(i)[0], stream_), "hipEventRecord");
         run_decode_step();
+        if (timed) hip_check(hipEventRecord(step_events(i)[1], stream_), "hipEventRecord");
       }
     }
-    if (gpu_ts_ == GpuTimestamps::per_token) hip_check(hipEventRecord(ts_events_[n], stream_), "hipEventRecord");
     hip_check(hipEventRecord(ev.b, stream_), "hipEventRecord");
     std::vector<std::int32_t> out(n);
     hip_check(hipMemcpyAsync(out.data(), history_.get<std::int32_t>() + 64 + history_len_, n * 4,
@@ -575,23 +604,7 @@ DecodeResult Qwen35Session::decode(const std::vector<std::uint32_t>& prompt_toke
     hip_check(hipStreamSynchronize(stream_), "decode");
     r.decode_ms = ms_since(t1);
     r.gpu_decode_us = ev.ms() * 1000.0;
-    auto us = [&](std::size_t a, std::size_t b) {
-      float v = 0.0f;
-      hip_check(hipEventElapsedTime(&v, ts_events_[a], ts_events_[b]), "hipEventElapsedTime");
-      return double(v) * 1000.0;
-    };
-    if (gpu_ts_ == GpuTimestamps::per_token) {
-      for (std::uint32_t i = 0; i < n; ++i) r.per_token_gpu_us.push_back(us(i, i + 1));
-    } else if (regions) {
-      for (std::size_t L = 0; L < NL; ++L) r.gpu_region_us.emplace_back("layer_" + std::to_string(L), 0.0);
-      r.gpu_region_us.emplace_back("lm_head", 0.0);
-      r.gpu_region_us.emplace_back("argmax", 0.0);
-      for (std::uint32_t i = 0; i < n; ++i) {
-        const std::size_t b = std::size_t(i) * per_step;
-        r.per_token_gpu_us.push_back(us(b, b + NL + 2));
-        for (std::size_t k = 0; k < NL + 2; ++k) r.gpu_region_us[k].second += us(b + k, b + k + 1);
-      }
-    }
+    if (timed) collect(n);
     pos_host_ += static_cast<std::int32_t>(n);
     history_len_ += n;
     for (auto t : out) r.generated_tokens.push_back(static_cast<std::uint32_t>(t));

@@ -132,26 +132,27 @@ def test_long_generation_past_8192_tokens(dev, small_artifact):
             s.generate(_prompt(8), 8994)
 
 
-@pytest.mark.parametrize("use_graph", [True, False])
-def test_gpu_timestamps(dev, small_artifact, use_graph):
+@pytest.mark.parametrize("use_graph,n", [(True, 12), (False, 12), (True, 200)])
+def test_gpu_timestamps(dev, small_artifact, use_graph, n):
     """Per-step and per-region GPU times (DecodeResult::per_token_gpu_us and
     gpu_region_us, vk_decode.hpp:19-20): same tokens as an untimed session;
     one time per decode step; the regions of a step tile it exactly, in step
-    order, so their sums equal the per-step sum."""
+    order, so their sums equal the per-step sum.  200 tokens run past two
+    64-step event batches, so the event sets are reused."""
     from spock_amd import model
-    print(f"[session gpu timestamps graph={use_graph}]", flush=True)
-    prompt, n = _prompt(20), 12
-    with model.Session(small_artifact, max_seq=64, use_graph=use_graph) as s:
+    print(f"[session gpu timestamps graph={use_graph} n={n}]", flush=True)
+    prompt = _prompt(20)
+    with model.Session(small_artifact, max_seq=256, use_graph=use_graph) as s:
         base = s.generate(prompt, n)
         assert base.per_token_gpu_us is None and base.gpu_region_us is None
-    with model.Session(small_artifact, max_seq=64, use_graph=use_graph, gpu_timestamps=1) as s:
+    with model.Session(small_artifact, max_seq=256, use_graph=use_graph, gpu_timestamps=1) as s:
         r = s.generate(prompt, n)
     assert r.tokens.tolist() == base.tokens.tolist() and r.used_graph == use_graph
     assert r.gpu_region_us is None
     t = r.per_token_gpu_us
     assert t is not None and len(t) == n - 1 and (t > 0).all()
     assert 0.5 * r.gpu_decode_ms * 1e3 <= t.sum() <= r.gpu_decode_ms * 1e3 * (1 + 1e-6) + 1.0
-    with model.Session(small_artifact, max_seq=64, use_graph=use_graph, gpu_timestamps=2) as s:
+    with model.Session(small_artifact, max_seq=256, use_graph=use_graph, gpu_timestamps=2) as s:
         r2 = s.generate(prompt, n)
         assert r2.tokens.tolist() == base.tokens.tolist() and not r2.used_graph
         t2, reg = r2.per_token_gpu_us, r2.gpu_region_us
