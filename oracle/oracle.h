@@ -20,13 +20,22 @@
  *   orc_delta_recurrence_f64    closed form of the gated delta rule; brute force
  *   orc_recurrent               reference GPU capture tests/data/layer0_step1_* of
  *                               deltanet_recurrent.comp (<=2 fp16 ulp)
- *   orc_conv_l2_qk              fp64 restatement + unit-norm invariant;
- *                               conv/L2 weights of the capture are absent, so the
- *                               captured chain is "parity unpinned" beyond that
- *   orc_recurrent_gbeta_norm_gate  beta pinned by layer0 g_beta capture (sigmoid
- *                               of captured b); recurrence pinned as orc_recurrent;
- *                               g and the norm-gate weight pinned only by fp64
- *                               restatement (weights absent: partially unpinned)
+ *   orc_conv_l2_qk              T decode steps against torch's depthwise
+ *                               conv1d (HF's causal-conv formulation) + SiLU +
+ *                               fp16 + per-head L2 in fp64; one-hot taps select
+ *                               the lagged input (tests/test_oracle_decode_pins.py)
+ *   orc_gbeta                   g at a + dt_bias = 0 equals -e^{A_log} ln 2;
+ *                               torch softplus / sigmoid in fp64 below softplus's
+ *                               threshold; the shader's large-argument limits
+ *   orc_norm_gate_f16 / orc_norm_gate_row  the reference GPU captures
+ *                               layer0_step1_dn_core + dn_z -> dn_gated: a norm
+ *                               weight fitted on one head reproduces the other 15
+ *                               heads' fp16 bits; wrong variants (no fp16 rounding
+ *                               of w*n, sigmoid gate, sum instead of mean) fail;
+ *                               the fused row equals the unfused form
+ *   orc_recurrent_gbeta_norm_gate  composed of orc_gbeta, the recurrence (as
+ *                               orc_recurrent) and orc_norm_gate_row, each pinned
+ *                               above; beta also by the layer0 g_beta capture
  *   orc_matvec_f16 / orc_lm_head  fp64 dot products -> one RNE rounding (<=1 ulp)
  *   orc_argmax_f16              brute-force emulation of argmax.comp's lane/tree
  *                               order on crafted tie patterns
