@@ -29,10 +29,12 @@
  *                               threshold; the shader's large-argument limits
  *   orc_norm_gate_f16 / orc_norm_gate_row  the reference GPU captures
  *                               layer0_step1_dn_core + dn_z -> dn_gated: a norm
- *                               weight fitted on one head reproduces the other 15
- *                               heads' fp16 bits; wrong variants (no fp16 rounding
- *                               of w*n, sigmoid gate, sum instead of mean) fail;
- *                               the fused row equals the unfused form
+ *                               weight fitted with each head held out reproduces
+ *                               it within 1 fp16 ulp (2 for head 0, whose core is
+ *                               subnormal); wrong variants (sigmoid gate, sum
+ *                               instead of mean, one norm across heads, eps
+ *                               outside the root) miss by > 100 ulp; the fused
+ *                               row equals the unfused form
  *   orc_recurrent_gbeta_norm_gate  composed of orc_gbeta, the recurrence (as
  *                               orc_recurrent) and orc_norm_gate_row, each pinned
  *                               above; beta also by the layer0 g_beta capture
