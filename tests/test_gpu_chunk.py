@@ -275,3 +275,38 @@ def test_many_sequences_device_table_path(dev, oracle):
     gc, gs = _run(dev, inp, cu=cu)
     assert max_rel(gc, cc) <= TOL
     assert max_rel(gs, cs) <= TOL
+
+
+def _random_case(i):
+    """Seeded random pack: head count, ragged lengths (empty, sub-chunk and
+    chunk-boundary lengths included), input dtype, L2 inside the kernel or
+    not, initial state or not."""
+    rng = np.random.default_rng(1000 + i)
+    H = int(rng.choice([1, 2, 3, 5, 8, 16]))
+    S = int(rng.integers(1, 7))
+    choices = [0, 1, 2, 31, 63, 64, 65, 127, 128, 129, 191, 200, 256, 300]
+    lens = [int(rng.choice(choices)) if rng.random() < 0.5 else int(rng.integers(1, 320)) for _ in range(S)]
+    if sum(lens) == 0:
+        lens[0] = 17
+    return H, lens, bool(rng.random() < 0.5), bool(rng.random() < 0.5), bool(rng.random() < 0.5)
+
+
+@pytest.mark.parametrize("i", range(20))
+def test_random_packs_against_oracle(dev, oracle, i):
+    """Seeded random packs through the packed launch (host sequence table,
+    split intra parts for the small ones) against the oracle's per-sequence
+    chunk rule, to the north-star tolerance."""
+    from spock_amd import synth
+    H, lens, l2, init, half = _random_case(i)
+    print(f"[random pack {i}: H={H} lens={lens} l2={l2} init={init} half={half}]", flush=True)
+    cu = synth.cu_seqlens_from(lens)
+    inp = synth.chunk_inputs(H, int(cu[-1]), seed=300 + i, l2=not l2)
+    if half:
+        for n in ("q", "k", "v"):
+            inp[n] = inp[n].astype(np.float16).astype(np.float32)
+    st0 = (np.random.default_rng(i).normal(0, 0.05, (len(lens), H, 128, 128)).astype(np.float32)
+           if init else None)
+    cc, cs = oracle.chunk_rule_varlen(**inp, cu=cu, init=st0, l2=l2)
+    gc, gs = _run(dev, inp, init=st0, cu=cu, l2=l2, half=half)
+    assert max_rel(gc, cc) <= TOL
+    assert max_rel(gs, cs) <= TOL
