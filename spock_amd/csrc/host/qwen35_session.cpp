@@ -587,9 +587,13 @@ DecodeResult Qwen35Session::decode(const std::vector<std::uint32_t>& prompt_toke
       // this step reuses the event set of step i - 2 kTsBatch: read that batch first
       if (timed && i % kTsBatch == 0 && i >= 2 * kTsBatch) collect(i - kTsBatch);
       if (regions) {
+        // cleared on every exit, so a later graph capture never records events
+        struct MarksGuard {
+          hipEvent_t*& m;
+          ~MarksGuard() { m = nullptr; }
+        } guard{marks_};
         marks_ = step_events(i);
         enqueue_decode_step();
-        marks_ = nullptr;
       } else {
         if (timed) hip_check(hipEventRecord(step_events(i)[0], stream_), "hipEventRecord");
         run_decode_step();
