@@ -11,8 +11,9 @@
 //
 // Two launches:
 //  1. chunk_intra_kernel -- one workgroup per (chunk, head), all chunks of all
-//     sequences in parallel.  Every global load is issued up front; K and V
-//     rows are staged in LDS in the input type (50 KB for fp16, so three
+//     sequences in parallel.  Every global load is issued up front; K rows
+//     are staged in LDS in the input type, V goes straight into the
+//     registers of the U products' B operand (34 KB of LDS for fp16, so four
 //     workgroups share a CU).  K K^T and Q K^T are 16x16x4 fp32 MFMA tiles,
 //     five independent accumulators per wavefront; T is inverted blockwise (4
 //     diagonal 16x16 blocks by per-lane forward substitution, written over L's,
@@ -181,7 +182,40 @@ template <> struct RawOf<uint16_t> {
   }
 };
 
-// K and V rows staged in LDS in the input type (fp16 rows stay fp16) with a
+// V operand of the U products: rows 16u+4lg+e (u, e = 0..3) of one value
+// column, read through a buffer resource of the chunk's len rows, so rows past
+// the chunk read 0 (the hardware range check) with no clamp or select.  fp16
+// rows are packed two to a register.
+template <typename TIn> struct VOperand;
+template <> struct VOperand<float> {
+  float x[4][4];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int voff) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        x[u][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + e * kD * 4, u * 16 * kD * 4, 0));
+  }
+  __device__ __forceinline__ float get(int u, int e) const { return x[u][e]; }
+};
+template <> struct VOperand<uint16_t> {
+  uint32_t x[4][2];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int voff) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, voff + e * kD * 2, u * 16 * kD * 2, 0);
+        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(r, voff + (e + 1) * kD * 2, u * 16 * kD * 2, 0);
+        x[u][e / 2] = lo | (hi << 16);
+      }
+  }
+  __device__ __forceinline__ float get(int u, int e) const {
+    return spk::h2f((uint16_t)((e & 1) ? x[u][e / 2] >> 16 : x[u][e / 2] & 0xffffu));
+  }
+};
+
+// K rows staged in LDS in the input type (fp16 rows stay fp16) with a
 // row stride of 132 elements: the 16 rows of one 16-lane group of an 8-byte
 // operand read (fp16), or the 8 rows of an 8-lane group of a 16-byte read
 // (fp32), start on distinct bank groups.
@@ -419,8 +453,11 @@ __device__ __forceinline__ void gram_dispatch(int part, int wave, const F& f) {
   }
 }
 
-// fp16 inputs: 3 workgroups per CU (50 KB of LDS each), so at most 168 VGPRs;
-// fp32 inputs stage 83 KB and run one workgroup per CU.
+// fp16 inputs, one workgroup per (chunk, head): 4 workgroups per CU (34 KB of
+// LDS each), so at most 128 VGPRs (with V staged in LDS as well, 50 KB and
+// three per CU measured 0.921 vs 0.907 ms for config 2); the split forms run
+// at most one workgroup per CU and keep a 168-VGPR budget.  fp32 inputs stage
+// 51 KB and are compiled for one workgroup per CU.
 //
 // PARTS workgroups per (chunk, head) (blockIdx.z = part), for launches with
 // too few (chunk, head) pairs to fill the chip: every part loads K and the
@@ -433,11 +470,10 @@ __device__ __forceinline__ void gram_dispatch(int part, int wave, const F& f) {
 // Each value is computed by the same operation sequence whatever PARTS is, so
 // the record is bit-identical.
 template <typename TIn, int PARTS>
-__global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_kernel(ChunkParams p) {
+__global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) void chunk_intra_kernel(ChunkParams p) {
   typedef RawOf<TIn> R;
   typedef RowStage<TIn> RS;
   __shared__ __align__(16) typename RS::T sK[64 * RS::kLd];  // K rows, raw
-  __shared__ __align__(16) typename RS::T sV[64 * RS::kLd];  // V rows, raw
   __shared__ __align__(16) float sL[10 * 256];  // L blocks; diagonal blocks become T's
   __shared__ __align__(16) float sT[6 * 256];   // off-diagonal T blocks
   __shared__ __align__(16) float sG[64];   // gcum
@@ -473,8 +509,8 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   float* ws = p.ws + ((size_t)gchunk * p.H + h) * kWsStride;
 
   // ---- every global load first: g/beta (wave 0), Q row block `wave` as MFMA
-  // A-operand registers, 8 K and 8 V row segments per thread.  Padding rows
-  // read row 0 and are zeroed when staged.
+  // A-operand registers, 8 K row segments per thread (padding rows read row 0
+  // and are zeroed when staged), the V elements of the U products.
   float gv = 0.0f, bv = 0.0f;
   if (wave == 0) {
     const int tt = lane < len ? lane : 0;
@@ -493,20 +529,28 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
 #pragma unroll
     for (int u = 0; u < 8; ++u) qa[u] = R::ld4(q, ((size_t)h * p.N + t0 + rr) * kD + 16 * u + 4 * lg);
   }
-  constexpr int kVCols = 128 / PARTS;
-  constexpr int kVIt = kVCols / 16;  // 16-byte V loads per thread
-  constexpr int kVq = kVCols / 4;    // threads per V row
-  float4 kr[8], vr[kVIt];
+  float4 kr[8];
   const int c4 = (tid & 31) * 4;
-  const int vc4 = kVCols * part + (tid % kVq) * 4;
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int r = (tid >> 5) + 8 * it;
     kr[it] = R::ld4(k, ((size_t)h * p.N + t0 + (r < len ? r : 0)) * kD + c4);
-    if (it < kVIt) {
-      const int rv = tid / kVq + (256 / kVq) * it;
-      vr[it < kVIt ? it : 0] = R::ld4(v, ((size_t)h * p.N + t0 + (rv < len ? rv : 0)) * kD + vc4);
-    }
+  }
+  // V enters only the U products, as their B operand: lane (li, lg) loads
+  // V[16u+4lg+s][16 ct+li] of its column tiles ct straight into registers
+  // (16 lanes read 32 contiguous bytes of a row), so V needs no LDS stage.
+  // Padding rows read 0 (VOperand's buffer range check).
+  constexpr int kTilesPerWave = PARTS == 1 ? 2 : 1;
+  auto u_tile = [&](int jj) {
+    return PARTS == 1 ? 2 * wave + jj : PARTS == 2 ? 4 * part + wave : PARTS == 4 ? 2 * part + (wave & 1) : part;
+  };
+  VOperand<TIn> vd[kTilesPerWave];
+  {
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<TIn*>(v + ((size_t)h * p.N + t0) * kD), 0, len * kD * (int)sizeof(TIn), kBufDword3);
+#pragma unroll
+    for (int jj = 0; jj < kTilesPerWave; ++jj)
+      vd[jj].load(vr, (4 * lg * kD + 16 * u_tile(jj) + li) * (int)sizeof(TIn));
   }
   // gcum (running sum in token order, deltanet_chunk.cpp:137-142): lane t adds
   // g_0 .. g_t left to right (adding +0 past t), so every lane's sum is
@@ -530,12 +574,6 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
     float4 kx = kr[it];
     if (r >= len) kx = make_float4(0.f, 0.f, 0.f, 0.f);
     RS::put4(sK, r, c4, kx);
-    if (it < kVIt) {
-      const int rv = tid / kVq + (256 / kVq) * it;
-      float4 vx = vr[it < kVIt ? it : 0];
-      if (rv >= len) vx = make_float4(0.f, 0.f, 0.f, 0.f);
-      RS::put4(sV, rv, vc4, vx);
-    }
   }
   __syncthreads();
 
@@ -632,13 +670,9 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
   // operand as it is read.  W is produced transposed so that each lane holds
   // four consecutive key dims of one token: the A-operand fragment of the
   // state scan.
-  constexpr int kTilesPerWave = PARTS == 1 ? 2 : 1;
 #pragma unroll
   for (int jj = 0; jj < kTilesPerWave; ++jj) {
-    const int ct = PARTS == 1   ? 2 * wave + jj
-                   : PARTS == 2 ? 4 * part + wave
-                   : PARTS == 4 ? 2 * part + (wave & 1)
-                                : part;
+    const int ct = u_tile(jj);
     // row blocks I of this wave: {0,3} or {1,2} (4 parts: by wave / 2; 8
     // parts: by wave % 2, waves 0-1 forming U and 2-3 forming W)
     const bool odd_rows = PARTS == 4 ? (wave >> 1) != 0 : (wave & 1) != 0;
@@ -659,7 +693,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 3 : 1) void chunk_intra_ker
       float vb[4], kb[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        vb[s] = RS::get1(sV, t + s, n) * elem(bb, s);
+        vb[s] = vd[jj].get(u, s) * elem(bb, s);
         kb[s] = RS::get1(sK, t + s, n) * elem(be, s);
       }
 #pragma unroll
