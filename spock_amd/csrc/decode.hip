@@ -82,6 +82,7 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
   __shared__ float s_q[128], s_k[128], s_v[128], s_delta[128];
   __shared__ float s_part[32][128];
   __shared__ float s_gb[2];
+  __shared__ float s_zs[128];  // SiLU(z) of the norm-gate, formed off the chain
 
   const int c4 = tid & 31;  // owns columns 4*c4 .. 4*c4+3
   const int rq = tid >> 5;  // owns row groups G*rq .. G*rq+G-1, i.e. rows M*rq .. M*rq+M-1
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
       a_log = p.alb[(p.layer * nh + h) * 2];
       dt_bias = p.alb[(p.layer * nh + h) * 2 + 1];
     }
-    if (NORM_GATE) {  // used by wave 0
+    if (NORM_GATE) {  // z: the SiLU wave (into s_zs); norm weights: wave 0
       const uint16_t* zr = p.z + (long long)seq * p.z_stride + h * 128;
       z16[0] = zr[lane];
       z16[1] = zr[lane + 64];
@@ -147,6 +148,13 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
       s_gb[0] = -spk::expf_det(a_log) * sp;
       s_gb[1] = 1.0f / (1.0f + spk::expf_det(-bv));
     }
+  }
+  if (REC && NORM_GATE && wave == (WAVES > 4 ? 4 : 3)) {
+    // the gate's SiLU(z) depends on nothing the step computes: an idle wave
+    // (wave 4; wave 3 beside g/beta when there are only four) forms it while
+    // waves 0-2 run the conv, so the output phase only reads it
+    s_zs[lane] = spk::silu_det(spk::h2f(z16[0]));
+    s_zs[lane + 64] = spk::silu_det(spk::h2f(z16[1]));
   }
   if (CONV) {
     if (wave < 3) {
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
         const float o = half ? ob : oa;
         const float normed = o * r;
         const float weighted = spk::h2f(spk::f2h(nw[half] * normed));
-        out[j] = spk::f2h(weighted * spk::silu_det(spk::h2f(z16[half])));
+        out[j] = spk::f2h(weighted * s_zs[j]);
       }
     } else {
       out[lane] = spk::f2h(oa);
