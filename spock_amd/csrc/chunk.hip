@@ -19,7 +19,7 @@
 //     diagonal 16x16 blocks by per-lane forward substitution, written over L's,
 //     off-diagonal blocks T_IJ = -T_II sum_M L_IM T_MJ as MFMA products); U
 //     and W are MFMA products over the nonzero blocks of T with beta and the
-//     decays applied to the B operand as it is read.  U^T, W, A, raw K^T and
+//     decays applied to the B operand as it is read.  U^T, W, A and the
 //     per-token scales go to the workspace.
 //  2. chunk_state_kernel -- one workgroup per (sequence, head, 16-column tile
 //     of the value dim): columns of S evolve independently, so the sequential
@@ -66,20 +66,19 @@ constexpr int kD = 128;
 //   W   [M 4][u 8][lane][4]   W[16M+li][16u+4lg+e]                 fp32
 //   U   [tile 8][M 4][lane][4] U[16M+4lg+e][16 tile+li]             fp32
 //   A   [M 4][J 4][lane][4]   A[16M+li][16J+4lg+e], blocks J <= M   fp32
-//   KT  [M 4][v 8][lane][4]   K[16(v%4)+4lg+e][32M+16(v/4)+li]     input type
 //   Qs  [64] Q scale (q_scale iq e^gcum)   Ks [64] e^{gL - gcum} ik
 //   Misc[0] e^{gL}
 // A's blocks above the diagonal (zero) are neither stored nor multiplied, and
-// the scan reads raw Q from the input rows rather than from a record copy:
-// 22 of the record's ~115 KB (fp16 inputs) less for the intra kernel to write.
+// the scan reads raw Q and raw K from the input rows rather than from record
+// copies: 38 of the ~115 KB a record would hold (fp16 inputs) that the intra
+// kernel does not write.
 constexpr int kWsW = 0;
 constexpr int kWsU = 8192;
 constexpr int kWsA = 16384;
-constexpr int kWsKT = 20480;
-constexpr int kWsQs = 36864;
-constexpr int kWsKs = 36928;
-constexpr int kWsMisc = 36992;
-constexpr int kWsStride = 37056;  // 148224 bytes, a multiple of 256
+constexpr int kWsQs = 20480;
+constexpr int kWsKs = 20544;
+constexpr int kWsMisc = 20608;
+constexpr int kWsStride = 20672;  // 82688 bytes, a multiple of 256
 // Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
 // which untyped loads/stores need for the num_records range check to apply.
 constexpr int kBufDword3 = 0x00020000;
@@ -168,6 +167,14 @@ template <typename TIn> struct RawOf;
 template <> struct RawOf<float> {
   static __device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
   static __device__ __forceinline__ float4 cvt4(const float4& r) { return r; }
+  // two adjacent elements of a row through a buffer resource (0 past its range)
+  typedef float2 Pair;
+  static __device__ __forceinline__ Pair ld_pair(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+  }
+  static __device__ __forceinline__ float lo(Pair v) { return v.x; }
+  static __device__ __forceinline__ float hi(Pair v) { return v.y; }
 };
 template <> struct RawOf<uint16_t> {
   // 4 halves kept as two 32-bit words in .x/.y of a float4
@@ -180,6 +187,12 @@ template <> struct RawOf<uint16_t> {
     return make_float4(spk::h2f((uint16_t)(x & 0xffffu)), spk::h2f((uint16_t)(x >> 16)),
                        spk::h2f((uint16_t)(y & 0xffffu)), spk::h2f((uint16_t)(y >> 16)));
   }
+  typedef uint32_t Pair;
+  static __device__ __forceinline__ Pair ld_pair(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  }
+  static __device__ __forceinline__ float lo(Pair v) { return spk::h2f((uint16_t)(v & 0xffffu)); }
+  static __device__ __forceinline__ float hi(Pair v) { return spk::h2f((uint16_t)(v >> 16)); }
 };
 
 // V operand of the U products: rows 16u+4lg+e (u, e = 0..3) of one value
@@ -720,19 +733,6 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
     }
     __builtin_amdgcn_sched_barrier(0);  // one column tile's operands live at a time
   }
-
-  // ---- K^T fragments of the state update, raw input type: fragment
-  // f = 64 v + l of wavefront M holds K[16(v%4)+4lg .. +3][32M+16(v/4)+li]
-  typename RS::T* kt = reinterpret_cast<typename RS::T*>(ws + kWsKT);
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    if (((it >> 1) % PARTS) != part) continue;  // fragment block M = it / 2
-    const int f = tid + 256 * it;  // [M][v][lane]
-    const int l = f & 63;
-    const int v8 = (f >> 6) & 7;
-    const int Mw = f >> 9;
-    RS::col4_to(sK, 16 * (v8 & 3) + 4 * (l >> 4), 32 * Mw + 16 * (v8 >> 2) + (l & 15), kt + f * 4);
-  }
 }
 
 // Sequence with rank `slot` by decreasing length (ties: lower index first).
@@ -760,9 +760,10 @@ struct ScanEarly {
   float4 w[8];  // W rows: token 16M+li, key dims 16u+4lg..+3
   float4 q[8];  // raw Q rows, same map
 };
+template <typename TIn>
 struct ScanLate {
   float4 a[4];   // A rows: token 16M+li, tokens 16u+4lg..+3
-  float4 kt[8];  // raw K^T rows 32M+16(v/4)+li, tokens 16(v%4)+4lg..+3
+  typename RawOf<TIn>::Pair kp[16];  // raw K[16u+4lg+k][32M+2li .. +1], index 4u+k
   float4 u;      // U^T: column n0+li, tokens 16M+4lg..+3
   float4 ks;     // Ks of tokens 16M+4lg..+3
   float4 qs;     // Qs of tokens 16M+4lg..+3
@@ -859,22 +860,32 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
       e.q[u] = R::ld4(qrow, 16 * u);
     }
   };
-  auto load_late = [&](ScanLate& l, int c) {
+  // Stage D's K operand comes straight from the input rows: kp[4u+k] holds
+  // K[16u+4lg+k][32M+2li .. 32M+2li+1] (16 lanes read 64 or 128 contiguous
+  // bytes of a row), through a buffer resource of the chunk's len rows, so
+  // padding rows read 0.  Issued last: stage D uses them last, and a wave's
+  // loads complete in issue order.
+  const TIn* kin = static_cast<const TIn*>(p.k) + ((size_t)h * p.N + t_begin) * kD;
+  auto load_late = [&](ScanLate<TIn>& l, int c) {
     const float* ws = record(c);
-    const TIn* kt = reinterpret_cast<const TIn*>(ws + kWsKT);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       l.a[u] = *reinterpret_cast<const float4*>(ws + kWsA + ((M * 4 + u) * 64 + lane) * 4);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) l.kt[u] = R::ld4(kt, ((M * 8 + u) * 64 + lane) * 4);
     l.u = *reinterpret_cast<const float4*>(ws + kWsU + ((tile * 4 + M) * 64 + lane) * 4);
     l.ks = *reinterpret_cast<const float4*>(ws + kWsKs + 16 * M + 4 * lg);
     l.qs = *reinterpret_cast<const float4*>(ws + kWsQs + 16 * M + 4 * lg);
     l.gle = ws[kWsMisc];
+    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<TIn*>(kin + (size_t)c * kC * kD), 0, min(kC, L - c * kC) * kD * (int)sizeof(TIn), kBufDword3);
+    const int voff = (4 * lg * kD + 32 * M + 2 * li) * (int)sizeof(TIn);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) l.kp[4 * u + k] = R::ld_pair(kr, voff, (16 * u + k) * kD * (int)sizeof(TIn));
   };
 
   // zero_s: S is zero (first chunk without an initial state)
-  auto step = [&](const ScanEarly& e, const ScanLate& l, int c, auto zero_s) {
+  auto step = [&](const ScanEarly& e, const ScanLate<TIn>& l, int c, auto zero_s) {
     const int tok0 = t_begin + c * kC;
     const int len = min(kC, L - c * kC);
 
@@ -954,31 +965,35 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(aq[r]), out,
                                             ((16 * M + 4 * lg + r) * kD + n0 + li) * (int)sizeof(float), 0, 0);
 
-    // ---- stage D: S rows 32M+16j.. <- e^{gL} S + K^T (Ks v_new), j = 0, 1
+    // ---- stage D: S^T <- e^{gL} S^T + (Ks v_new)^T K, computed transposed so
+    // that K is the B operand read from its rows: lane (li, lg) holds
+    // S^T[column 4lg+r][key 32M+2li+t] in s0 (t = 0) and s1 (t = 1).  Each
+    // output element gets the same products in the same order as
+    // K^T (Ks v_new) would.
     f4v s0, s1;
-    {
-      const float4 x0 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 32 * M + 4 * lg]);
-      const float4 x1 = *reinterpret_cast<const float4*>(&sST[li * kLdST + 32 * M + 16 + 4 * lg]);
-      s0 = f4v{x0.x * l.gle, x0.y * l.gle, x0.z * l.gle, x0.w * l.gle};
-      s1 = f4v{x1.x * l.gle, x1.y * l.gle, x1.z * l.gle, x1.w * l.gle};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float2 x = *reinterpret_cast<const float2*>(&sST[(4 * lg + r) * kLdST + 32 * M + 2 * li]);
+      s0[r] = x.x * l.gle;
+      s1[r] = x.y * l.gle;
     }
     float4 vs[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) vs[u] = *reinterpret_cast<const float4*>(&sVS[li * kLdVT + 16 * u + 4 * lg]);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const float4 k0 = R::cvt4(l.kt[u]);
-      const float4 k1 = R::cvt4(l.kt[4 + u]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        s0 = mfma4(elem(k0, k), elem(vs[u], k), s0);
-        s1 = mfma4(elem(k1, k), elem(vs[u], k), s1);
+        const float a = elem(vs[u], k);
+        s0 = mfma4(a, R::lo(l.kp[4 * u + k]), s0);
+        s1 = mfma4(a, R::hi(l.kp[4 * u + k]), s1);
       }
     }
     // every wave read sST (stage A) before the barrier above and only its own
-    // rows here, so the rows are replaced in place
-    *reinterpret_cast<float4*>(&sST[li * kLdST + 32 * M + 4 * lg]) = make_float4(s0[0], s0[1], s0[2], s0[3]);
-    *reinterpret_cast<float4*>(&sST[li * kLdST + 32 * M + 16 + 4 * lg]) = make_float4(s1[0], s1[1], s1[2], s1[3]);
+    // keys here, so they are replaced in place
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<float2*>(&sST[(4 * lg + r) * kLdST + 32 * M + 2 * li]) = make_float2(s0[r], s1[r]);
     __syncthreads();
   };
 
@@ -989,7 +1004,7 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   // peeled loop for every launch, made the fp16 instance spill more).
   using NZ = std::integral_constant<bool, false>;
   ScanEarly ea, eb;
-  ScanLate lt;
+  ScanLate<TIn> lt;
   if constexpr (ZERO_INIT) {
     __syncthreads();
     if (nchunks > 0) {
