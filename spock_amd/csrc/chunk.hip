@@ -479,7 +479,7 @@ __device__ __forceinline__ void gram_dispatch(int part, int wave, const F& f) {
 // 2*part and 2*part+1 (PARTS 4: its four wavefronts split the two tiles' row
 // blocks as {0,3} / {1,2}, 40 MFMA each instead of 160) or tile `part`
 // (PARTS 8: waves 0-1 form U, 2-3 form W, row blocks {0,3} / {1,2}, 20 MFMA
-// each), and the A and K^T blocks of the wavefronts w with w % PARTS == part.
+// each), and the A blocks of the wavefronts w with w % PARTS == part.
 // Each value is computed by the same operation sequence whatever PARTS is, so
 // the record is bit-identical.
 template <typename TIn, int PARTS>
@@ -515,7 +515,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int li = lane & 15;
   const int lg = lane >> 4;
-  const bool own_block = (wave % PARTS) == part;  // this wave's A / raw Q / K^T block
+  const bool own_block = (wave % PARTS) == part;  // this wave's A block (and raw Q rows)
   const TIn* q = static_cast<const TIn*>(p.q);
   const TIn* k = static_cast<const TIn*>(p.k);
   const TIn* v = static_cast<const TIn*>(p.v);
@@ -780,9 +780,9 @@ struct ScanLate {
 //   D  S rows 32M..32M+31 <- e^{gL} S + K^T diag(Ks) v_new
 // 100-112 MFMA per wavefront per chunk (stage C: 4 (M+1)).
 // MINB workgroups per CU.  fp16 inputs, large launches: three (168 VGPRs;
-// the instance spills a few): more resident wavefronts measured faster than
-// two workgroups holding both operand sets double-buffered.  fp32 inputs hold
-// twice the Q and K^T operand registers: at 168 VGPRs they spilled 236 bytes
+// the instance spills 3): more resident wavefronts measured faster than two
+// workgroups holding both operand sets double-buffered.  fp32 inputs hold
+// twice the Q and K operand registers: at 168 VGPRs they spilled 236 bytes
 // per lane inside the chunk loop (6.5-9 us per chunk step against 3.1 for
 // fp16), so they run two workgroups per CU without spilling, as do small
 // fp16 launches.
@@ -802,7 +802,7 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   // longest sequence first so the longest chunk scans start earliest, and the
   // eight tiles of a group get workgroup ids congruent mod 8 -- the same XCD
   // (ids are dealt to the 8 XCDs round-robin) -- so they share one L2 for W,
-  // Q, A and K^T.
+  // A and the Q and K rows.
   const int b = blockIdx.x;
   const int groups = (p.nsel > 0 ? p.nsel : p.S) * p.H;
   int gi, tile;
@@ -1123,7 +1123,7 @@ int launch_intra(const ChunkParams& p, int chunks, bool f32, hipStream_t s) {
 
 int launch_scan(const ChunkParams& p, int nseq, bool f32, hipStream_t s) {
   dim3 g((unsigned)(kTiles * p.H * nseq));
-  // Three fp16 workgroups per CU (168 VGPRs, a 56-byte spill) only when the
+  // Three fp16 workgroups per CU (168 VGPRs, a 16-byte spill) only when the
   // launch has that many workgroups to keep resident; otherwise two per CU
   // without spilling, with the first-chunk skip when there is no initial
   // state (that instance's peeled loop spilled more at 168 VGPRs).  Measured,
