@@ -612,20 +612,24 @@ __global__ __launch_bounds__(kThreads) void ordered_chunk_prep_kernel(OrdArgs a)
     }
   }
   if (tid < kC) {
+    // :137-151: lane t of wave 0 adds g_0 .. g_t left to right (adding +0
+    // past t), so its sum is rounded exactly as the reference's running sum;
+    // g_j by readlane (no serial chain through LDS on one thread)
     const int tok = base + tid;
-    gcum[tid] = tok < a.T ? a.g[(size_t)h * a.T + tok] : 0.0f;  // g until the prefix below
+    const float gv = tok < a.T ? a.g[(size_t)h * a.T + tok] : 0.0f;
     bc[tid] = tok < a.T ? a.beta[(size_t)h * a.T + tok] : 0.0f;
+    float running = 0.0f;
+    const int gbits = __float_as_int(gv);
+#pragma unroll
+    for (int j = 0; j < kC; ++j) {
+      const float gj = __int_as_float(__builtin_amdgcn_readlane(gbits, j));
+      running = running + (j <= tid ? gj : 0.0f);
+    }
+    gcum[tid] = running;
   }
   __syncthreads();
-  if (tid == 0) {  // :137-151, in place
-    float running = 0.0f;
-    for (int t = 0; t < kC; ++t) {
-      gcum[t] = running + gcum[t];
-      running = gcum[t];
-    }
-  }
   if (a.l2) {
-    if (tid >= 64 && tid < 64 + 2 * kC) {  // waves 1, 2 (wave 0 runs the prefix)
+    if (tid >= 64 && tid < 64 + 2 * kC) {  // waves 1, 2
       const int t = tid & (kC - 1);
       const float* x = tid < 128 ? qs[t] : ks[t];
       float sq = 0.0f;
