@@ -906,11 +906,13 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
           aq = mfma4(elem(x, k), elem(sb, k), aq);
         }
       }
-      // The loads issued just before this stage (same scheduling region) are
-      // spread over the MFMA stream rather than issued as one burst, which
-      // would queue in the CU's vector-memory pipe behind the other
-      // wavefronts' bursts.  (sched_group_barrier masks: 0x020 VMEM read,
-      // 0x008 MFMA.)
+      // The loads issued just before this stage (same scheduling region, about
+      // 40 of them) are spread over the MFMA stream rather than issued as one
+      // burst, which would queue in the CU's vector-memory pipe behind the
+      // other wavefronts' bursts: 2 and 3 loads around each 4 MFMAs.  Measured
+      // on config 2 (ms per call, same box, bit-identical): 2+3 0.875-0.878,
+      // 3+2 0.875-0.878, 2+4 0.878-0.881, 1+4 0.879-0.883, 1+3 0.881-0.885,
+      // 2+2 0.895-0.898, 4+2 0.899, 4+4 0.967.
       // (masks: 0x100 LDS read, 0x020 VMEM read, 0x008 MFMA) -- the S piece
       // of step u+1 goes out before step u's 8 MFMAs
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
@@ -918,7 +920,7 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
       for (int i = 0; i < 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 3, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         if (i < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
