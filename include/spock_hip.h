@@ -60,8 +60,16 @@ uint32_t spk_abi_version(void);
  * one sequence of N tokens; otherwise sequence s owns tokens
  * [cu_seqlens[s], cu_seqlens[s+1]) (device int32, num_seqs+1 entries, host
  * copy in cu_seqlens_host) and is chunked from its own start and zero padded
- * independently.  initial_state (nullable = zeros, which is what the tiled
- * shader assumes, :66-71) and out_state are [num_seqs][H][dk][dv] fp32.
+ * independently.  Precondition: the device copy holds the same values as
+ * cu_seqlens_host when the kernels run.  The call validates and sizes the
+ * launch from the host copy (and, for up to 32 sequences, builds the
+ * kernels' sequence tables from it, never reading the device copy); for
+ * larger packs the kernels read the device copy and treat a span outside
+ * [0, total_tokens], or one whose chunks would exceed the workspace sized
+ * from the host copy, as empty -- a differing device copy gives wrong
+ * results, but no access outside the caller's buffers.
+ * initial_state (nullable = zeros, which is what the tiled shader assumes,
+ * :66-71) and out_state are [num_seqs][H][dk][dv] fp32.
  * out_core row (h, t) starts at out_core + (h*core_head_stride + t)*dv, so the
  * reference's single output buffer [H*total_seq*dv | H*dk*dv] is addressed by
  * core_head_stride = total_seq and out_state = out_core + H*total_seq*dv.

@@ -2,7 +2,8 @@
 // line of the reference's CPU driver (apps/spock-deltanet-chunk.cpp:40-112).
 //
 // Kept from that driver, because callers script against it:
-//   `--input FILE` (exit 2 when absent), a JSON object with num_heads,
+//   `--input FILE` (exit 2 when absent; other arguments are ignored), `--help`
+//   (exit 0), a JSON object with num_heads,
 //   sequence_length, key_dim, value_dim, chunk_size (default 64),
 //   use_qk_l2norm (boolean, default true), query/key/value/g/beta arrays and an
 //   optional initial_state (array or null); stdout is a JSON object with
@@ -120,15 +121,16 @@ int usage_error(const std::string& msg) {
 
 int main(int argc, char** argv) {
   std::string path;
+  // As the reference driver does, arguments other than --help and
+  // "--input FILE" are ignored, and a trailing --input without a FILE counts
+  // as no input.
   for (int i = 1; i < argc; ++i) {
     const std::string arg = argv[i];
-    if (arg == "--help" || arg == "-h") {
+    if (arg == "--help") {
       std::printf("usage: %s --input FILE\n", kTool);
       return 0;
     }
-    if (arg != "--input") return usage_error("unknown argument '" + arg + "'");
-    if (i + 1 >= argc) return usage_error("--input needs a FILE");
-    path = argv[++i];
+    if (arg == "--input" && i + 1 < argc) path = argv[++i];
   }
   if (path.empty()) return usage_error("--input is required");
 

@@ -111,6 +111,7 @@ struct ChunkParams {
   float* state;
   const int* cu;
   float* ws;
+  int chunks;                   // workspace records per head (host count)
   int nsel;
   int sel_seq[kSelMax];         // sequence index (row of initial/out state)
   int sel_t0[kSelMax];          // its first token
@@ -134,6 +135,17 @@ __device__ __forceinline__ float elem(const float4& v, int e) {
   return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
 }
 
+// Span of sequence s from the device cu_seqlens (packs of more than kSelMax
+// sequences).  The launch was sized from the host copy; a span that does not
+// lie inside [0, N] counts as empty, and both kernels apply the same rule, so
+// their workspace numbering agrees and no access leaves the tensors even if
+// the device copy differs from the host one.
+__device__ __forceinline__ int seq_span(const ChunkParams& p, int s, int& t0) {
+  t0 = p.cu[s];
+  const int t1 = p.cu[s + 1];
+  return (t0 >= 0 && t1 >= t0 && t1 <= p.N) ? t1 - t0 : 0;
+}
+
 // Global chunk id -> (sequence, chunk within it, first token, valid tokens).
 __device__ __forceinline__ void locate_chunk(const ChunkParams& p, int gchunk, int& seq,
                                              int& t0, int& len) {
@@ -145,12 +157,13 @@ __device__ __forceinline__ void locate_chunk(const ChunkParams& p, int gchunk, i
   }
   int acc = 0;
   for (int s = 0; s < p.S; ++s) {
-    const int L = p.cu[s + 1] - p.cu[s];
+    int ts;
+    const int L = seq_span(p, s, ts);
     const int n = (L + kC - 1) / kC;
     if (gchunk < acc + n) {
       const int c = gchunk - acc;
       seq = s;
-      t0 = p.cu[s] + c * kC;
+      t0 = ts + c * kC;
       len = min(kC, L - c * kC);
       return;
     }
@@ -169,8 +182,8 @@ template <> struct RawOf<float> {
   static __device__ __forceinline__ float4 cvt4(const float4& r) { return r; }
   // two adjacent elements of a row through a buffer resource (0 past its range)
   typedef float2 Pair;
-  static __device__ __forceinline__ Pair ld_pair(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  static __device__ __forceinline__ Pair ld_pair(__amdgpu_buffer_rsrc_t r, int voff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
     return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
   }
   static __device__ __forceinline__ float lo(Pair v) { return v.x; }
@@ -188,8 +201,8 @@ template <> struct RawOf<uint16_t> {
                        spk::h2f((uint16_t)(y & 0xffffu)), spk::h2f((uint16_t)(y >> 16)));
   }
   typedef uint32_t Pair;
-  static __device__ __forceinline__ Pair ld_pair(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  static __device__ __forceinline__ Pair ld_pair(__amdgpu_buffer_rsrc_t r, int voff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
   }
   static __device__ __forceinline__ float lo(Pair v) { return spk::h2f((uint16_t)(v & 0xffffu)); }
   static __device__ __forceinline__ float hi(Pair v) { return spk::h2f((uint16_t)(v >> 16)); }
@@ -199,6 +212,10 @@ template <> struct RawOf<uint16_t> {
 // column, read through a buffer resource of the chunk's len rows, so rows past
 // the chunk read 0 (the hardware range check) with no clamp or select.  fp16
 // rows are packed two to a register.
+// The whole byte offset goes in the VGPR offset and the scalar offset stays 0:
+// on gfx9-family raw buffers the range check compares only voffset +
+// inst_offset with num_records, so a row offset passed as soffset would read
+// past the chunk (the next sequence's rows, or past the tensor) unchecked.
 template <typename TIn> struct VOperand;
 template <> struct VOperand<float> {
   float x[4][4];
@@ -207,7 +224,7 @@ template <> struct VOperand<float> {
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        x[u][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + e * kD * 4, u * 16 * kD * 4, 0));
+        x[u][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + (16 * u + e) * kD * 4, 0, 0));
   }
   __device__ __forceinline__ float get(int u, int e) const { return x[u][e]; }
 };
@@ -218,8 +235,8 @@ template <> struct VOperand<uint16_t> {
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int e = 0; e < 4; e += 2) {
-        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, voff + e * kD * 2, u * 16 * kD * 2, 0);
-        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(r, voff + (e + 1) * kD * 2, u * 16 * kD * 2, 0);
+        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, voff + (16 * u + e) * kD * 2, 0, 0);
+        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(r, voff + (16 * u + e + 1) * kD * 2, 0, 0);
         x[u][e / 2] = lo | (hi << 16);
       }
   }
@@ -739,10 +756,11 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
 __device__ __forceinline__ int lpt_sequence(const ChunkParams& p, int slot) {
   if (p.cu == nullptr || p.S > 64) return slot;
   for (int s = 0; s < p.S; ++s) {
-    const int Ls = p.cu[s + 1] - p.cu[s];
+    int t;
+    const int Ls = seq_span(p, s, t);
     int rank = 0;
     for (int s2 = 0; s2 < p.S; ++s2) {
-      const int L2 = p.cu[s2 + 1] - p.cu[s2];
+      const int L2 = seq_span(p, s2, t);
       rank += (L2 > Ls) || (L2 == Ls && s2 < s);
     }
     if (rank == slot) return s;
@@ -829,9 +847,12 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     L = p.sel_len[slot];
     co = p.sel_co[slot];
   } else if (p.cu) {
-    t_begin = p.cu[seq];
-    L = p.cu[seq + 1] - t_begin;
-    for (int s = 0; s < seq; ++s) co += (p.cu[s + 1] - p.cu[s] + kC - 1) / kC;
+    L = seq_span(p, seq, t_begin);
+    for (int s = 0; s < seq; ++s) {
+      int ts;
+      co += (seq_span(p, s, ts) + kC - 1) / kC;
+    }
+    if (co + (L + kC - 1) / kC > p.chunks) L = 0;  // records past the workspace: empty
   }
   const int nchunks = (L + kC - 1) / kC;
 
@@ -881,7 +902,7 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) l.kp[4 * u + k] = R::ld_pair(kr, voff, (16 * u + k) * kD * (int)sizeof(TIn));
+      for (int k = 0; k < 4; ++k) l.kp[4 * u + k] = R::ld_pair(kr, voff + (16 * u + k) * kD * (int)sizeof(TIn));
   };
 
   // zero_s: S is zero (first chunk without an initial state)
@@ -1209,6 +1230,7 @@ extern "C" int spk_chunk_prefill(const SpkChunkArgs* a, spk_stream_t stream) {
   p.state = a->out_state;
   p.cu = a->cu_seqlens;
   p.ws = static_cast<float*>(a->workspace);
+  p.chunks = (int)chunks;
   p.nsel = 0;
   hipStream_t s = spk::to_hip(stream);
   const bool f32 = a->input_dtype == SPK_F32;

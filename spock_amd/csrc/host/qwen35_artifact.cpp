@@ -248,9 +248,9 @@ WeightArtifact WeightArtifact::load(const std::string& repack_dir) {
   namespace fs = std::filesystem;
   const auto root = json::read_file((fs::path(repack_dir) / "text_repack_manifest.json").string());
   WeightArtifact a;
-  a.weights_file_path_ = (fs::path(repack_dir) / "text_weights.bin").string();
+  a.bin_path_ = (fs::path(repack_dir) / "text_weights.bin").string();
   const json::Value* arr = root.get("tensors");
-  if (!arr || !arr->is_array()) throw std::runtime_error("manifest missing 'tensors' array");
+  if (!arr || !arr->is_array()) throw std::runtime_error("text_repack_manifest.json: no \"tensors\" list");
   for (const auto& e : arr->as_array()) {
     TensorInfo t;
     t.role_path = e.get_string("role_path");
@@ -260,11 +260,11 @@ WeightArtifact WeightArtifact::load(const std::string& repack_dir) {
     t.dtype = e.get_string("dtype");
     if (const json::Value* sh = e.get("shape"); sh && sh->is_array())
       for (const auto& d : sh->as_array()) t.shape.push_back(static_cast<std::size_t>(d.as_double()));
-    const std::size_t idx = a.tensors_.size();
-    a.name_index_[t.name] = idx;
-    a.role_index_[t.role_path] = idx;
-    a.total_bytes_ = std::max<std::size_t>(a.total_bytes_, t.offset + t.nbytes);
-    a.tensors_.push_back(std::move(t));
+    const std::size_t idx = a.entries_.size();
+    a.by_name_[t.name] = idx;
+    a.by_role_[t.role_path] = idx;
+    a.extent_ = std::max<std::size_t>(a.extent_, t.offset + t.nbytes);
+    a.entries_.push_back(std::move(t));
   }
   if (const json::Value* md = root.get("model"); md && md->is_object()) {
     a.shape_.layers = static_cast<std::uint32_t>(md->get_int("layers"));
@@ -274,14 +274,14 @@ WeightArtifact WeightArtifact::load(const std::string& repack_dir) {
     while (a.find_by_role("layer." + std::to_string(a.shape_.layers) + ".input_norm")) ++a.shape_.layers;
     a.shape_.vocab = static_cast<std::uint32_t>(a.token_embedding().shape.at(0));
   }
-  const int fd = ::open(a.weights_file_path_.c_str(), O_RDONLY);
-  if (fd < 0) throw std::runtime_error("cannot open " + a.weights_file_path_);
+  const int fd = ::open(a.bin_path_.c_str(), O_RDONLY);
+  if (fd < 0) throw std::runtime_error("cannot open " + a.bin_path_);
   struct stat sb {};
   if (::fstat(fd, &sb) != 0) {
     ::close(fd);
-    throw std::runtime_error("cannot stat " + a.weights_file_path_);
+    throw std::runtime_error("cannot stat " + a.bin_path_);
   }
-  if (static_cast<std::size_t>(sb.st_size) < a.total_bytes_) {
+  if (static_cast<std::size_t>(sb.st_size) < a.extent_) {
     ::close(fd);
     throw std::runtime_error("text_weights.bin is shorter than the manifest's tensor extent");
   }
@@ -290,7 +290,7 @@ WeightArtifact WeightArtifact::load(const std::string& repack_dir) {
   ::close(fd);
   if (a.map_ == MAP_FAILED) {
     a.map_ = nullptr;
-    throw std::runtime_error("cannot map " + a.weights_file_path_);
+    throw std::runtime_error("cannot map " + a.bin_path_);
   }
   return a;
 }
@@ -304,11 +304,11 @@ WeightArtifact::WeightArtifact(WeightArtifact&& o) noexcept { *this = std::move(
 WeightArtifact& WeightArtifact::operator=(WeightArtifact&& o) noexcept {
   if (this != &o) {
     if (map_) ::munmap(map_, map_bytes_);
-    tensors_ = std::move(o.tensors_);
-    name_index_ = std::move(o.name_index_);
-    role_index_ = std::move(o.role_index_);
-    weights_file_path_ = std::move(o.weights_file_path_);
-    total_bytes_ = o.total_bytes_;
+    entries_ = std::move(o.entries_);
+    by_name_ = std::move(o.by_name_);
+    by_role_ = std::move(o.by_role_);
+    bin_path_ = std::move(o.bin_path_);
+    extent_ = o.extent_;
     map_ = o.map_;
     map_bytes_ = o.map_bytes_;
     shape_ = o.shape_;
@@ -319,13 +319,13 @@ WeightArtifact& WeightArtifact::operator=(WeightArtifact&& o) noexcept {
 }
 
 const TensorInfo* WeightArtifact::find_by_role(const std::string& role_path) const {
-  auto it = role_index_.find(role_path);
-  return it == role_index_.end() ? nullptr : &tensors_[it->second];
+  auto it = by_role_.find(role_path);
+  return it == by_role_.end() ? nullptr : &entries_[it->second];
 }
 
 const TensorInfo* WeightArtifact::find_by_name(const std::string& name) const {
-  auto it = name_index_.find(name);
-  return it == name_index_.end() ? nullptr : &tensors_[it->second];
+  auto it = by_name_.find(name);
+  return it == by_name_.end() ? nullptr : &entries_[it->second];
 }
 
 const TensorInfo* WeightArtifact::find_by_state_dict_key(const std::string& key) const {
@@ -335,19 +335,19 @@ const TensorInfo* WeightArtifact::find_by_state_dict_key(const std::string& key)
 
 const TensorInfo& WeightArtifact::require(const std::string& role_path) const {
   const TensorInfo* t = find_by_role(role_path);
-  if (!t) throw std::runtime_error("artifact tensor not found: " + role_path);
+  if (!t) throw std::runtime_error("artifact has no entry for role " + role_path);
   return *t;
 }
 
 const TensorInfo& WeightArtifact::token_embedding() const {
   const TensorInfo* t = find_by_role("global.token_embedding");
-  if (!t) throw std::runtime_error("token embedding tensor not found");
+  if (!t) throw std::runtime_error("artifact has no global.token_embedding entry");
   return *t;
 }
 
 const TensorInfo& WeightArtifact::final_norm() const {
   const TensorInfo* t = find_by_role("global.final_norm");
-  if (!t) throw std::runtime_error("final norm tensor not found");
+  if (!t) throw std::runtime_error("artifact has no global.final_norm entry");
   return *t;
 }
 

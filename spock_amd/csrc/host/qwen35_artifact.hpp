@@ -81,10 +81,10 @@ class WeightArtifact {
   // Role lookup that throws std::runtime_error naming the role when absent.
   const TensorInfo& require(const std::string& role_path) const;
 
-  const std::string& weights_file_path() const { return weights_file_path_; }
-  const std::vector<TensorInfo>& tensors() const { return tensors_; }
-  std::size_t total_bytes() const { return total_bytes_; }
-  std::size_t tensor_count() const { return tensors_.size(); }
+  const std::string& weights_file_path() const { return bin_path_; }
+  const std::vector<TensorInfo>& tensors() const { return entries_; }
+  std::size_t total_bytes() const { return extent_; }
+  std::size_t tensor_count() const { return entries_.size(); }
   // Mapped bytes of one tensor (valid while the artifact lives).
   const void* data(const TensorInfo& t) const;
   const void* mapped() const { return map_; }
@@ -93,11 +93,11 @@ class WeightArtifact {
   Qwen35Shape shape() const { return shape_; }
 
  private:
-  std::vector<TensorInfo> tensors_;
-  std::unordered_map<std::string, std::size_t> name_index_;
-  std::unordered_map<std::string, std::size_t> role_index_;
-  std::string weights_file_path_;
-  std::size_t total_bytes_ = 0;
+  std::vector<TensorInfo> entries_;
+  std::unordered_map<std::string, std::size_t> by_name_;
+  std::unordered_map<std::string, std::size_t> by_role_;
+  std::string bin_path_;
+  std::size_t extent_ = 0;
   void* map_ = nullptr;
   std::size_t map_bytes_ = 0;
   Qwen35Shape shape_;

@@ -45,10 +45,14 @@ _CU_CHECKED: dict = {}
 
 
 def _check_cu_dev(cu_dev: torch.Tensor, cu_host: np.ndarray, dev) -> None:
-    """The kernels index sequences through the device copy and size the grid
-    from the host copy, so the two must agree.  The comparison reads the
-    device tensor back once per (buffer, version) and is cached, so repeated
-    calls with the same offsets stay asynchronous."""
+    """The launch is sized from the host copy; for packs of more than 32
+    sequences the kernels find the sequences through the device copy, so the
+    two must agree (the kernels keep every access in bounds either way, but a
+    differing copy gives wrong results).  The comparison reads the device
+    tensor back once per (buffer, torch version counter, host offsets) and is
+    cached, so repeated calls stay asynchronous: offsets rewritten behind
+    torch's back (through a raw pointer, without a version bump) are not seen
+    again, and must not be."""
     if cu_dev.device != dev or cu_dev.dtype != torch.int32 or not cu_dev.is_contiguous():
         raise _lib.SpockError("chunk_prefill: cu_seqlens_dev must be a contiguous int32 tensor on q's device")
     if cu_dev.numel() != cu_host.size:

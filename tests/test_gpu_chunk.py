@@ -127,28 +127,97 @@ def test_reference_output_buffer_layout(dev, oracle):
     assert max_rel(got[H * total * 128:].reshape(H, 128, 128), cs) <= TOL
 
 
-def test_config2_full_size_properties(dev, oracle):
-    """Config 2 at full size (8 sequences, lengths U[512, 8192], fp16 q/k/v):
-    each sequence of the packed call equals the single-sequence call bit for
-    bit, and the two shortest sequences match the oracle."""
-    from spock_amd import synth
+def _trunc16(x):
+    """fp32 -> fp16 bits rounded toward zero with flush to zero, formed from
+    numpy's round-to-nearest cast: where the nearest fp16 lies above |x|,
+    step one ulp toward zero; |x| below fp16's smallest normal gives +-0 and
+    |x| >= 2^16 gives +-inf (the reference's float_to_half,
+    vk_session.cpp:69-89).  Finite inputs only."""
+    x = np.asarray(x, np.float32)
+    with np.errstate(over="ignore"):
+        h = x.astype(np.float16).view(np.uint16).astype(np.int32)
+    above = np.abs(h.astype(np.uint16).view(np.float16).astype(np.float64)) > np.abs(x.astype(np.float64))
+    h = np.where(above & ((h & 0x7FFF) != 0), h - 1, h)
+    sign = (x.view(np.uint32) >> 16).astype(np.int32) & 0x8000
+    h = np.where(np.abs(x) < np.float32(2.0 ** -14), sign, h)
+    h = np.where(np.abs(x) >= np.float32(65536.0), sign | 0x7C00, h)
+    return h.astype(np.uint16)
+
+
+def _oracle_pack_threads(oracle, inp, cu):
+    """The oracle's chunk rule for every (sequence, head) of a pack, split
+    over the host's threads (ctypes releases the GIL during each call)."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+    S = len(cu) - 1
+    H = inp["q"].shape[0]
+    jobs = [(s, h) for s in range(S) for h in range(H)]
+
+    def one(job):
+        s, h = job
+        t0, t1 = int(cu[s]), int(cu[s + 1])
+        sub = {n: np.ascontiguousarray(a[h:h + 1, t0:t1]) for n, a in inp.items()}
+        return oracle.chunk_rule(**sub)
+
+    try:
+        nt = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nt = os.cpu_count() or 1
+    with ThreadPoolExecutor(max(1, min(16, nt))) as ex:
+        res = list(ex.map(one, jobs))
+    core = np.empty((H, int(cu[-1]), 128), np.float32)
+    state = np.empty((S, H, 128, 128), np.float32)
+    for (s, h), (c, st) in zip(jobs, res):
+        core[h, int(cu[s]):int(cu[s + 1])] = c[0]
+        state[s, h] = st[0]
+    return core, state
+
+
+def test_config2_full_size_against_oracle(dev, oracle):
+    """Config 2 at full size (8 sequences, lengths U[512, 8192], fp16 q/k/v,
+    34,878 tokens): every sequence of the packed call, the 124-chunk one
+    included, against the oracle's chunk rule (deltanet_chunk.cpp:53-284) run
+    per (sequence, head), to the north-star bar on the floored metric; the
+    pure relative error |g - c| / |c| is reported beside it.  The packed
+    result also equals the single-sequence call bit for bit (shortest and
+    longest), and the last-token fp16 hand-off of every sequence equals the
+    truncated last row (deltanet_chunk_last_to_fp16.comp:70-76)."""
+    from spock_amd import ops, synth
     lens = synth.ragged_lengths(8, 512, 8192, seed=2024)
     cu = synth.cu_seqlens_from(lens)
     N = int(cu[-1])
     inp = synth.chunk_inputs(16, N, seed=2)
     for n in ("q", "k", "v"):
         inp[n] = inp[n].astype(np.float16).astype(np.float32)
-    gc, gs = _run(dev, inp, cu=cu, half=True)
+    dt = torch.float16
+    q, k, v = (_to(dev, inp[n], dt) for n in ("q", "k", "v"))
+    core_d, state_d = ops.chunk_prefill(q, k, v, _to(dev, inp["g"]), _to(dev, inp["beta"]), cu_seqlens=cu)
+    torch.cuda.synchronize()
+    gc, gs = core_d.cpu().numpy(), state_d.cpu().numpy()
     assert np.isfinite(gc).all() and np.isfinite(gs).all()
+    print(f"[config 2 oracle: lens {list(map(int, lens))}]", flush=True)
+    cc, cs = _oracle_pack_threads(oracle, inp, cu)
+    for s in range(len(lens)):
+        t0, t1 = int(cu[s]), int(cu[s + 1])
+        ec, es = max_rel(gc[:, t0:t1], cc[:, t0:t1]), max_rel(gs[s], cs[s])
+        a, b = gc[:, t0:t1].astype(np.float64), cc[:, t0:t1].astype(np.float64)
+        nz = b != 0
+        pure_c = float(np.max(np.abs(a - b)[nz] / np.abs(b)[nz]))
+        nzs = cs[s] != 0
+        pure_s = float(np.max(np.abs(gs[s].astype(np.float64) - cs[s])[nzs] / np.abs(cs[s].astype(np.float64))[nzs]))
+        print(f"  seq {s} len {t1 - t0} ({(t1 - t0 + 63) // 64} chunks): floored core {ec:.2e} state {es:.2e}; "
+              f"pure relative core {pure_c:.2e} state {pure_s:.2e}", flush=True)
+        assert ec <= TOL and es <= TOL, (s, ec, es)
+        # last-token hand-off: row (h*N + t1 - 1) of every head
+        last = ops.chunk_last_to_fp16(core_d, seq_len=t1, total_seq=N)
+        torch.cuda.synchronize()
+        assert np.array_equal(last.cpu().numpy().view(np.uint16), _trunc16(gc[:, t1 - 1, :]).reshape(-1)), s
     order = np.argsort(lens)
-    for s in list(order[:2]) + [order[-1]]:
+    for s in (order[0], order[-1]):
         t0, L = int(cu[s]), int(lens[s])
         sub = {k_: v_[:, t0:t0 + L] for k_, v_ in inp.items()}
         c1, s1 = _run(dev, sub, half=True)
         assert np.array_equal(c1, gc[:, t0:t0 + L]) and np.array_equal(s1[0], gs[s])
-        if s in order[:2]:
-            cc, cs = oracle.chunk_rule(**sub)
-            assert max_rel(c1, cc) <= TOL and max_rel(s1[0], cs) <= TOL
 
 
 @pytest.mark.parametrize("half", [False, True])
@@ -310,3 +379,45 @@ def test_random_packs_against_oracle(dev, oracle, i):
     gc, gs = _run(dev, inp, init=st0, cu=cu, l2=l2, half=half)
     assert max_rel(gc, cc) <= TOL
     assert max_rel(gs, cs) <= TOL
+
+
+def _poisoned(dev, a, dtype, fill, extra_rows=64):
+    """`a` [H][N][128] copied to the front of a larger device buffer whose
+    remaining `extra_rows` rows hold `fill` (NaN or Inf): a row read past the
+    tensor's end returns that value instead of finite garbage."""
+    H, N, D = a.shape
+    buf = torch.full((H * N * D + extra_rows * D,), fill, dtype=dtype, device=dev)
+    buf[:H * N * D] = torch.from_numpy(np.ascontiguousarray(a)).to(dev, dtype).reshape(-1)
+    return buf[:H * N * D].view(H, N, D)
+
+
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("last", [1, 17, 63])
+def test_padding_rows_never_read_past_the_chunk(dev, oracle, half, last):
+    """The last chunk of a sequence is zero padded to 64 rows.  The kernels
+    must not read the padding rows from memory: q/k/v are placed at the front
+    of larger buffers whose tail holds NaN (q, v) and Inf (k), the pack's last
+    sequence ends on a partial chunk of `last` rows, so its padding rows fall
+    past the tensor's end.  One head alone (H=1) and 16 heads, packed after a
+    ragged sequence, must match the oracle and stay finite (NaN or Inf read
+    into U, W or S would spread through 0 * Inf into every output row)."""
+    from spock_amd import ops, synth
+    dt = torch.float16 if half else torch.float32
+    for H, lens in ((1, [last]), (16, [130, 64 + last])):
+        print(f"[poisoned tail H={H} lens={lens} half={half}]", flush=True)
+        cu = synth.cu_seqlens_from(lens)
+        inp = synth.chunk_inputs(H, int(cu[-1]), seed=40 + last)
+        if half:
+            for n in ("q", "k", "v"):
+                inp[n] = inp[n].astype(np.float16).astype(np.float32)
+        q = _poisoned(dev, inp["q"], dt, float("nan"))
+        k = _poisoned(dev, inp["k"], dt, float("inf"))
+        v = _poisoned(dev, inp["v"], dt, float("nan"))
+        core, state = ops.chunk_prefill(q, k, v, _to(dev, inp["g"]), _to(dev, inp["beta"]),
+                                        cu_seqlens=cu)
+        torch.cuda.synchronize()
+        gc, gs = core.cpu().numpy(), state.cpu().numpy()
+        assert np.isfinite(gc).all() and np.isfinite(gs).all()
+        cc, cs = oracle.chunk_rule_varlen(**inp, cu=cu)
+        assert max_rel(gc, cc) <= TOL
+        assert max_rel(gs, cs) <= TOL

@@ -28,9 +28,10 @@ def _u16(t):
     return t.cpu().numpy().view(np.uint16)
 
 
-# workgroup shape: 16 wavefronts up to B = 4, 8 up to B = 32, then 4; the
-# batches on both sides of each switch are included
-@pytest.mark.parametrize("B", [1, 3, 4, 5, 16, 32, 33, 64, 100, 256])
+# workgroup shape (decode_waves, 16 heads): 16 wavefronts up to 256
+# workgroups (B <= 16), 8 up to 512 (B <= 32), then 4; the batches on both
+# sides of each switch are included
+@pytest.mark.parametrize("B", [1, 3, 4, 5, 16, 17, 32, 33, 64, 100, 256])
 def test_fused_decode_step_bitexact(dev, oracle, B):
     from spock_amd import ops, synth
     print(f"[decode B={B}]", flush=True)

@@ -24,10 +24,16 @@ def _built():
 def test_chunk_cli_usage():
     r = subprocess.run([str(H.CHUNK_CLI)], capture_output=True, text=True)
     assert r.returncode == 2 and "--input is required" in r.stderr
+    # as in the reference driver (apps/spock-deltanet-chunk.cpp:42-50): a
+    # trailing --input without a FILE counts as no input, other arguments are
+    # ignored
     r = subprocess.run([str(H.CHUNK_CLI), "--input"], capture_output=True, text=True)
-    assert r.returncode == 2 and "--input needs a FILE" in r.stderr
+    assert r.returncode == 2 and "--input is required" in r.stderr
     r = subprocess.run([str(H.CHUNK_CLI), "--bogus"], capture_output=True, text=True)
-    assert r.returncode == 2 and "unknown argument" in r.stderr
+    assert r.returncode == 2 and "--input is required" in r.stderr
+    r = subprocess.run([str(H.CHUNK_CLI), "--bogus", "--input", "/nonexistent/request.json", "-x"],
+                       capture_output=True, text=True)
+    assert r.returncode == 1 and "/nonexistent/request.json" in r.stderr
     r = subprocess.run([str(H.CHUNK_CLI), "--help"], capture_output=True, text=True)
     assert r.returncode == 0 and r.stdout.startswith("usage: spock-deltanet-chunk")
 
