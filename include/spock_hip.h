@@ -335,6 +335,22 @@ int spk_lm_head_argmax_key(const uint16_t* W, const uint16_t* x, const uint16_t*
  * capacity, *count += 1, *pos += 1). */
 int spk_argmax_key_take(uint64_t* key, int32_t vocab, uint32_t* out_index, int32_t* pos, int32_t* count,
                         int32_t* history, int32_t capacity, spk_stream_t stream);
+/* spk_lm_head_argmax_key and spk_argmax_key_take in one launch (the final
+ * norm, lm_head, argmax and record-token dispatches of vk_session.cpp:3533-3563
+ * as one kernel): each workgroup of the lm_head writes its 64-bit key to a
+ * slot of its own, and one extra workgroup polls the slots until all are
+ * written, reduces them with argmax.comp's tie rule, sets them back to 0 and
+ * writes *out_index (and the bookkeeping of spk_argmax_key_take when pos !=
+ * NULL).  slots: slot_words >= spk_lm_head_take_slots(vocab) 64-bit words of
+ * device memory that hold 0 before the call (the call leaves them at 0);
+ * calls that overlap on one slot array race.  The poll is bounded: if the
+ * slots are not all written within seconds (which only a corrupted slot
+ * array can cause), *out_index is 0xffffffff. */
+size_t spk_lm_head_take_slots(int32_t vocab);
+int spk_lm_head_argmax_take(const uint16_t* W, const uint16_t* x, const uint16_t* norm_w, int32_t vocab,
+                            int32_t hidden, uint16_t* logits, uint64_t* slots, size_t slot_words,
+                            uint32_t* out_index, int32_t* pos, int32_t* count, int32_t* history,
+                            int32_t capacity, spk_stream_t stream);
 /* *p += delta on the device (advances a device position counter). */
 int spk_add_i32(int32_t* p, int32_t delta, spk_stream_t stream);
 

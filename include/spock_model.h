@@ -50,11 +50,15 @@ enum {
   SPK_MODEL_GPU_TIMESTAMPS = 4,  /* GPU time of every decode step (the reference's
                                     SPOCK_GPU_TIMESTAMPS, vk_session.cpp:2188-2201):
                                     a HIP event before each step, graph kept */
-  SPK_MODEL_GPU_REGIONS = 8      /* also GPU time per region of the step
+  SPK_MODEL_GPU_REGIONS = 8,     /* also GPU time per region of the step
                                     (SPOCK_GPU_BLOCK_TIMESTAMPS, vk_session.cpp:
                                     2204-2218): events after each layer, lm_head and
                                     argmax; the step's kernels are then launched one
                                     by one, since a recorded graph holds no events */
+  SPK_MODEL_LMHEAD_TWO_LAUNCH = 16  /* final norm + lm_head + argmax as the key launch
+                                    then the take (spk_lm_head_argmax_key,
+                                    spk_argmax_key_take) instead of one launch
+                                    (spk_lm_head_argmax_take); same tokens */
 };
 
 /* Opens <repack_dir>, uploads every tensor, allocates the per-layer state for
@@ -84,9 +88,11 @@ int spk_model_gpu_token_us(const SpkModel* m, double* us, int32_t capacity, int3
  * 4139-4176), SPK_MODEL_GPU_REGIONS only: microseconds per region summed over
  * the steps, in step order: "layer_0" .. "layer_<n-1>" ("layer_0" includes the
  * embedding gather, which its input norm reads directly, so there is no
- * "embedding" region), "lm_head" (final norm, lm_head and the argmax key in one
- * launch, so no separate "final_norm"), "argmax" (the take that records the
- * token).  *name stays valid until the next spk_model_generate call. */
+ * "embedding" region), "lm_head" (final norm, lm_head and the argmax in one
+ * launch, so no separate "final_norm"; with SPK_MODEL_LMHEAD_TWO_LAUNCH the
+ * argmax key only), "argmax" (with SPK_MODEL_LMHEAD_TWO_LAUNCH the take that
+ * records the token; empty otherwise, the lm_head launch records it).  *name
+ * stays valid until the next spk_model_generate call. */
 int spk_model_gpu_region_count(const SpkModel* m, int32_t* count);
 int spk_model_gpu_region(const SpkModel* m, int32_t index, const char** name, double* us);
 

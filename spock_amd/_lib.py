@@ -51,6 +51,8 @@ SIGNATURES = {
     "spk_record_token": (C.c_int, [_p, _p, _p, _p, _i32, _p]),
     "spk_lm_head_argmax_key": (C.c_int, [_p, _p, _p, _i32, _i32, _p, _p, _p]),
     "spk_argmax_key_take": (C.c_int, [_p, _i32, _p, _p, _p, _p, _i32, _p]),
+    "spk_lm_head_take_slots": (_sz, [_i32]),
+    "spk_lm_head_argmax_take": (C.c_int, [_p, _p, _p, _i32, _i32, _p, _p, _sz, _p, _p, _p, _p, _i32, _p]),
     "spk_gemm_f16": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _i32, _i32, _i32, _p]),
     "spk_deltanet_prefill_conv": (C.c_int, [_p, _i64, _p, _p, _i32, _p, _p, _p, _p]),
     "spk_deltanet_prefill_gbeta": (C.c_int, [_p, _p, _i64, _p, _i32, _i32, _p, _p, _p]),

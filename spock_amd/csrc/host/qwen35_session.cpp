@@ -92,10 +92,11 @@ std::vector<float> rope_table(std::uint32_t max_seq) {
 }
 
 Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::uint32_t max_seq, bool use_graph,
-                             bool ordered_prefill, GpuTimestamps gpu_timestamps)
+                             bool ordered_prefill, GpuTimestamps gpu_timestamps, bool lm_head_one_launch)
     : verbose_(verbose),
       use_graph_(use_graph),
       ordered_prefill_(ordered_prefill),
+      lm_one_launch_(lm_head_one_launch),
       max_seq_(max_seq ? max_seq : MAX_SEQ),
       gpu_ts_(gpu_timestamps) {
   if (max_seq_ > 65536) throw std::runtime_error("max_seq must be <= 65536");
@@ -178,6 +179,8 @@ Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::u
   attn_ws_ = DeviceBuffer(spk_attention_workspace_size(static_cast<int32_t>(max_seq_), 1));
   argmax_key_ = DeviceBuffer(SPK_ARGMAX_KEY_WORDS * 8);
   argmax_key_.zero(stream_);  // spk_argmax_key_take returns it to zero after every use
+  take_slots_ = DeviceBuffer(spk_lm_head_take_slots(static_cast<int32_t>(V)) * 8);
+  take_slots_.zero(stream_);  // spk_lm_head_argmax_take returns them to zero after every use
   tok_ = DeviceBuffer(256);
   pos_ = DeviceBuffer(256);
   history_cap_ = max_seq_;
@@ -365,21 +368,14 @@ std::uint32_t Qwen35Session::prefill(const std::vector<std::uint32_t>& tokens) {
   // Last token: final norm, lm_head + argmax, token bookkeeping on the device.
   const std::uint16_t* last = Hs + std::size_t(T - 1) * H;
   hip_check(hipMemcpyAsync(h_.get(), last, H * 2, hipMemcpyDeviceToDevice, stream_), "last hidden");
-  const int32_t vocab = static_cast<int32_t>(shape_.vocab);
-  spk_check(spk_lm_head_argmax_key(embed_, last, final_norm_, vocab, H, logits_.get<std::uint16_t>(),
-                                   argmax_key_.get<std::uint64_t>(), S(stream_)),
-            "lm_head");
   const std::int32_t pos_count[2] = {p0 + Ti - 1, 0};
   hip_check(hipMemcpyAsync(pos_.get(), &pos_count[0], 4, hipMemcpyHostToDevice, stream_), "position");
   hip_check(hipMemcpyAsync(history_.get(), &pos_count[1], 4, hipMemcpyHostToDevice, stream_), "history count");
-  std::int32_t* hist = history_.get<std::int32_t>();
-  spk_check(spk_argmax_key_take(argmax_key_.get<std::uint64_t>(), vocab, tok_.get<std::uint32_t>(),
-                                pos_.get<std::int32_t>(), hist, hist + 64, static_cast<int32_t>(history_cap_),
-                                S(stream_)),
-            "argmax take");
+  lm_head_token(last, tok_.get<std::uint32_t>(), false);
   hip_check(hipEventRecord(ev.b, stream_), "hipEventRecord");
   std::int32_t first = 0;
-  hip_check(hipMemcpyAsync(&first, hist + 64, 4, hipMemcpyDeviceToHost, stream_), "first token");
+  hip_check(hipMemcpyAsync(&first, history_.get<std::int32_t>() + 64, 4, hipMemcpyDeviceToHost, stream_),
+            "first token");
   hip_check(hipStreamSynchronize(stream_), "prefill");
   last_gpu_prefill_ms_ = ev.ms();
   pos_host_ = p0 + Ti;
@@ -473,18 +469,39 @@ void Qwen35Session::enqueue_decode_step() {
     spk_check(spk_gemv_fused(&di, &dout, 1, S(stream_)), "down_proj");
     mark(L + 1);
   }
-  // final norm + lm_head + argmax key in one launch; the take records the token
+  // final norm + lm_head + argmax + the token's bookkeeping
+  lm_head_token(h, reinterpret_cast<std::uint32_t*>(tok), true);
+}
+
+// Final norm, lm_head and argmax of hidden row h; the token goes to *tok and
+// is recorded in the history (count, position).  One launch
+// (spk_lm_head_argmax_take) by default, else the key launch then the take;
+// with region marks, "lm_head" ends after the first launch and "argmax" after
+// the take (empty in the one-launch form).
+void Qwen35Session::lm_head_token(const std::uint16_t* h, std::uint32_t* tok, bool marks) {
   const int32_t vocab = static_cast<int32_t>(shape_.vocab);
+  std::int32_t* hist = history_.get<std::int32_t>();
+  const std::size_t NL = layers_.size();
+  if (lm_one_launch_) {
+    spk_check(spk_lm_head_argmax_take(embed_, h, final_norm_, vocab, H, logits_.get<std::uint16_t>(),
+                                      take_slots_.get<std::uint64_t>(), take_slots_.bytes() / 8, tok,
+                                      pos_.get<std::int32_t>(), hist, hist + 64,
+                                      static_cast<int32_t>(history_cap_), S(stream_)),
+              "lm_head + argmax");
+    if (marks) {
+      mark(NL + 1);
+      mark(NL + 2);
+    }
+    return;
+  }
   spk_check(spk_lm_head_argmax_key(embed_, h, final_norm_, vocab, H, logits_.get<std::uint16_t>(),
                                    argmax_key_.get<std::uint64_t>(), S(stream_)),
             "lm_head");
-  mark(NL + 1);
-  std::int32_t* hist = history_.get<std::int32_t>();
-  spk_check(spk_argmax_key_take(argmax_key_.get<std::uint64_t>(), vocab, reinterpret_cast<std::uint32_t*>(tok),
-                                pos_.get<std::int32_t>(), hist, hist + 64, static_cast<int32_t>(history_cap_),
-                                S(stream_)),
+  if (marks) mark(NL + 1);
+  spk_check(spk_argmax_key_take(argmax_key_.get<std::uint64_t>(), vocab, tok, pos_.get<std::int32_t>(), hist,
+                                hist + 64, static_cast<int32_t>(history_cap_), S(stream_)),
             "argmax take");
-  mark(NL + 2);
+  if (marks) mark(NL + 2);
 }
 
 void Qwen35Session::ensure_graph() {
@@ -690,7 +707,8 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
   SpkModel* m = nullptr;
   const int rc = guarded([&] {
     if (!repack_dir) throw std::runtime_error("spk_model_open: NULL directory");
-    if (flags & ~(SPK_MODEL_NO_GRAPH | SPK_MODEL_MATRIX_PREFILL | SPK_MODEL_GPU_TIMESTAMPS | SPK_MODEL_GPU_REGIONS))
+    if (flags & ~(SPK_MODEL_NO_GRAPH | SPK_MODEL_MATRIX_PREFILL | SPK_MODEL_GPU_TIMESTAMPS | SPK_MODEL_GPU_REGIONS |
+                  SPK_MODEL_LMHEAD_TWO_LAUNCH))
       throw std::runtime_error("spk_model_open: unknown flags");
     using spock::hip::GpuTimestamps;
     const GpuTimestamps ts = (flags & SPK_MODEL_GPU_REGIONS)      ? GpuTimestamps::per_region
@@ -699,7 +717,8 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
     auto s = std::make_unique<spock::hip::Qwen35Session>(repack_dir, false,
                                                          max_seq > 0 ? static_cast<std::uint32_t>(max_seq) : 0u,
                                                          (flags & SPK_MODEL_NO_GRAPH) == 0,
-                                                         (flags & SPK_MODEL_MATRIX_PREFILL) == 0, ts);
+                                                         (flags & SPK_MODEL_MATRIX_PREFILL) == 0, ts,
+                                                         (flags & SPK_MODEL_LMHEAD_TWO_LAUNCH) == 0);
     m = new SpkModel{std::move(s), {}};
   });
   return rc == 0 ? m : nullptr;

@@ -72,7 +72,7 @@ class Qwen35Session {
   // holds no timing events).
   explicit Qwen35Session(const std::string& repack_dir, bool verbose = false, std::uint32_t max_seq = MAX_SEQ,
                          bool use_graph = true, bool ordered_prefill = true,
-                         GpuTimestamps gpu_timestamps = GpuTimestamps::off);
+                         GpuTimestamps gpu_timestamps = GpuTimestamps::off, bool lm_head_one_launch = true);
   ~Qwen35Session();
   Qwen35Session(const Qwen35Session&) = delete;
   Qwen35Session& operator=(const Qwen35Session&) = delete;
@@ -120,6 +120,7 @@ class Qwen35Session {
   void run_decode_step();
   void ensure_ts_events(std::size_t n);
   void mark(std::size_t k);
+  void lm_head_token(const std::uint16_t* h, std::uint32_t* tok, bool marks);
   float* dn_state_layer(std::uint32_t i) const { return dn_state_.get<float>() + std::size_t(i) * kStateFloats; }
   std::uint16_t* conv_layer(std::uint32_t i) const { return conv_state_.get<std::uint16_t>() + std::size_t(i) * 6144 * 4; }
   std::uint16_t* kv_layer(std::uint32_t i) const {
@@ -129,6 +130,7 @@ class Qwen35Session {
   bool verbose_ = false;
   bool use_graph_ = true;
   bool ordered_prefill_ = true;
+  bool lm_one_launch_ = true;  // spk_lm_head_argmax_take, else the key + take pair
   Qwen35Shape shape_;
   std::uint32_t max_seq_ = MAX_SEQ;
   std::uint32_t n_dn_ = 0, n_attn_ = 0;
@@ -151,7 +153,7 @@ class Qwen35Session {
   DeviceBuffer dn_state_, conv_state_, kv_cache_, a_log_bias_, rope_;
   // decode activations
   DeviceBuffer h_, qkv_, z_, a_, b_, qg_, k_, v_, attn_out_, gate_, up_, logits_;
-  DeviceBuffer attn_ws_, argmax_key_, tok_, pos_, history_;
+  DeviceBuffer attn_ws_, argmax_key_, take_slots_, tok_, pos_, history_;
   std::uint32_t history_cap_ = 0;   // token history capacity (= max_seq_: one token per position)
   // prefill activations (capacity prefill_cap_ tokens)
   std::uint32_t prefill_cap_ = 0;

@@ -21,6 +21,7 @@
 namespace {
 
 constexpr int kHidden = 1024;
+constexpr int kLmKeyRows = 8;  // vocabulary rows per wavefront of the lm_head key kernels
 constexpr int kHeadDim = 256;
 constexpr int kQHeads = 8;
 constexpr int kKvHeads = 2;
@@ -923,12 +924,69 @@ __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <int N8, int R, bool NORM>
+// One-launch form: the workgroups' keys go to one slot each (agent-scope
+// store, posted: no compute workgroup waits on a memory round trip), and one
+// extra workgroup -- the last id, so the last dispatched on its XCD -- polls
+// the slots until every one is filled, reduces them, clears them and records
+// the token.  A slot holds key + 1 (keys are below 2^64 - 1: the largest,
+// +inf's, has 0xff800000 above), so 0 means "not written yet".  The poll is
+// bounded: after kTakePolls rounds (seconds) it gives up and records index
+// 0xffffffff, so the kernel always ends.
+constexpr int kTakePolls = 1 << 21;
+
+struct TakeArgs {
+  unsigned long long* slots;
+  int nblocks;
+  uint32_t* out;
+  int32_t* pos;
+  int32_t* count;
+  int32_t* history;
+  int cap;
+};
+
+__device__ __forceinline__ void take_slots(const TakeArgs& t, uint32_t E) {
+  const int tid = threadIdx.x;
+  unsigned long long best = 0ull;
+  int missing = 1;
+  for (int it = 0; it < kTakePolls && missing; ++it) {
+    best = 0ull;
+    int miss = 0;
+    for (int j = tid; j < t.nblocks; j += 256) {
+      const unsigned long long v = __hip_atomic_load(t.slots + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      best = spk::umax64(best, v);
+      miss |= (v == 0ull);
+    }
+    missing = __syncthreads_or(miss);
+    if (missing) __builtin_amdgcn_s_sleep(4);
+  }
+  best = spk::block_max_u64<256>(best);
+  for (int j = tid; j < t.nblocks; j += 256)
+    __hip_atomic_store(t.slots + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    const uint32_t idx = missing ? 0xffffffffu : spk::key_to_index(best - 1ull, E);
+    *t.out = idx;
+    if (t.pos) {
+      const int i = t.count[0];
+      if (i >= 0 && i < t.cap) t.history[i] = (int32_t)idx;
+      t.count[0] = i + 1;
+      t.pos[0] = t.pos[0] + 1;
+    }
+  }
+}
+
+template <int N8, int R, bool NORM, bool ONE = false>
 __global__ __launch_bounds__(256) void lm_head_key_kernel(const uint16_t* __restrict__ W,
                                                           const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ norm_w,
                                                           uint16_t* __restrict__ logits, int vocab,
-                                                          uint32_t E, unsigned long long* key_out) {
+                                                          uint32_t E, unsigned long long* key_out,
+                                                          TakeArgs take) {
+  if constexpr (ONE) {
+    if ((int)blockIdx.x == take.nblocks) {
+      take_slots(take, E);
+      return;
+    }
+  }
   __shared__ float xs[512 * N8];
   __shared__ float red[257];
   const int tid = threadIdx.x;
@@ -1006,9 +1064,13 @@ __global__ __launch_bounds__(256) void lm_head_key_kernel(const uint16_t* __rest
     }
   }
   key = spk::block_max_u64<256>(key);
-  if (tid == 0 && key != 0ull)
-    __hip_atomic_fetch_max(key_out + (blockIdx.x & (SPK_ARGMAX_KEY_WORDS - 1)), key, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+  if constexpr (ONE) {
+    if (tid == 0) __hip_atomic_store(take.slots + blockIdx.x, key + 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    if (tid == 0 && key != 0ull)
+      __hip_atomic_fetch_max(key_out + (blockIdx.x & (SPK_ARGMAX_KEY_WORDS - 1)), key, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // *out = index of the largest of the 64 key words (which are then zeroed);
@@ -1330,20 +1392,20 @@ extern "C" int spk_lm_head_argmax_key(const uint16_t* W, const uint16_t* x, cons
                      vocab, hidden);
   if (!spk::aligned(W, 16) || !spk::aligned(x, 16) || !spk::aligned(key, 8) || (norm_w && !spk::aligned(norm_w, 8)))
     return spk::fail(SPK_ERR_ALIGN, "%s: W/x must be 16-byte aligned, key and norm_w 8-byte", name);
-  constexpr int R = 8;
+  constexpr int R = kLmKeyRows;
   const uint32_t E = (uint32_t)((vocab + 255) / 256);
   const int blocks = (vocab + 4 * R - 1) / (4 * R);
   hipStream_t s = spk::to_hip(stream);
   auto* k = reinterpret_cast<unsigned long long*>(key);
   if (norm_w) {
     hipLaunchKernelGGL((lm_head_key_kernel<2, R, true>), dim3(blocks), dim3(256), 0, s, W, x, norm_w, logits,
-                       vocab, E, k);
+                       vocab, E, k, TakeArgs{});
     return spk::check_launch(name);
   }
 #define SPK_LMK_CASE(n8)                                                                                      \
   case n8:                                                                                                    \
     hipLaunchKernelGGL((lm_head_key_kernel<n8, R, false>), dim3(blocks), dim3(256), 0, s, W, x, nullptr,   \
-                       logits, vocab, E, k);                                                                  \
+                       logits, vocab, E, k, TakeArgs{});                                                      \
     break;
   switch (hidden / 512) {
     SPK_LMK_CASE(1)
@@ -1370,6 +1432,57 @@ extern "C" int spk_argmax_key_take(uint64_t* key, int32_t vocab, uint32_t* out_i
   hipLaunchKernelGGL(argmax_take_kernel, dim3(1), dim3(64), 0, spk::to_hip(stream),
                      reinterpret_cast<unsigned long long*>(key), E, out_index, pos, count, history, capacity);
   return spk::check_launch("spk_argmax_key_take");
+}
+
+extern "C" size_t spk_lm_head_take_slots(int32_t vocab) {
+  return vocab > 0 ? (size_t)((vocab + 4 * kLmKeyRows - 1) / (4 * kLmKeyRows)) : 0;
+}
+
+extern "C" int spk_lm_head_argmax_take(const uint16_t* W, const uint16_t* x, const uint16_t* norm_w, int32_t vocab,
+                                       int32_t hidden, uint16_t* logits, uint64_t* slots, size_t slot_words,
+                                       uint32_t* out_index, int32_t* pos, int32_t* count, int32_t* history,
+                                       int32_t capacity, spk_stream_t stream) {
+  const char* name = "spk_lm_head_argmax_take";
+  if (!W || !x || !slots || !out_index) return spk::fail(SPK_ERR_NULL, "%s: NULL pointer", name);
+  if (vocab > 0 && slot_words < spk_lm_head_take_slots(vocab))
+    return spk::fail(SPK_ERR_ARG, "%s: %zu slot words < %zu for vocab %d", name, slot_words,
+                     spk_lm_head_take_slots(vocab), vocab);
+  if (pos && (!count || !history)) return spk::fail(SPK_ERR_NULL, "%s: count/history NULL with pos", name);
+  if (vocab <= 0 || hidden <= 0 || hidden % 512 != 0 || hidden > 4096 || (norm_w && hidden != kHidden))
+    return spk::fail(SPK_ERR_SHAPE, "%s: vocab %d hidden %d (multiple of 512, <= 4096; 1024 with norm_w)", name,
+                     vocab, hidden);
+  if (!spk::aligned(W, 16) || !spk::aligned(x, 16) || !spk::aligned(slots, 8) || (norm_w && !spk::aligned(norm_w, 8)))
+    return spk::fail(SPK_ERR_ALIGN, "%s: W/x must be 16-byte aligned, slots and norm_w 8-byte", name);
+  constexpr int R = kLmKeyRows;
+  const uint32_t E = (uint32_t)((vocab + 255) / 256);
+  const int blocks = (int)spk_lm_head_take_slots(vocab);
+  const TakeArgs take{reinterpret_cast<unsigned long long*>(slots), blocks, out_index, pos, count, history, capacity};
+  hipStream_t s = spk::to_hip(stream);
+  // one more workgroup than the rows need: the last one takes the argmax
+  if (norm_w) {
+    hipLaunchKernelGGL((lm_head_key_kernel<2, R, true, true>), dim3(blocks + 1), dim3(256), 0, s, W, x, norm_w,
+                       logits, vocab, E, nullptr, take);
+    return spk::check_launch(name);
+  }
+#define SPK_LMT_CASE(n8)                                                                                      \
+  case n8:                                                                                                    \
+    hipLaunchKernelGGL((lm_head_key_kernel<n8, R, false, true>), dim3(blocks + 1), dim3(256), 0, s, W, x,    \
+                       nullptr, logits, vocab, E, nullptr, take);                                             \
+    break;
+  switch (hidden / 512) {
+    SPK_LMT_CASE(1)
+    SPK_LMT_CASE(2)
+    SPK_LMT_CASE(3)
+    SPK_LMT_CASE(4)
+    SPK_LMT_CASE(5)
+    SPK_LMT_CASE(6)
+    SPK_LMT_CASE(7)
+    SPK_LMT_CASE(8)
+    default:
+      return spk::fail(SPK_ERR_SHAPE, "%s: hidden %d", name, hidden);
+  }
+#undef SPK_LMT_CASE
+  return spk::check_launch(name);
 }
 
 extern "C" int spk_record_token(const int32_t* token, int32_t* pos, int32_t* count, int32_t* history,

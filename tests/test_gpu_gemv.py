@@ -92,28 +92,39 @@ def test_argmax_tie_rule(dev, oracle, i):
     assert int(out.cpu()[0]) == oracle.argmax_f16(v.view(np.uint16))
 
 
-def _key_path(dev, W, x, norm_w=None, logits=None):
-    """spk_lm_head_argmax_key + spk_argmax_key_take through the C ABI."""
+def _key_path(dev, W, x, norm_w=None, logits=None, one=False):
+    """Through the C ABI: spk_lm_head_argmax_key + spk_argmax_key_take, or
+    (one=True) spk_lm_head_argmax_take, the same in one launch."""
     from spock_amd import _lib
     lib = _lib.lib()
     s = torch.cuda.current_stream().cuda_stream
     vocab, hidden = W.shape
-    key = torch.zeros(64, dtype=torch.int64, device=dev)  # SPK_ARGMAX_KEY_WORDS
     idx = torch.full((1,), -1, dtype=torch.int32, device=dev)
-    rc = lib.spk_lm_head_argmax_key(W.data_ptr(), x.data_ptr(), None if norm_w is None else norm_w.data_ptr(),
-                                    vocab, hidden, None if logits is None else logits.data_ptr(), key.data_ptr(), s)
-    _lib.check(rc, "spk_lm_head_argmax_key")
-    _lib.check(lib.spk_argmax_key_take(key.data_ptr(), vocab, idx.data_ptr(), None, None, None, 0, s),
-               "spk_argmax_key_take")
+    nw = None if norm_w is None else norm_w.data_ptr()
+    lg = None if logits is None else logits.data_ptr()
+    if one:
+        n = lib.spk_lm_head_take_slots(vocab)
+        key = torch.zeros(n, dtype=torch.int64, device=dev)
+        rc = lib.spk_lm_head_argmax_take(W.data_ptr(), x.data_ptr(), nw, vocab, hidden, lg, key.data_ptr(), n,
+                                         idx.data_ptr(), None, None, None, 0, s)
+        _lib.check(rc, "spk_lm_head_argmax_take")
+    else:
+        key = torch.zeros(64, dtype=torch.int64, device=dev)  # SPK_ARGMAX_KEY_WORDS
+        rc = lib.spk_lm_head_argmax_key(W.data_ptr(), x.data_ptr(), nw, vocab, hidden, lg, key.data_ptr(), s)
+        _lib.check(rc, "spk_lm_head_argmax_key")
+        _lib.check(lib.spk_argmax_key_take(key.data_ptr(), vocab, idx.data_ptr(), None, None, None, 0, s),
+                   "spk_argmax_key_take")
     torch.cuda.synchronize()
-    assert not key.cpu().numpy().any()  # the take leaves the key words at zero
+    assert not key.cpu().numpy().any()  # the take leaves the key words / slots at zero
     return int(idx.cpu()[0])
 
 
+@pytest.mark.parametrize("one", [False, True])
 @pytest.mark.parametrize("norm", [False, True])
-def test_lm_head_argmax_key_config3(dev, oracle, norm):
-    """Final norm + lm_head + argmax in one launch (device atomic max of the
-    argmax keys) against the oracle: bit-exact logits and index."""
+def test_lm_head_argmax_key_config3(dev, oracle, norm, one):
+    """Final norm + lm_head + argmax (device atomic max of the argmax keys,
+    then the take; or one launch whose last workgroup takes the per-workgroup
+    key slots) against the oracle: bit-exact logits and index."""
     import oracle_model
     from spock_amd import synth
     V, Hd = 248320, 1024
@@ -128,15 +139,16 @@ def test_lm_head_argmax_key_config3(dev, oracle, norm):
     e_idx, e_logits = oracle.lm_head_argmax(W, x)
     logits = torch.empty(V, dtype=torch.float16, device=dev)
     Wd = _t(dev, W)
-    got = _key_path(dev, Wd, _t(dev, h), None if nw is None else _t(dev, nw), logits)
+    got = _key_path(dev, Wd, _t(dev, h), None if nw is None else _t(dev, nw), logits, one=one)
     assert np.array_equal(logits.cpu().numpy().view(np.uint16), e_logits)
     assert got == e_idx
     # again without logits (the key words were returned to zero by the take)
-    assert _key_path(dev, Wd, _t(dev, h), None if nw is None else _t(dev, nw)) == e_idx
+    assert _key_path(dev, Wd, _t(dev, h), None if nw is None else _t(dev, nw), one=one) == e_idx
 
 
-@pytest.mark.parametrize("vocab,hidden", [(1000, 512), (77777, 2048), (4096, 1024)])
-def test_lm_head_argmax_key_ties(dev, oracle, vocab, hidden):
+@pytest.mark.parametrize("one", [False, True])
+@pytest.mark.parametrize("vocab,hidden", [(1000, 512), (77777, 2048), (4096, 1024), (1, 512), (33, 4096)])
+def test_lm_head_argmax_key_ties(dev, oracle, vocab, hidden, one):
     """Rows repeated across the vocabulary make exact logit ties; the key path
     keeps argmax.comp's tie rule (same index as the oracle)."""
     from spock_amd import synth
@@ -144,4 +156,42 @@ def test_lm_head_argmax_key_ties(dev, oracle, vocab, hidden):
     W = np.ascontiguousarray(base[np.arange(vocab) % 37])
     x = synth.gemv_input(hidden, seed=hidden)
     e_idx, _ = oracle.lm_head_argmax(W, x)
-    assert _key_path(dev, _t(dev, W), _t(dev, x)) == e_idx
+    assert _key_path(dev, _t(dev, W), _t(dev, x), one=one) == e_idx
+
+
+def test_lm_head_argmax_take_bookkeeping_and_invalid_rows(dev, oracle):
+    """The one-launch form records the token as spk_argmax_key_take does
+    (history[count] = index, count += 1, pos += 1; no history write once count
+    reaches the capacity), over several calls in a row on one slot array; rows
+    whose logits are -inf or NaN never win, and a whole workgroup of them
+    still fills its slot."""
+    from spock_amd import _lib, synth
+    lib = _lib.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    V, Hd = 5000, 1024
+    W = synth.gemv_weights(V, Hd, seed=7)
+    W[:600] = np.float16(np.nan).view(np.uint16)  # rows 0..599: NaN logits (whole workgroups)
+    W[600:700] = np.float16(-np.inf).view(np.uint16)
+    x = synth.gemv_input(Hd, seed=8)
+    Wd, xd = _t(dev, W), _t(dev, x)
+    n = lib.spk_lm_head_take_slots(V)
+    slots = torch.zeros(n, dtype=torch.int64, device=dev)
+    idx = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    pos = torch.tensor([10], dtype=torch.int32, device=dev)
+    hist = torch.full((1 + 3,), -7, dtype=torch.int32, device=dev)  # [count | history of capacity 3]
+    hist[0] = 0
+    e_idx, _ = oracle.lm_head_argmax(W, x)
+    assert e_idx >= 700
+    for call in range(5):
+        _lib.check(lib.spk_lm_head_argmax_take(Wd.data_ptr(), xd.data_ptr(), None, V, Hd, None, slots.data_ptr(), n,
+                                               idx.data_ptr(), pos.data_ptr(), hist.data_ptr(),
+                                               hist[1:].data_ptr(), 3, s), "spk_lm_head_argmax_take")
+        torch.cuda.synchronize()
+        assert int(idx.cpu()[0]) == e_idx
+        assert not slots.cpu().numpy().any()
+    assert int(pos.cpu()[0]) == 15
+    h = hist.cpu().numpy()
+    assert h[0] == 5 and list(h[1:]) == [e_idx] * 3
+    # too few slot words is an argument error, before any launch
+    assert lib.spk_lm_head_argmax_take(Wd.data_ptr(), xd.data_ptr(), None, V, Hd, None, slots.data_ptr(), n - 1,
+                                       idx.data_ptr(), None, None, None, 0, s) == -5
