@@ -55,10 +55,11 @@ enum {
                                     2204-2218): events after each layer, lm_head and
                                     argmax; the step's kernels are then launched one
                                     by one, since a recorded graph holds no events */
-  SPK_MODEL_LMHEAD_TWO_LAUNCH = 16  /* final norm + lm_head + argmax as the key launch
-                                    then the take (spk_lm_head_argmax_key,
-                                    spk_argmax_key_take) instead of one launch
-                                    (spk_lm_head_argmax_take); same tokens */
+  SPK_MODEL_LMHEAD_ONE_LAUNCH = 16  /* final norm + lm_head + argmax in one launch
+                                    (spk_lm_head_argmax_take) instead of the key
+                                    launch then the take (spk_lm_head_argmax_key,
+                                    spk_argmax_key_take); same tokens, measured
+                                    about 1 us per token slower */
 };
 
 /* Opens <repack_dir>, uploads every tensor, allocates the per-layer state for
@@ -88,11 +89,11 @@ int spk_model_gpu_token_us(const SpkModel* m, double* us, int32_t capacity, int3
  * 4139-4176), SPK_MODEL_GPU_REGIONS only: microseconds per region summed over
  * the steps, in step order: "layer_0" .. "layer_<n-1>" ("layer_0" includes the
  * embedding gather, which its input norm reads directly, so there is no
- * "embedding" region), "lm_head" (final norm, lm_head and the argmax in one
- * launch, so no separate "final_norm"; with SPK_MODEL_LMHEAD_TWO_LAUNCH the
- * argmax key only), "argmax" (with SPK_MODEL_LMHEAD_TWO_LAUNCH the take that
- * records the token; empty otherwise, the lm_head launch records it).  *name
- * stays valid until the next spk_model_generate call. */
+ * "embedding" region), "lm_head" (final norm, lm_head and the argmax key in
+ * one launch, so no separate "final_norm"; with SPK_MODEL_LMHEAD_ONE_LAUNCH
+ * the whole argmax), "argmax" (the take that records the token; empty with
+ * SPK_MODEL_LMHEAD_ONE_LAUNCH).  *name stays valid until the next
+ * spk_model_generate call. */
 int spk_model_gpu_region_count(const SpkModel* m, int32_t* count);
 int spk_model_gpu_region(const SpkModel* m, int32_t index, const char** name, double* us);
 

@@ -474,10 +474,11 @@ void Qwen35Session::enqueue_decode_step() {
 }
 
 // Final norm, lm_head and argmax of hidden row h; the token goes to *tok and
-// is recorded in the history (count, position).  One launch
-// (spk_lm_head_argmax_take) by default, else the key launch then the take;
-// with region marks, "lm_head" ends after the first launch and "argmax" after
-// the take (empty in the one-launch form).
+// is recorded in the history (count, position).  The key launch then the take
+// by default, else one launch (spk_lm_head_argmax_take; measured on one box,
+// config 4: 679.7-680.5 vs 678.4-678.9 us per token for the pair, lm_head
+// alone 83.8 vs 83.1 us); with region marks, "lm_head" ends after the first
+// launch and "argmax" after the take (empty in the one-launch form).
 void Qwen35Session::lm_head_token(const std::uint16_t* h, std::uint32_t* tok, bool marks) {
   const int32_t vocab = static_cast<int32_t>(shape_.vocab);
   std::int32_t* hist = history_.get<std::int32_t>();
@@ -708,7 +709,7 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
   const int rc = guarded([&] {
     if (!repack_dir) throw std::runtime_error("spk_model_open: NULL directory");
     if (flags & ~(SPK_MODEL_NO_GRAPH | SPK_MODEL_MATRIX_PREFILL | SPK_MODEL_GPU_TIMESTAMPS | SPK_MODEL_GPU_REGIONS |
-                  SPK_MODEL_LMHEAD_TWO_LAUNCH))
+                  SPK_MODEL_LMHEAD_ONE_LAUNCH))
       throw std::runtime_error("spk_model_open: unknown flags");
     using spock::hip::GpuTimestamps;
     const GpuTimestamps ts = (flags & SPK_MODEL_GPU_REGIONS)      ? GpuTimestamps::per_region
@@ -718,7 +719,7 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
                                                          max_seq > 0 ? static_cast<std::uint32_t>(max_seq) : 0u,
                                                          (flags & SPK_MODEL_NO_GRAPH) == 0,
                                                          (flags & SPK_MODEL_MATRIX_PREFILL) == 0, ts,
-                                                         (flags & SPK_MODEL_LMHEAD_TWO_LAUNCH) == 0);
+                                                         (flags & SPK_MODEL_LMHEAD_ONE_LAUNCH) != 0);
     m = new SpkModel{std::move(s), {}};
   });
   return rc == 0 ? m : nullptr;

@@ -72,7 +72,7 @@ class Qwen35Session {
   // holds no timing events).
   explicit Qwen35Session(const std::string& repack_dir, bool verbose = false, std::uint32_t max_seq = MAX_SEQ,
                          bool use_graph = true, bool ordered_prefill = true,
-                         GpuTimestamps gpu_timestamps = GpuTimestamps::off, bool lm_head_one_launch = true);
+                         GpuTimestamps gpu_timestamps = GpuTimestamps::off, bool lm_head_one_launch = false);
   ~Qwen35Session();
   Qwen35Session(const Qwen35Session&) = delete;
   Qwen35Session& operator=(const Qwen35Session&) = delete;
@@ -130,7 +130,7 @@ class Qwen35Session {
   bool verbose_ = false;
   bool use_graph_ = true;
   bool ordered_prefill_ = true;
-  bool lm_one_launch_ = true;  // spk_lm_head_argmax_take, else the key + take pair
+  bool lm_one_launch_ = false;  // spk_lm_head_argmax_take, else the key + take pair
   Qwen35Shape shape_;
   std::uint32_t max_seq_ = MAX_SEQ;
   std::uint32_t n_dn_ = 0, n_attn_ = 0;

@@ -944,6 +944,12 @@ struct TakeArgs {
   int cap;
 };
 
+// Slots one thread of the taker reads per group, all issued before any is
+// used: a poll is one memory round trip per 256 x kTakePer slots (read one
+// after the other, each waited for, a poll of 7,760 slots took ~30 loads'
+// latency).
+constexpr int kTakePer = 32;
+
 __device__ __forceinline__ void take_slots(const TakeArgs& t, uint32_t E) {
   const int tid = threadIdx.x;
   unsigned long long best = 0ull;
@@ -951,13 +957,20 @@ __device__ __forceinline__ void take_slots(const TakeArgs& t, uint32_t E) {
   for (int it = 0; it < kTakePolls && missing; ++it) {
     best = 0ull;
     int miss = 0;
-    for (int j = tid; j < t.nblocks; j += 256) {
-      const unsigned long long v = __hip_atomic_load(t.slots + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      best = spk::umax64(best, v);
-      miss |= (v == 0ull);
+    for (int j0 = 0; j0 < t.nblocks; j0 += 256 * kTakePer) {
+      unsigned long long v[kTakePer];
+#pragma unroll
+      for (int i = 0; i < kTakePer; ++i)  // past the end: the last slot again
+        v[i] = __hip_atomic_load(t.slots + min(j0 + tid + 256 * i, t.nblocks - 1), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int i = 0; i < kTakePer; ++i) {
+        best = spk::umax64(best, v[i]);
+        miss |= (v[i] == 0ull);
+      }
     }
     missing = __syncthreads_or(miss);
-    if (missing) __builtin_amdgcn_s_sleep(4);
+    if (missing) __builtin_amdgcn_s_sleep(2);
   }
   best = spk::block_max_u64<256>(best);
   for (int j = tid; j < t.nblocks; j += 256)
