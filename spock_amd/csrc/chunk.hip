@@ -8,26 +8,33 @@
 //   A  = lower(q_i . k_j * scale * Gamma_ij)
 //   v_new = U - W S,  o = (Q scale e^gcum) S + A v_new,
 //   S <- e^{gcum_last} S + (K e^{gcum_last - gcum})^T v_new.
+// Computed here with T moved next to the matrices that meet it:
+//   R  = V * beta - (K S) * beta e^gcum          (so v_new = T R)
+//   o  = (Q scale e^gcum) S + (A T) R
+//   S <- e^{gcum_last} S + K'^T R,  K' = T^T diag(e^{gcum_last - gcum}) K
+// -- the same sums in another association (measured in fp32 against the
+// reference algorithm: same distance from the fp64 result).  A T and K' do
+// not depend on S, so all chunks form them in parallel; U, W and v_new are
+// never stored.
 //
 // Two launches:
 //  1. chunk_intra_kernel -- one workgroup per (chunk, head), all chunks of all
 //     sequences in parallel.  Every global load is issued up front; K rows
-//     are staged in LDS in the input type, V goes straight into the
-//     registers of the U products' B operand (34 KB of LDS for fp16, so four
+//     are staged in LDS in the input type (34 KB of LDS for fp16, so four
 //     workgroups share a CU).  K K^T and Q K^T are 16x16x4 fp32 MFMA tiles,
 //     five independent accumulators per wavefront; T is inverted blockwise (4
 //     diagonal 16x16 blocks by per-lane forward substitution, written over L's,
-//     off-diagonal blocks T_IJ = -T_II sum_M L_IM T_MJ as MFMA products); U
-//     and W are MFMA products over the nonzero blocks of T with beta and the
-//     decays applied to the B operand as it is read.  U^T, W, A and the
-//     per-token scales go to the workspace.
+//     off-diagonal blocks T_IJ = -T_II sum_M L_IM T_MJ as MFMA products); A T
+//     and K' are MFMA products over the nonzero blocks of T with Ks applied to
+//     the K operand as it is read.  They go to the workspace with the
+//     per-token scales.
 //  2. chunk_state_kernel -- one workgroup per (sequence, head, 16-column tile
 //     of the value dim): columns of S evolve independently, so the sequential
 //     chunk scan runs on 8*H*num_seqs workgroups.  The 128x16 state tile lives
-//     in LDS; wavefront M owns token block M of W S, Q S and the output, and
-//     state rows 32M..32M+31 of the update (S += K^T diag(Ks) v_new), all
-//     16x16x4 MFMA, with the next chunk's operands prefetched into registers
-//     during the current one.
+//     in LDS; wavefront M owns token block M of K S, Q S, R and the output,
+//     and state rows 32M..32M+31 of the update (S += K'^T R), all 16x16x4
+//     MFMA, with the next chunk's operands prefetched into registers during
+//     the current one.
 // MFMA operand trick: the contraction index of a 16x16x4 step is a free
 // permutation, so lane (m = l%16, g = l/16) reads a float4 at k = 16u + 4g and
 // feeds its elements to 4 consecutive steps; the B operand uses the same map.
@@ -57,28 +64,35 @@ __device__ __forceinline__ void ws_store(void* p, uint32_t a, uint32_t b) {
 
 constexpr int kC = 64;
 constexpr int kD = 128;
-// Workspace record per (chunk, head), in floats.  The matrices are stored in
-// the state scan's MFMA fragment order: fragment f of wavefront M is 64 lanes
-// x 4 consecutive contraction-index elements, so every load of the scan reads
-// one contiguous 1 KB (fp32) or 512 B (fp16) block.  Loads whose 64 lanes
-// touch 16 separate rows (the row-major alternative) cost the vector-memory
-// pipe several times more per byte.  Lane l = 16*lg + li.
-//   W   [M 4][u 8][lane][4]   W[16M+li][16u+4lg+e]                 fp32
-//   U   [tile 8][M 4][lane][4] U[16M+4lg+e][16 tile+li]             fp32
-//   A   [M 4][J 4][lane][4]   A[16M+li][16J+4lg+e], blocks J <= M   fp32
-//   Qs  [64] Q scale (q_scale iq e^gcum)   Ks [64] e^{gL - gcum} ik
+// Workspace record per (chunk, head), in floats.  The chunk rule is stored
+// with T = (I + L)^{-1} folded into the two matrices that meet it: with
+// R = beta*V - (beta e^g ik)*(K S) (per-token row scales),
+//   v_new = U - W S = T R,   o = Qs*(Q S) + (A T) R,
+//   S' = e^{gL} S + K^T diag(Ks) v_new = e^{gL} S + K'^T R,  K' = T^T diag(Ks) K,
+// so the scan needs A T and K' (and raw K, Q, V from the input) instead of
+// U, W and A: 42 KB of record instead of 74 KB, and the intra kernel never
+// reads V.  The matrices are in the scan's MFMA fragment order: fragment f of
+// wavefront M is 64 lanes x 4 consecutive elements, so every load of the scan
+// reads one contiguous 1 KB block.  Loads whose 64 lanes touch 16 separate
+// rows (the row-major alternative) cost the vector-memory pipe several times
+// more per byte.  Lane l = 16*lg + li.
+//   K'  [M 4][u 4][t 2][lane][4]  K'[16u+4lg+e][32M+2li+t]          fp32
+//   AT  [M 4][J 4][lane][4]       (A T)[16M+li][16J+4lg+e], J <= M   fp32
+//   Qs  [64] Q scale (q_scale iq e^gcum)
+//   C1  [64] beta           C2 [64] beta e^gcum ik
 //   Misc[0] e^{gL}
-// A's blocks above the diagonal (zero) are neither stored nor multiplied, and
-// the scan reads raw Q and raw K from the input rows rather than from record
-// copies: 38 of the ~115 KB a record would hold (fp16 inputs) that the intra
-// kernel does not write.
-constexpr int kWsW = 0;
-constexpr int kWsU = 8192;
-constexpr int kWsA = 16384;
-constexpr int kWsQs = 20480;
-constexpr int kWsKs = 20544;
-constexpr int kWsMisc = 20608;
-constexpr int kWsStride = 20672;  // 82688 bytes, a multiple of 256
+//   Kr  [M 4][u 8][lane][4]       K[16M+li][16u+4lg+e], raw input type
+// A T's blocks above the diagonal (zero) are neither stored nor multiplied.
+// Kr is the scan's stage-A operand: raw K rows read from the input instead
+// (16 rows of 32 bytes per load instruction) made the scan 25% slower.
+constexpr int kWsKp = 0;
+constexpr int kWsA = 8192;
+constexpr int kWsQs = 12288;
+constexpr int kWsC1 = 12352;
+constexpr int kWsC2 = 12416;
+constexpr int kWsMisc = 12480;
+constexpr int kWsKr = 12544;      // 8192 elements: 16 KB (fp16) or 32 KB (fp32)
+constexpr int kWsStride = 20736;  // 82944 bytes, a multiple of 256
 // Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
 // which untyped loads/stores need for the num_records range check to apply.
 constexpr int kBufDword3 = 0x00020000;
@@ -180,14 +194,6 @@ template <typename TIn> struct RawOf;
 template <> struct RawOf<float> {
   static __device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
   static __device__ __forceinline__ float4 cvt4(const float4& r) { return r; }
-  // two adjacent elements of a row through a buffer resource (0 past its range)
-  typedef float2 Pair;
-  static __device__ __forceinline__ Pair ld_pair(__amdgpu_buffer_rsrc_t r, int voff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
-    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
-  }
-  static __device__ __forceinline__ float lo(Pair v) { return v.x; }
-  static __device__ __forceinline__ float hi(Pair v) { return v.y; }
 };
 template <> struct RawOf<uint16_t> {
   // 4 halves kept as two 32-bit words in .x/.y of a float4
@@ -200,48 +206,38 @@ template <> struct RawOf<uint16_t> {
     return make_float4(spk::h2f((uint16_t)(x & 0xffffu)), spk::h2f((uint16_t)(x >> 16)),
                        spk::h2f((uint16_t)(y & 0xffffu)), spk::h2f((uint16_t)(y >> 16)));
   }
-  typedef uint32_t Pair;
-  static __device__ __forceinline__ Pair ld_pair(__amdgpu_buffer_rsrc_t r, int voff) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
-  }
-  static __device__ __forceinline__ float lo(Pair v) { return spk::h2f((uint16_t)(v & 0xffffu)); }
-  static __device__ __forceinline__ float hi(Pair v) { return spk::h2f((uint16_t)(v >> 16)); }
 };
 
-// V operand of the U products: rows 16u+4lg+e (u, e = 0..3) of one value
-// column, read through a buffer resource of the chunk's len rows, so rows past
-// the chunk read 0 (the hardware range check) with no clamp or select.  fp16
-// rows are packed two to a register.
+// V elements of the scan's stage B: rows 16M+4lg+e (e = 0..3) of value
+// column n0+li, read through a buffer resource of the chunk's len rows, so
+// rows past the chunk read 0 (the hardware range check) with no clamp or
+// select.  fp16 rows are packed two to a register.
 // The whole byte offset goes in the VGPR offset and the scalar offset stays 0:
 // on gfx9-family raw buffers the range check compares only voffset +
 // inst_offset with num_records, so a row offset passed as soffset would read
 // past the chunk (the next sequence's rows, or past the tensor) unchecked.
-template <typename TIn> struct VOperand;
-template <> struct VOperand<float> {
-  float x[4][4];
+template <typename TIn> struct VTile;
+template <> struct VTile<float> {
+  float x[4];
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int voff) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        x[u][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + (16 * u + e) * kD * 4, 0, 0));
+    for (int e = 0; e < 4; ++e)
+      x[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + e * kD * 4, 0, 0));
   }
-  __device__ __forceinline__ float get(int u, int e) const { return x[u][e]; }
+  __device__ __forceinline__ float get(int e) const { return x[e]; }
 };
-template <> struct VOperand<uint16_t> {
-  uint32_t x[4][2];
+template <> struct VTile<uint16_t> {
+  uint32_t x[2];
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int voff) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int e = 0; e < 4; e += 2) {
-        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, voff + (16 * u + e) * kD * 2, 0, 0);
-        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(r, voff + (16 * u + e + 1) * kD * 2, 0, 0);
-        x[u][e / 2] = lo | (hi << 16);
-      }
+    for (int e = 0; e < 4; e += 2) {
+      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, voff + e * kD * 2, 0, 0);
+      const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(r, voff + (e + 1) * kD * 2, 0, 0);
+      x[e / 2] = lo | (hi << 16);
+    }
   }
-  __device__ __forceinline__ float get(int u, int e) const {
-    return spk::h2f((uint16_t)((e & 1) ? x[u][e / 2] >> 16 : x[u][e / 2] & 0xffffu));
+  __device__ __forceinline__ float get(int e) const {
+    return spk::h2f((uint16_t)((e & 1) ? x[e / 2] >> 16 : x[e / 2] & 0xffffu));
   }
 };
 
@@ -263,11 +259,10 @@ template <> struct RowStage<uint16_t> {
                        spk::h2f((uint16_t)(u.y & 0xffffu)), spk::h2f((uint16_t)(u.y >> 16)));
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return spk::h2f(s[r * kLd + c]); }
-  // rows r..r+3 of column c, stored as 4 consecutive elements at dst
-  static __device__ __forceinline__ void col4_to(const T* s, int r, int c, T* dst) {
-    const uint32_t a = s[r * kLd + c], b = s[(r + 1) * kLd + c];
-    const uint32_t x = s[(r + 2) * kLd + c], y = s[(r + 3) * kLd + c];
-    ws_store(dst, a | (b << 16), x | (y << 16));
+  // row r, columns c..c+3, stored raw as 4 consecutive elements at dst
+  static __device__ __forceinline__ void row4_to(const T* s, int r, int c, T* dst) {
+    const uint2 u = *reinterpret_cast<const uint2*>(s + r * kLd + c);
+    ws_store(dst, u.x, u.y);
   }
 };
 template <> struct RowStage<float> {
@@ -280,8 +275,9 @@ template <> struct RowStage<float> {
     return *reinterpret_cast<const float4*>(s + r * kLd + c);
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return s[r * kLd + c]; }
-  static __device__ __forceinline__ void col4_to(const T* s, int r, int c, T* dst) {
-    ws_store(dst, s[r * kLd + c], s[(r + 1) * kLd + c], s[(r + 2) * kLd + c], s[(r + 3) * kLd + c]);
+  static __device__ __forceinline__ void row4_to(const T* s, int r, int c, T* dst) {
+    const float4 v = *reinterpret_cast<const float4*>(s + r * kLd + c);
+    ws_store(dst, v.x, v.y, v.z, v.w);
   }
 };
 
@@ -365,13 +361,13 @@ __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, 
 }
 
 // Epilogue of the Gram tiles: L = strict_lower(beta_i k_i.k_j Gamma_ij) into
-// LDS, A = lower(q_i.k_j scale Gamma_ij) into the workspace in fragment order
-// (with the inverse L2 norms when requested; 1 otherwise).  iq_scale is the
-// scale of query row 16 QB + li.
+// LDS; A = lower(q_i.k_j scale Gamma_ij) stays in the K Q^T tiles' registers
+// (replacing the raw dot products) until T is known and A T is formed (with
+// the inverse L2 norms when requested; 1 otherwise).  iq_scale is the scale of
+// query row 16 QB + li.
 template <unsigned KMASK, int QB>
-__device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG, const float* sB,
-                                           const float* sIK, float iq_scale, float* sL, float* ws,
-                                           int li, int lg, int lane) {
+__device__ __forceinline__ void gram_store(f4v (&acc)[5], const float* sG, const float* sB, const float* sIK,
+                                           float iq_scale, float* sL, int li, int lg) {
   constexpr int NT = gram_ntiles<KMASK, QB>();
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -390,14 +386,36 @@ __device__ __forceinline__ void gram_store(const f4v (&acc)[5], const float* sG,
       // lane (li, lg) holds A[i][j], i = 16QB + li, j = 16J + 4lg + r
       const int W = g.I, J = g.J;
       const int i = 16 * W + li;
-      float o[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * J + 4 * lg + r;
         const float dec = __builtin_amdgcn_exp2f((sG[i] - sG[j]) * kLog2e);
-        o[r] = (j <= i) ? (acc[t][r] * (iq_scale * sIK[j])) * dec : 0.0f;
+        acc[t][r] = (j <= i) ? (acc[t][r] * (iq_scale * sIK[j])) * dec : 0.0f;
       }
-      ws_store(ws + kWsA + ((W * 4 + J) * 64 + lane) * 4, o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// (A T)^T blocks of query block QB: lane (li, lg) of block (QB, K), K <= QB,
+// ends up holding (A T)[16 QB + li][16K + 4lg + r] -- the A-operand fragment
+// of the scan's stage C.  MFMA A operand T^T (T's block (J, K) read by
+// column), B operand A^T (the lane's own A values of block J: acc[nK + J]).
+// T is unit lower triangular, so the sum runs over J = K .. QB.
+template <unsigned KMASK, int QB>
+__device__ __forceinline__ void at_store(const f4v (&acc)[5], const float* sL, const float* sT, float* ws,
+                                         int li, int lg, int lane) {
+  if constexpr (QB >= 0) {
+    constexpr int nK = gram_ntiles<KMASK, -1>();  // the K K^T tiles come first
+#pragma unroll
+    for (int K = 0; K <= QB; ++K) {
+      f4v x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int J = K; J <= QB; ++J) {
+        const float* tb = (J == K) ? sL + blk(K, K) : sT + offblk(J, K);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x = mfma4(tb[(4 * lg + e) * 16 + li], acc[nK + J][e], x);
+      }
+      ws_store(ws + kWsA + ((QB * 4 + K) * 64 + lane) * 4, x[0], x[1], x[2], x[3]);
     }
   }
 }
@@ -424,14 +442,24 @@ struct GramTilesOp {
   }
 };
 struct GramStoreOp {
-  const f4v (&acc)[5];
+  f4v (&acc)[5];
   const float *sG, *sB, *sIK;
   float iq_scale;
-  float *sL, *ws;
+  float* sL;
+  int li, lg;
+  template <unsigned KM, int QB>
+  __device__ __forceinline__ void run() const {
+    gram_store<KM, QB>(acc, sG, sB, sIK, iq_scale, sL, li, lg);
+  }
+};
+struct AtStoreOp {
+  const f4v (&acc)[5];
+  const float *sL, *sT;
+  float* ws;
   int li, lg, lane;
   template <unsigned KM, int QB>
   __device__ __forceinline__ void run() const {
-    gram_store<KM, QB>(acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane);
+    at_store<KM, QB>(acc, sL, sT, ws, li, lg, lane);
   }
 };
 
@@ -508,7 +536,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
   __shared__ __align__(16) float sT[6 * 256];   // off-diagonal T blocks
   __shared__ __align__(16) float sG[64];   // gcum
   __shared__ __align__(16) float sB[64];   // beta
-  __shared__ __align__(16) float sBE[64];  // beta e^gcum ik
+  __shared__ __align__(16) float sKS[64];  // Ks = e^{gL - gcum} ik
   __shared__ __align__(16) float sIK[64];  // inverse K norms (1 without L2 normalisation)
 
   int gchunk = blockIdx.x;
@@ -535,12 +563,11 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
   const bool own_block = (wave % PARTS) == part;  // this wave's A block (and raw Q rows)
   const TIn* q = static_cast<const TIn*>(p.q);
   const TIn* k = static_cast<const TIn*>(p.k);
-  const TIn* v = static_cast<const TIn*>(p.v);
   float* ws = p.ws + ((size_t)gchunk * p.H + h) * kWsStride;
 
   // ---- every global load first: g/beta (wave 0), Q row block `wave` as MFMA
   // A-operand registers, 8 K row segments per thread (padding rows read row 0
-  // and are zeroed when staged), the V elements of the U products.
+  // and are zeroed when staged).  V is not needed here: the scan reads it.
   float gv = 0.0f, bv = 0.0f;
   if (wave == 0) {
     const int tt = lane < len ? lane : 0;
@@ -566,22 +593,11 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
     const int r = (tid >> 5) + 8 * it;
     kr[it] = R::ld4(k, ((size_t)h * p.N + t0 + (r < len ? r : 0)) * kD + c4);
   }
-  // V enters only the U products, as their B operand: lane (li, lg) loads
-  // V[16u+4lg+s][16 ct+li] of its column tiles ct straight into registers
-  // (16 lanes read 32 contiguous bytes of a row), so V needs no LDS stage.
-  // Padding rows read 0 (VOperand's buffer range check).
+  // K' column tiles ct = 2M + t of this wavefront (keys 32M + 2c + t)
   constexpr int kTilesPerWave = PARTS == 1 ? 2 : 1;
-  auto u_tile = [&](int jj) {
+  auto kp_tile = [&](int jj) {
     return PARTS == 1 ? 2 * wave + jj : PARTS == 2 ? 4 * part + wave : PARTS == 4 ? 2 * part + (wave & 1) : part;
   };
-  VOperand<TIn> vd[kTilesPerWave];
-  {
-    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<TIn*>(v + ((size_t)h * p.N + t0) * kD), 0, len * kD * (int)sizeof(TIn), kBufDword3);
-#pragma unroll
-    for (int jj = 0; jj < kTilesPerWave; ++jj)
-      vd[jj].load(vr, (4 * lg * kD + 16 * u_tile(jj) + li) * (int)sizeof(TIn));
-  }
   // gcum (running sum in token order, deltanet_chunk.cpp:137-142): lane t adds
   // g_0 .. g_t left to right (adding +0 past t), so every lane's sum is
   // rounded exactly as the reference's running sum
@@ -606,6 +622,14 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
     RS::put4(sK, r, c4, kx);
   }
   __syncthreads();
+
+  // ---- raw K rows of token block `wave` in the scan's stage-A fragment
+  // order (the wavefront owning the block writes them; padding rows are 0)
+  if (own_block) {
+    typename RS::T* kf = reinterpret_cast<typename RS::T*>(ws + kWsKr);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) RS::row4_to(sK, 16 * wave + li, 16 * u + 4 * lg, kf + ((wave * 8 + u) * 64 + lane) * 4);
+  }
 
   // ---- inverse L2 norms (eps inside the sqrt, deltanet_chunk.cpp:27-39):
   // K rows from LDS, 4 threads per row; Q rows from this lane's registers
@@ -641,13 +665,15 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
 
   // ---- epilogue: L into LDS, A into the workspace; per-token scales
   const float iq_scale = iq * p.q_scale;  // lane li of any group: row 16*wave + li
-  gram_dispatch<PARTS>(part, wave, GramStoreOp{acc, sG, sB, sIK, iq_scale, sL, ws, li, lg, lane});
+  gram_dispatch<PARTS>(part, wave, GramStoreOp{acc, sG, sB, sIK, iq_scale, sL, li, lg});
   const float gL = sG[63];
   if (lg == 0 && own_block) ws[kWsQs + 16 * wave + li] = iq_scale * expf(sG[16 * wave + li]);  // the scan re-reads Q raw
   if (tid < 64) {
-    const float eg = expf(sG[tid]);
-    sBE[tid] = sB[tid] * eg * sIK[tid];
-    if (part == 0) ws[kWsKs + tid] = expf(gL - sG[tid]) * sIK[tid];
+    sKS[tid] = expf(gL - sG[tid]) * sIK[tid];
+    if (part == 0) {
+      ws[kWsC1 + tid] = sB[tid];
+      ws[kWsC2 + tid] = sB[tid] * expf(sG[tid]) * sIK[tid];
+    }
   }
   if (tid == 0 && part == 0) ws[kWsMisc] = expf(gL);
   __syncthreads();
@@ -694,59 +720,48 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
     __syncthreads();
   }
 
-  // ---- U = T diag(beta) V and W^T = K^T diag(beta e^g ik) T^T, row blocks
-  // I = 0..3 of 16-column tiles (two per wavefront without a split),
-  // accumulated together; the per-token factors are applied to the V / K
-  // operand as it is read.  W is produced transposed so that each lane holds
-  // four consecutive key dims of one token: the A-operand fragment of the
-  // state scan.
+  // ---- A T for this wavefront's A block (the owner of query block `wave`)
+  gram_dispatch<PARTS>(part, wave, AtStoreOp{acc, sL, sT, ws, li, lg, lane});
+
+  // ---- K' = T^T diag(Ks) K, by 16-column key tiles ct = 2M + t (keys
+  // 32M + 2c + t, c = 0..15: the pair of adjacent keys a lane of the scan's
+  // stage D holds) and row blocks u = 0..3 (two tiles per wavefront without a
+  // split).  MFMA A operand T^T (T's block (J, u) read by column, J >= u),
+  // B operand Ks * K with the per-token factor applied as it is read; lane
+  // (li, lg) ends up holding K'[16u+4lg+r][32M+2li+t].
 #pragma unroll
   for (int jj = 0; jj < kTilesPerWave; ++jj) {
-    const int ct = u_tile(jj);
-    // row blocks I of this wave: {0,3} or {1,2} (4 parts: by wave / 2; 8
-    // parts: by wave % 2, waves 0-1 forming U and 2-3 forming W)
-    const bool odd_rows = PARTS == 4 ? (wave >> 1) != 0 : (wave & 1) != 0;
-    const unsigned imask = PARTS >= 4 ? (odd_rows ? 0x6u : 0x9u) : 0xFu;
-    const int umax = PARTS >= 4 ? (odd_rows ? 2 : 3) : 3;
-    const bool do_u = PARTS < 8 || wave < 2;
-    const bool do_w = PARTS < 8 || wave >= 2;
-    const int n = 16 * ct + li;
-    f4v au[4], aw[4];
+    const int ct = kp_tile(jj);
+    const int M = ct >> 1, t = ct & 1;
+    // row blocks u of this wave: all; {0,3} or {1,2} (4 parts: by wave / 2);
+    // block `wave` (8 parts: 4, 3, 2, 1 block products)
+    const bool odd_rows = (wave >> 1) != 0;
+    const unsigned umask = PARTS == 8 ? (1u << wave) : PARTS == 4 ? (odd_rows ? 0x6u : 0x9u) : 0xFu;
+    const int jmin = PARTS == 8 ? wave : PARTS == 4 ? (odd_rows ? 1 : 0) : 0;
+    const int n = 32 * M + 2 * li + t;
+    f4v ak[4];
 #pragma unroll
-    for (int I = 0; I < 4; ++I) au[I] = aw[I] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 4; ++u) ak[u] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (u > umax) break;
-      const int t = 16 * u + 4 * lg;
-      const float4 bb = *reinterpret_cast<const float4*>(&sB[t]);
-      const float4 be = *reinterpret_cast<const float4*>(&sBE[t]);
-      float vb[4], kb[4];
+    for (int J = 0; J < 4; ++J) {
+      if (J < jmin) continue;
+      const int tk = 16 * J + 4 * lg;
+      const float4 ks = *reinterpret_cast<const float4*>(&sKS[tk]);
+      float kb[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        vb[s] = vd[jj].get(u, s) * elem(bb, s);
-        kb[s] = RS::get1(sK, t + s, n) * elem(be, s);
-      }
+      for (int e = 0; e < 4; ++e) kb[e] = RS::get1(sK, tk + e, n) * elem(ks, e);
 #pragma unroll
-      for (int I = u; I < 4; ++I) {
-        if (!((imask >> I) & 1u)) continue;
-        const float* tp = (I == u) ? sL + blk(I, I) : sT + offblk(I, u);
-        const float4 a4 = *reinterpret_cast<const float4*>(&tp[li * 16 + 4 * lg]);
-        if (do_u) {
+      for (int u = 0; u <= J; ++u) {
+        if (!((umask >> u) & 1u)) continue;
+        const float* tb = (u == J) ? sL + blk(J, J) : sT + offblk(J, u);
 #pragma unroll
-          for (int s = 0; s < 4; ++s) au[I] = mfma4(elem(a4, s), vb[s], au[I]);
-        }
-        if (do_w) {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) aw[I] = mfma4(kb[s], elem(a4, s), aw[I]);
-        }
+        for (int e = 0; e < 4; ++e) ak[u] = mfma4(tb[(4 * lg + e) * 16 + li], kb[e], ak[u]);
       }
     }
-    // U: lane (li, lg) holds U[16I+4lg+r][n]; W^T: W[16I+li][16 ct+4lg+r]
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      if (!((imask >> I) & 1u)) continue;
-      if (do_u) ws_store(ws + kWsU + ((ct * 4 + I) * 64 + lane) * 4, au[I][0], au[I][1], au[I][2], au[I][3]);
-      if (do_w) ws_store(ws + kWsW + ((I * 8 + ct) * 64 + lane) * 4, aw[I][0], aw[I][1], aw[I][2], aw[I][3]);
+    for (int u = 0; u < 4; ++u) {
+      if (!((umask >> u) & 1u)) continue;
+      ws_store(ws + kWsKp + (((M * 4 + u) * 2 + t) * 64 + lane) * 4, ak[u][0], ak[u][1], ak[u][2], ak[u][3]);
     }
     __builtin_amdgcn_sched_barrier(0);  // one column tile's operands live at a time
   }
@@ -770,32 +785,33 @@ __device__ __forceinline__ int lpt_sequence(const ChunkParams& p, int slot) {
 
 constexpr int kTiles = 8;   // 16-column tiles of the value dim per (sequence, head)
 constexpr int kLdST = 132;  // LDS row stride of the transposed state tile (floats)
-constexpr int kLdVT = 68;   // LDS row stride of the transposed v_new tile (floats)
+constexpr int kLdVT = 68;   // LDS row stride of the transposed R tile (floats)
 
 // Operands of one chunk for stage A (prefetched a chunk ahead) and for stages
 // B-D (loaded at the start of the chunk's own step, in flight during stage A).
 struct ScanEarly {
-  float4 w[8];  // W rows: token 16M+li, key dims 16u+4lg..+3
+  float4 k[8];  // raw K (record Kr): token 16M+li, key dims 16u+4lg..+3
   float4 q[8];  // raw Q rows, same map
 };
 template <typename TIn>
 struct ScanLate {
-  float4 a[4];   // A rows: token 16M+li, tokens 16u+4lg..+3
-  typename RawOf<TIn>::Pair kp[16];  // raw K[16u+4lg+k][32M+2li .. +1], index 4u+k
-  float4 u;      // U^T: column n0+li, tokens 16M+4lg..+3
-  float4 ks;     // Ks of tokens 16M+4lg..+3
-  float4 qs;     // Qs of tokens 16M+4lg..+3
+  VTile<TIn> v;  // V: tokens 16M+4lg..+3, column n0+li
+  float4 c1;     // beta of tokens 16M+4lg..+3
+  float4 c2;     // beta e^gcum ik of the same tokens
+  float4 qs;     // Qs of the same tokens
+  float4 a[4];   // A T rows: token 16M+li, tokens 16u+4lg..+3
   float gle;     // e^{gL}
+  float4 kq[4][2];  // K'[16u+4lg..+3][32M+2li+t] at [u][t]
 };
 
 // Sequential chunk scan over one 128x16 state tile: one workgroup of 4
 // wavefronts per (sequence, head, 16-column tile), so a 16-head batch of 8
 // sequences gives 1024 workgroups and three run on each CU (independent
 // barriers: one workgroup's waits are the others' issue slots).  Wavefront M:
-//   A  v_new rows and output rows of token block M: W_M S and Q_M S
-//   B  v_new = U - W S  -> LDS, also scaled by Ks
-//   C  o = qs (Q S) + A v_new -> core
-//   D  S rows 32M..32M+31 <- e^{gL} S + K^T diag(Ks) v_new
+//   A  rows of token block M: K_M S and Q_M S
+//   B  R = beta V - (beta e^g ik) (K S)  -> LDS
+//   C  o = qs (Q S) + (A T) R -> core
+//   D  S rows 32M..32M+31 <- e^{gL} S + K'^T R
 // 100-112 MFMA per wavefront per chunk (stage C: 4 (M+1)).
 // MINB workgroups per CU.  fp16 inputs, large launches: three (168 VGPRs;
 // the instance spills 3): more resident wavefronts measured faster than two
@@ -805,16 +821,15 @@ struct ScanLate {
 // fp16), so they run two workgroups per CU without spilling, as do small
 // fp16 launches.
 // ZERO_INIT (no initial state): S is zero entering each sequence's first
-// chunk, so that chunk's W S and Q S are exactly zero and stage A is skipped.
+// chunk, so that chunk's K S and Q S are exactly zero and stage A is skipped.
 template <typename TIn, bool ZERO_INIT, int MINB>
 __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   typedef RawOf<TIn> R;
-  // S tile and v_new stored transposed ([column][contraction index]) so one
+  // S tile and R stored transposed ([column][contraction index]) so one
   // ds_read_b128 feeds four consecutive MFMA steps; strides 132 and 68 keep
   // the 8-lane groups of a b128 access on distinct banks.
   __shared__ __align__(16) float sST[16 * kLdST];
-  __shared__ __align__(16) float sVT[16 * kLdVT];  // v_new
-  __shared__ __align__(16) float sVS[16 * kLdVT];  // v_new scaled by Ks
+  __shared__ __align__(16) float sVT[16 * kLdVT];  // R = beta V - (beta e^g ik) K S
 
   // Workgroup -> (tile, head, sequence).  Groups (sequence, head) are dealt
   // longest sequence first so the longest chunk scans start earliest, and the
@@ -868,41 +883,42 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   // rather than guarded), so the compiler's vmcnt bookkeeping stays exact.
   // Each load instruction reads one contiguous fragment.
   auto record = [&](int c) { return p.ws + ((size_t)(co + c) * p.H + h) * kWsStride; };
-  // raw Q row 16M+li of chunk c from the input (padding rows read the
-  // chunk's row 0, as the intra kernel's Q operand does; qs zeroes them)
-  const TIn* qin = static_cast<const TIn*>(p.q) + ((size_t)h * p.N + t_begin) * kD + 4 * lg;
+  // raw K rows of token block M from the record (fragment order), raw Q rows
+  // 16M+li from the input (padding rows read the chunk's row 0, as the intra
+  // kernel's Q operand does; their output rows are dropped)
+  const size_t in_off = ((size_t)h * p.N + t_begin) * kD;
+  const TIn* qin = static_cast<const TIn*>(p.q) + in_off + 4 * lg;
   auto load_early = [&](ScanEarly& e, int c) {
-    const float* ws = record(c);
+    const TIn* kf = reinterpret_cast<const TIn*>(record(c) + kWsKr) + (M * 8 * 64 + lane) * 4;
     const int row = 16 * M + li;
     const TIn* qrow = qin + (size_t)(c * kC + (row < L - c * kC ? row : 0)) * kD;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      e.w[u] = *reinterpret_cast<const float4*>(ws + kWsW + ((M * 8 + u) * 64 + lane) * 4);
+      e.k[u] = R::ld4(kf, u * 64 * 4);
       e.q[u] = R::ld4(qrow, 16 * u);
     }
   };
-  // Stage D's K operand comes straight from the input rows: kp[4u+k] holds
-  // K[16u+4lg+k][32M+2li .. 32M+2li+1] (16 lanes read 64 or 128 contiguous
-  // bytes of a row), through a buffer resource of the chunk's len rows, so
-  // padding rows read 0.  Issued last: stage D uses them last, and a wave's
-  // loads complete in issue order.
-  const TIn* kin = static_cast<const TIn*>(p.k) + ((size_t)h * p.N + t_begin) * kD;
+  // Stage B-D operands, in the order the stages use them (a wave's loads
+  // complete in issue order): V through a buffer resource of the chunk's len
+  // rows (padding rows read 0) and the per-token factors, then A T, then K'.
+  const TIn* vin = static_cast<const TIn*>(p.v) + in_off;
   auto load_late = [&](ScanLate<TIn>& l, int c) {
     const float* ws = record(c);
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<TIn*>(vin + (size_t)c * kC * kD), 0, min(kC, L - c * kC) * kD * (int)sizeof(TIn), kBufDword3);
+    l.v.load(vr, ((16 * M + 4 * lg) * kD + n0 + li) * (int)sizeof(TIn));
+    l.c1 = *reinterpret_cast<const float4*>(ws + kWsC1 + 16 * M + 4 * lg);
+    l.c2 = *reinterpret_cast<const float4*>(ws + kWsC2 + 16 * M + 4 * lg);
+    l.qs = *reinterpret_cast<const float4*>(ws + kWsQs + 16 * M + 4 * lg);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       l.a[u] = *reinterpret_cast<const float4*>(ws + kWsA + ((M * 4 + u) * 64 + lane) * 4);
-    l.u = *reinterpret_cast<const float4*>(ws + kWsU + ((tile * 4 + M) * 64 + lane) * 4);
-    l.ks = *reinterpret_cast<const float4*>(ws + kWsKs + 16 * M + 4 * lg);
-    l.qs = *reinterpret_cast<const float4*>(ws + kWsQs + 16 * M + 4 * lg);
     l.gle = ws[kWsMisc];
-    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<TIn*>(kin + (size_t)c * kC * kD), 0, min(kC, L - c * kC) * kD * (int)sizeof(TIn), kBufDword3);
-    const int voff = (4 * lg * kD + 32 * M + 2 * li) * (int)sizeof(TIn);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) l.kp[4 * u + k] = R::ld_pair(kr, voff + (16 * u + k) * kD * (int)sizeof(TIn));
+      for (int t = 0; t < 2; ++t)
+        l.kq[u][t] = *reinterpret_cast<const float4*>(ws + kWsKp + (((M * 4 + u) * 2 + t) * 64 + lane) * 4);
   };
 
   // zero_s: S is zero (first chunk without an initial state)
@@ -910,8 +926,8 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     const int tok0 = t_begin + c * kC;
     const int len = min(kC, L - c * kC);
 
-    // ---- stage A: W_M S and Q_M S share the B operand (S); the per-row Q
-    // scale is applied to the product
+    // ---- stage A: K_M S and Q_M S share the B operand (S); the per-row
+    // factors are applied to the products
     f4v aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
     if constexpr (!decltype(zero_s)::value) {
       // the S piece of step u+1 is read while step u's MFMAs run
@@ -920,15 +936,16 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
       for (int u = 0; u < 8; ++u) {
         const float4 sb = sb_next;
         if (u + 1 < 8) sb_next = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * (u + 1) + 4 * lg]);
+        const float4 xk = R::cvt4(e.k[u]);
         const float4 x = R::cvt4(e.q[u]);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          aw = mfma4(elem(e.w[u], k), elem(sb, k), aw);
+          aw = mfma4(elem(xk, k), elem(sb, k), aw);
           aq = mfma4(elem(x, k), elem(sb, k), aq);
         }
       }
       // The loads issued just before this stage (same scheduling region, about
-      // 40 of them) are spread over the MFMA stream rather than issued as one
+      // 36 of them) are spread over the MFMA stream rather than issued as one
       // burst, which would queue in the CU's vector-memory pipe behind the
       // other wavefronts' bursts: 2 and 3 loads around each 4 MFMAs.  Measured
       // on config 2 (ms per call, same box, bit-identical): 2+3 0.875-0.878,
@@ -947,18 +964,18 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
       }
     }
 
-    // ---- stage B: v_new = U - W S, and v_new scaled by Ks for the update
+    // ---- stage B: R = beta V - (beta e^g ik) (K S) for the rows of token
+    // block M (v_new = T R itself is never formed: T sits in A T and K')
     {
-      const float4 v = make_float4(l.u.x - aw[0], l.u.y - aw[1], l.u.z - aw[2], l.u.w - aw[3]);
-      const int tok = 16 * M + 4 * lg;
-      *reinterpret_cast<float4*>(&sVT[li * kLdVT + tok]) = v;
-      *reinterpret_cast<float4*>(&sVS[li * kLdVT + tok]) =
-          make_float4(v.x * l.ks.x, v.y * l.ks.y, v.z * l.ks.z, v.w * l.ks.w);
+      float r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = elem(l.c1, e) * l.v.get(e) - elem(l.c2, e) * aw[e];
+      *reinterpret_cast<float4*>(&sVT[li * kLdVT + 16 * M + 4 * lg]) = make_float4(r[0], r[1], r[2], r[3]);
     }
     __syncthreads();
 
-    // ---- stage C: o = qs (Q S) + A v_new over the blocks J <= M of A's row
-    // block (two accumulator chains: J = 0, 1 and J = 2, 3)
+    // ---- stage C: o = qs (Q S) + (A T) R over the blocks J <= M of A T's
+    // row block (two accumulator chains: J = 0, 1 and J = 2, 3)
     {
       float4 vb[4];
 #pragma unroll
@@ -988,11 +1005,9 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(aq[r]), out,
                                             ((16 * M + 4 * lg + r) * kD + n0 + li) * (int)sizeof(float), 0, 0);
 
-    // ---- stage D: S^T <- e^{gL} S^T + (Ks v_new)^T K, computed transposed so
-    // that K is the B operand read from its rows: lane (li, lg) holds
-    // S^T[column 4lg+r][key 32M+2li+t] in s0 (t = 0) and s1 (t = 1).  Each
-    // output element gets the same products in the same order as
-    // K^T (Ks v_new) would.
+    // ---- stage D: S^T <- e^{gL} S^T + R^T K', computed transposed so that
+    // K' is the B operand in the record's fragment order: lane (li, lg) holds
+    // S^T[column 4lg+r][key 32M+2li+t] in s0 (t = 0) and s1 (t = 1).
     f4v s0, s1;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1002,14 +1017,14 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     }
     float4 vs[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) vs[u] = *reinterpret_cast<const float4*>(&sVS[li * kLdVT + 16 * u + 4 * lg]);
+    for (int u = 0; u < 4; ++u) vs[u] = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float a = elem(vs[u], k);
-        s0 = mfma4(a, R::lo(l.kp[4 * u + k]), s0);
-        s1 = mfma4(a, R::hi(l.kp[4 * u + k]), s1);
+        s0 = mfma4(a, elem(l.kq[u][0], k), s0);
+        s1 = mfma4(a, elem(l.kq[u][1], k), s1);
       }
     }
     // every wave read sST (stage A) before the barrier above and only its own
