@@ -208,10 +208,10 @@ template <> struct RawOf<uint16_t> {
   }
 };
 
-// V elements of the scan's stage B: rows 16M+4lg+e (e = 0..3) of value
-// column n0+li, read through a buffer resource of the chunk's len rows, so
-// rows past the chunk read 0 (the hardware range check) with no clamp or
-// select.  fp16 rows are packed two to a register.
+// V elements of the scan's stage B: row 16M+li, value columns n0+4lg..+3 (one
+// 8-byte (fp16) or 16-byte (fp32) load per lane), read through a buffer
+// resource of the chunk's len rows, so rows past the chunk read 0 (the
+// hardware range check) with no clamp or select.
 // The whole byte offset goes in the VGPR offset and the scalar offset stays 0:
 // on gfx9-family raw buffers the range check compares only voffset +
 // inst_offset with num_records, so a row offset passed as soffset would read
@@ -220,21 +220,18 @@ template <typename TIn> struct VTile;
 template <> struct VTile<float> {
   float x[4];
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int voff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      x[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + e * kD * 4, 0, 0));
+    for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(v[e]);
   }
   __device__ __forceinline__ float get(int e) const { return x[e]; }
 };
 template <> struct VTile<uint16_t> {
   uint32_t x[2];
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int voff) {
-#pragma unroll
-    for (int e = 0; e < 4; e += 2) {
-      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, voff + e * kD * 2, 0, 0);
-      const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(r, voff + (e + 1) * kD * 2, 0, 0);
-      x[e / 2] = lo | (hi << 16);
-    }
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
+    x[0] = v[0];
+    x[1] = v[1];
   }
   __device__ __forceinline__ float get(int e) const {
     return spk::h2f((uint16_t)((e & 1) ? x[e / 2] >> 16 : x[e / 2] & 0xffffu));
@@ -795,10 +792,10 @@ struct ScanEarly {
 };
 template <typename TIn>
 struct ScanLate {
-  VTile<TIn> v;  // V: tokens 16M+4lg..+3, column n0+li
-  float4 c1;     // beta of tokens 16M+4lg..+3
-  float4 c2;     // beta e^gcum ik of the same tokens
-  float4 qs;     // Qs of the same tokens
+  VTile<TIn> v;  // V: token 16M+li, columns n0+4lg..+3
+  float c1;      // beta of token 16M+li
+  float c2;      // beta e^gcum ik of the same token
+  float qs;      // Qs of the same token
   float4 a[4];   // A T rows: token 16M+li, tokens 16u+4lg..+3
   float gle;     // e^{gL}
   float4 kq[4][2];  // K'[16u+4lg..+3][32M+2li+t] at [u][t]
@@ -906,10 +903,10 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     const float* ws = record(c);
     const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<TIn*>(vin + (size_t)c * kC * kD), 0, min(kC, L - c * kC) * kD * (int)sizeof(TIn), kBufDword3);
-    l.v.load(vr, ((16 * M + 4 * lg) * kD + n0 + li) * (int)sizeof(TIn));
-    l.c1 = *reinterpret_cast<const float4*>(ws + kWsC1 + 16 * M + 4 * lg);
-    l.c2 = *reinterpret_cast<const float4*>(ws + kWsC2 + 16 * M + 4 * lg);
-    l.qs = *reinterpret_cast<const float4*>(ws + kWsQs + 16 * M + 4 * lg);
+    l.v.load(vr, ((16 * M + li) * kD + n0 + 4 * lg) * (int)sizeof(TIn));
+    l.c1 = ws[kWsC1 + 16 * M + li];
+    l.c2 = ws[kWsC2 + 16 * M + li];
+    l.qs = ws[kWsQs + 16 * M + li];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       l.a[u] = *reinterpret_cast<const float4*>(ws + kWsA + ((M * 4 + u) * 64 + lane) * 4);
@@ -926,8 +923,10 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     const int tok0 = t_begin + c * kC;
     const int len = min(kC, L - c * kC);
 
-    // ---- stage A: K_M S and Q_M S share the B operand (S); the per-row
-    // factors are applied to the products
+    // ---- stage A: (K_M S)^T = S^T K_M^T and (Q_M S)^T share the A operand
+    // (S^T, from LDS); lane (li, lg) ends up holding row 16M+li, columns
+    // n0+4lg..+3 of K S and Q S.  The per-row factors are applied to the
+    // products.
     f4v aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
     if constexpr (!decltype(zero_s)::value) {
       // the S piece of step u+1 is read while step u's MFMAs run
@@ -940,8 +939,8 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
         const float4 x = R::cvt4(e.q[u]);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          aw = mfma4(elem(xk, k), elem(sb, k), aw);
-          aq = mfma4(elem(x, k), elem(sb, k), aq);
+          aw = mfma4(elem(sb, k), elem(xk, k), aw);
+          aq = mfma4(elem(sb, k), elem(x, k), aq);
         }
       }
       // The loads issued just before this stage (same scheduling region, about
@@ -965,45 +964,45 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     }
 
     // ---- stage B: R = beta V - (beta e^g ik) (K S) for the rows of token
-    // block M (v_new = T R itself is never formed: T sits in A T and K')
-    {
-      float r[4];
+    // block M (v_new = T R itself is never formed: T sits in A T and K'),
+    // stored transposed
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = elem(l.c1, e) * l.v.get(e) - elem(l.c2, e) * aw[e];
-      *reinterpret_cast<float4*>(&sVT[li * kLdVT + 16 * M + 4 * lg]) = make_float4(r[0], r[1], r[2], r[3]);
-    }
+    for (int e = 0; e < 4; ++e) sVT[(4 * lg + e) * kLdVT + 16 * M + li] = l.c1 * l.v.get(e) - l.c2 * aw[e];
     __syncthreads();
 
-    // ---- stage C: o = qs (Q S) + (A T) R over the blocks J <= M of A T's
-    // row block (two accumulator chains: J = 0, 1 and J = 2, 3)
+    // ---- stage C: o^T = (Q S)^T diag(qs) + R^T (A T)^T over the blocks
+    // J <= M of A T's row block (two accumulator chains: J = 0, 1 and
+    // J = 2, 3); lane (li, lg) ends up holding row 16M+li, columns
+    // n0+4lg..+3 of o
     {
       float4 vb[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) vb[u] = *reinterpret_cast<const float4*>(&sVT[li * kLdVT + 16 * u + 4 * lg]);
-      f4v ac = {aq[0] * l.qs.x, aq[1] * l.qs.y, aq[2] * l.qs.z, aq[3] * l.qs.w};
+      f4v ac = {aq[0] * l.qs, aq[1] * l.qs, aq[2] * l.qs, aq[3] * l.qs};
       f4v ad = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         if (u <= M) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) ac = mfma4(elem(l.a[u], k), elem(vb[u], k), ac);
+          for (int k = 0; k < 4; ++k) ac = mfma4(elem(vb[u], k), elem(l.a[u], k), ac);
         }
         if (u + 2 <= M) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) ad = mfma4(elem(l.a[u + 2], k), elem(vb[u + 2], k), ad);
+          for (int k = 0; k < 4; ++k) ad = mfma4(elem(vb[u + 2], k), elem(l.a[u + 2], k), ad);
         }
       }
       aq = ac + ad;
     }
     // rows tok0 .. tok0+len-1 of this head through a buffer resource of len
     // rows: the hardware drops the padding rows' stores (offset past
-    // num_records), with no branch around the stores
-    const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
-        p.core + ((size_t)h * p.core_hs + tok0) * kD, 0, len * kD * (int)sizeof(float), kBufDword3);
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(aq[r]), out,
-                                            ((16 * M + 4 * lg + r) * kD + n0 + li) * (int)sizeof(float), 0, 0);
+    // num_records), with no branch around the store
+    {
+      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+          p.core + ((size_t)h * p.core_hs + tok0) * kD, 0, len * kD * (int)sizeof(float), kBufDword3);
+      typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+      const u32x4v ov = {__float_as_uint(aq[0]), __float_as_uint(aq[1]), __float_as_uint(aq[2]), __float_as_uint(aq[3])};
+      __builtin_amdgcn_raw_buffer_store_b128(ov, out, ((16 * M + li) * kD + n0 + 4 * lg) * (int)sizeof(float), 0, 0);
+    }
 
     // ---- stage D: S^T <- e^{gL} S^T + R^T K', computed transposed so that
     // K' is the B operand in the record's fragment order: lane (li, lg) holds
