@@ -327,6 +327,9 @@ __host__ __device__ constexpr int gram_nj() {  // K row blocks read: 0 .. nJ-1
   return m + 1;
 }
 
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
 template <typename TIn, unsigned KMASK, int QB>
 __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, const float4 (&qa)[8],
                                            int li, int lg, f4v (&acc)[5]) {
@@ -337,6 +340,35 @@ __device__ __forceinline__ void gram_tiles(const typename RowStage<TIn>::T* sK, 
   static_assert(NT <= 5, "at most five Gram tiles per wavefront");
 #pragma unroll
   for (int t = 0; t < 5; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
+  if constexpr (std::is_same<TIn, uint16_t>::value) {
+    // fp16 inputs: the products of two halves are exact in fp32, so the
+    // 16x16x32 f16 MFMA (fp32 accumulation) forms the same dot products as
+    // the fp32 one up to the summation order, at 1/32 of its issue cycles.
+    // Lane (li, lg) feeds keys 32v+4lg..+3 and 32v+16+4lg..+3 (its Q
+    // registers qa[2v], qa[2v+1]) to both operands.
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      h8v kb[nJ];
+#pragma unroll
+      for (int J = 0; J < nJ; ++J) {
+        const uint2 a = *reinterpret_cast<const uint2*>(sK + (16 * J + li) * RS::kLd + 32 * v + 4 * lg);
+        const uint2 b = *reinterpret_cast<const uint2*>(sK + (16 * J + li) * RS::kLd + 32 * v + 16 + 4 * lg);
+        kb[J] = __builtin_bit_cast(h8v, (u32x4v{a.x, a.y, b.x, b.y}));
+      }
+      const h8v qf = __builtin_bit_cast(h8v, (u32x4v{__float_as_uint(qa[2 * v].x), __float_as_uint(qa[2 * v].y),
+                                                      __float_as_uint(qa[2 * v + 1].x),
+                                                      __float_as_uint(qa[2 * v + 1].y)}));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const GramTile g = gram_tile<KMASK, QB>(t);
+        if (g.q)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[g.J], qf, acc[t], 0, 0, 0);
+        else
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[g.I], kb[g.J], acc[t], 0, 0, 0);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     float4 kb[nJ];
