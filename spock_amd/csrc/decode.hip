@@ -62,55 +62,6 @@ __device__ __forceinline__ float tree32(const float (*part)[128], int col) {
   return v[0];
 }
 
-// Four 32-lane trees (one per column) over the row-group partials of each
-// half wave, adjacent pairs first -- the order of tree32 -- ending in lanes 0
-// and 32 (other lanes hold partial sums no caller reads).  Every lane of the
-// wave must be active.
-__device__ __forceinline__ void tree32_half_to_lane0(float (&v)[4]) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) v[c] = spk::add_row_shl<1>(v[c]);
-#pragma unroll
-  for (int c = 0; c < 4; ++c) v[c] = spk::add_row_shl<2>(v[c]);
-#pragma unroll
-  for (int c = 0; c < 4; ++c) v[c] = spk::add_row_shl<4>(v[c]);
-#pragma unroll
-  for (int c = 0; c < 4; ++c) v[c] = spk::add_row_shl<8>(v[c]);
-#pragma unroll
-  for (int c = 0; c < 4; ++c) v[c] = v[c] + spk::lanes_down16(v[c]);
-}
-
-// Lane 0's value in lanes 0..31, lane 32's in lanes 32..63.
-__device__ __forceinline__ float half_broadcast(float v, int lane) {
-  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  return lane < 32 ? lo : hi;
-}
-
-// Output of one head from wave 0: lane holds o[lane] and o[lane + 64].  With
-// NORM_GATE the gated RMSNorm (128-wide tree of o^2 in the shader's order,
-// r = 1/sqrt(sum/128 + eps), fp16(fp16(w o r) * SiLU(z))), else fp16(o).
-template <bool NORM_GATE>
-__device__ __forceinline__ void norm_gate_out(float oa, float ob, uint16_t* out, int lane, const float (&nw)[2],
-                                              const float* s_zs, float eps) {
-  if (NORM_GATE) {
-    float v = oa * oa + ob * ob;
-    v = spk::tree64_to_lane0(v);
-    const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));  // lane 0 broadcast, no LDS
-    const float r = spk::rsqrt_det(tot / 128.0f + eps);
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int j = lane + 64 * half;
-      const float o = half ? ob : oa;
-      const float normed = o * r;
-      const float weighted = spk::h2f(spk::f2h(nw[half] * normed));
-      out[j] = spk::f2h(weighted * s_zs[j]);
-    }
-  } else {
-    out[lane] = spk::f2h(oa);
-    out[lane + 64] = spk::f2h(ob);
-  }
-}
-
 // CONV: run the conv/L2 phase.  REC: run the recurrence.  GB_TAIL: g/beta from
 // the state tail (deltanet_recurrent.comp) instead of a/b/A_log/dt_bias.
 // NORM_GATE: RMSNorm-gate the output (else fp16 of the raw output).
@@ -130,19 +81,11 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
 
   __shared__ float s_q[128], s_k[128], s_v[128], s_delta[128];
   __shared__ float s_part[32][128];
-  __shared__ float s_gb[3];  // g, beta, e^g
+  __shared__ float s_gb[2];
   __shared__ float s_zs[128];  // SiLU(z) of the norm-gate, formed off the chain
 
-  // Lane ownership: columns 4*c4 .. 4*c4+3, row groups G*rq .. G*rq+G-1
-  // (rows M*rq .. M*rq+M-1).  With 4 or 8 wavefronts c4 runs along the lanes
-  // (a half wave reads 512 contiguous bytes of a state row) and the column
-  // sums are combined through LDS.  With 16 (G = 1: one row group per lane)
-  // the roles swap: the 32 lanes of a half wave hold the 32 row groups of
-  // four columns, so every column sum is a 32-lane tree inside the half
-  // wave, with no LDS round trip and two barriers fewer.
-  constexpr bool kLaneRows = WAVES == 16;
-  const int c4 = kLaneRows ? tid >> 5 : tid & 31;
-  const int rq = kLaneRows ? tid & 31 : tid >> 5;
+  const int c4 = tid & 31;  // owns columns 4*c4 .. 4*c4+3
+  const int rq = tid >> 5;  // owns row groups G*rq .. G*rq+G-1, i.e. rows M*rq .. M*rq+M-1
   // Load order: the conv operands, then the small g/beta and norm-gate
   // operands, then the state, all without a branch (a branch around a load
   // makes the compiler wait for the loads before it).  A wave's loads return
@@ -197,16 +140,13 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
   }
 
   if (REC && !GB_TAIL && wave == 3) {
-    // g/beta (and e^g) while waves 0-2 run the conv
-    // (deltanet_recurrent_gbeta_norm_gate.comp:102-116)
+    // g/beta while waves 0-2 run the conv (deltanet_recurrent_gbeta_norm_gate.comp:102-116)
     if (lane == 0) {
       const float av = spk::h2f(a16);
       const float bv = spk::h2f(b16);
       const float sp = spk::logf_det(1.0f + spk::expf_det(av + dt_bias));
-      const float gg = -spk::expf_det(a_log) * sp;
-      s_gb[0] = gg;
+      s_gb[0] = -spk::expf_det(a_log) * sp;
       s_gb[1] = 1.0f / (1.0f + spk::expf_det(-bv));
-      s_gb[2] = spk::expf_det(gg);
     }
   }
   if (REC && NORM_GATE && wave == (WAVES > 4 ? 4 : 3)) {
@@ -274,65 +214,17 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
   if (!REC) return;
 
   __syncthreads();
-  float beta, eg;
+  float g, beta;
   if (GB_TAIL) {
+    g = g_tail;
     beta = beta_tail;
-    eg = spk::expf_det(g_tail);
   } else {
+    g = s_gb[0];
     beta = s_gb[1];
-    eg = s_gb[2];
-  }
-
-  if constexpr (kLaneRows) {
-    // decay; kv = S^T k per column: the lane's 4-row fma chain from 0, then
-    // the 32 row groups of the half wave combined adjacent pairs first (DPP
-    // shifts by 1, 2, 4, 8 within each row of 16 lanes, then lane l + 16):
-    // the sum lands in lanes 0 and 32 and is broadcast by v_readlane
-    const float4 kr = *reinterpret_cast<const float4*>(&s_k[4 * rq]);
-    const float4 qr = *reinterpret_cast<const float4*>(&s_q[4 * rq]);
-    const float kk[4] = {kr.x, kr.y, kr.z, kr.w};
-    const float qq[4] = {qr.x, qr.y, qr.z, qr.w};
-    float kp[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      S[m].x = S[m].x * eg;
-      S[m].y = S[m].y * eg;
-      S[m].z = S[m].z * eg;
-      S[m].w = S[m].w * eg;
-      kp[0] = __builtin_fmaf(S[m].x, kk[m], kp[0]);
-      kp[1] = __builtin_fmaf(S[m].y, kk[m], kp[1]);
-      kp[2] = __builtin_fmaf(S[m].z, kk[m], kp[2]);
-      kp[3] = __builtin_fmaf(S[m].w, kk[m], kp[3]);
-    }
-    tree32_half_to_lane0(kp);
-    const float4 vv = *reinterpret_cast<const float4*>(&s_v[4 * c4]);
-    const float vc[4] = {vv.x, vv.y, vv.z, vv.w};
-    float d[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) d[c] = (vc[c] - half_broadcast(kp[c], lane)) * beta;
-    // rank-1 update, state write-back, o = S^T q the same way
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      S[m].x = __builtin_fmaf(kk[m], d[0], S[m].x);
-      S[m].y = __builtin_fmaf(kk[m], d[1], S[m].y);
-      S[m].z = __builtin_fmaf(kk[m], d[2], S[m].z);
-      S[m].w = __builtin_fmaf(kk[m], d[3], S[m].w);
-      *reinterpret_cast<float4*>(st_head + (rq * M + m) * 128 + c4 * 4) = S[m];
-      o[0] = __builtin_fmaf(S[m].x, qq[m], o[0]);
-      o[1] = __builtin_fmaf(S[m].y, qq[m], o[1]);
-      o[2] = __builtin_fmaf(S[m].z, qq[m], o[2]);
-      o[3] = __builtin_fmaf(S[m].w, qq[m], o[3]);
-    }
-    tree32_half_to_lane0(o);
-    if ((lane & 31) == 0) *reinterpret_cast<float4*>(&s_delta[4 * c4]) = make_float4(o[0], o[1], o[2], o[3]);
-    __syncthreads();
-    if (wave == 0) norm_gate_out<NORM_GATE>(s_delta[lane], s_delta[lane + 64], qkv + 2 * nh * 128 + h * 128, lane,
-                                            nw, s_zs, p.eps);
-    return;
   }
 
   // decay + kv partials, one per 4-row group
+  const float eg = spk::expf_det(g);
 #pragma unroll
   for (int gq = 0; gq < G; ++gq) {
     float kp0 = 0.f, kp1 = 0.f, kp2 = 0.f, kp3 = 0.f;
@@ -380,9 +272,28 @@ __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  if (wave == 0)
-    norm_gate_out<NORM_GATE>(tree32(s_part, lane), tree32(s_part, lane + 64), qkv + 2 * nh * 128 + h * 128, lane,
-                             nw, s_zs, p.eps);
+  if (wave == 0) {
+    const float oa = tree32(s_part, lane);
+    const float ob = tree32(s_part, lane + 64);
+    uint16_t* out = qkv + 2 * nh * 128 + h * 128;
+    if (NORM_GATE) {
+      float v = oa * oa + ob * ob;
+      v = spk::tree64_to_lane0(v);
+      const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));  // lane 0 broadcast, no LDS
+      const float r = spk::rsqrt_det(tot / 128.0f + p.eps);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int j = lane + 64 * half;
+        const float o = half ? ob : oa;
+        const float normed = o * r;
+        const float weighted = spk::h2f(spk::f2h(nw[half] * normed));
+        out[j] = spk::f2h(weighted * s_zs[j]);
+      }
+    } else {
+      out[lane] = spk::f2h(oa);
+      out[lane + 64] = spk::f2h(ob);
+    }
+  }
 }
 
 int validate(const SpkDecodeArgs* a, bool conv, bool rec, bool gb_inline, bool norm_gate) {
