@@ -81,7 +81,7 @@ constexpr int kD = 128;
 //   Qs  [64] Q scale (q_scale iq e^gcum)
 //   C1  [64] beta           C2 [64] beta e^gcum ik
 //   Misc[0] e^{gL}
-//   Kr  [M 4][u 8][lane][4]       K[16M+li][16u+4lg+e], raw input type
+//   Kr  [M 4][j 4][lane][8]       K[16M+li][32j+8lg+e], raw input type
 // A T's blocks above the diagonal (zero) are neither stored nor multiplied.
 // Kr is the scan's stage-A operand: raw K rows read from the input instead
 // (16 rows of 32 bytes per load instruction) made the scan 25% slower.
@@ -194,6 +194,14 @@ template <typename TIn> struct RawOf;
 template <> struct RawOf<float> {
   static __device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
   static __device__ __forceinline__ float4 cvt4(const float4& r) { return r; }
+  // 8 consecutive elements (two 16-byte loads), element i converted at use
+  struct R8 {
+    float4 a, b;
+  };
+  static __device__ __forceinline__ R8 ld8(const float* p) {
+    return R8{*reinterpret_cast<const float4*>(p), *reinterpret_cast<const float4*>(p + 4)};
+  }
+  static __device__ __forceinline__ float get8(const R8& r, int i) { return elem(i < 4 ? r.a : r.b, i & 3); }
 };
 template <> struct RawOf<uint16_t> {
   // 4 halves kept as two 32-bit words in .x/.y of a float4
@@ -205,6 +213,13 @@ template <> struct RawOf<uint16_t> {
     const uint32_t x = __float_as_uint(r.x), y = __float_as_uint(r.y);
     return make_float4(spk::h2f((uint16_t)(x & 0xffffu)), spk::h2f((uint16_t)(x >> 16)),
                        spk::h2f((uint16_t)(y & 0xffffu)), spk::h2f((uint16_t)(y >> 16)));
+  }
+  // 8 consecutive halves (one 16-byte load), half i converted at use
+  typedef uint4 R8;
+  static __device__ __forceinline__ R8 ld8(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ float get8(const R8& r, int i) {
+    const uint32_t w = (i >> 1) == 0 ? r.x : (i >> 1) == 1 ? r.y : (i >> 1) == 2 ? r.z : r.w;
+    return spk::h2f((uint16_t)((i & 1) ? w >> 16 : w & 0xffffu));
   }
 };
 
@@ -256,10 +271,12 @@ template <> struct RowStage<uint16_t> {
                        spk::h2f((uint16_t)(u.y & 0xffffu)), spk::h2f((uint16_t)(u.y >> 16)));
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return spk::h2f(s[r * kLd + c]); }
-  // row r, columns c..c+3, stored raw as 4 consecutive elements at dst
-  static __device__ __forceinline__ void row4_to(const T* s, int r, int c, T* dst) {
+  // row r, columns c..c+7, stored raw as 8 consecutive elements at dst
+  static __device__ __forceinline__ void row8_to(const T* s, int r, int c, T* dst) {
     const uint2 u = *reinterpret_cast<const uint2*>(s + r * kLd + c);
-    ws_store(dst, u.x, u.y);
+    const uint2 w = *reinterpret_cast<const uint2*>(s + r * kLd + c + 4);
+    ws_store(reinterpret_cast<float*>(dst), __uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(w.x),
+             __uint_as_float(w.y));
   }
 };
 template <> struct RowStage<float> {
@@ -272,9 +289,11 @@ template <> struct RowStage<float> {
     return *reinterpret_cast<const float4*>(s + r * kLd + c);
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return s[r * kLd + c]; }
-  static __device__ __forceinline__ void row4_to(const T* s, int r, int c, T* dst) {
+  static __device__ __forceinline__ void row8_to(const T* s, int r, int c, T* dst) {
     const float4 v = *reinterpret_cast<const float4*>(s + r * kLd + c);
+    const float4 w = *reinterpret_cast<const float4*>(s + r * kLd + c + 4);
     ws_store(dst, v.x, v.y, v.z, v.w);
+    ws_store(dst + 4, w.x, w.y, w.z, w.w);
   }
 };
 
@@ -657,7 +676,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
   if (own_block) {
     typename RS::T* kf = reinterpret_cast<typename RS::T*>(ws + kWsKr);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) RS::row4_to(sK, 16 * wave + li, 16 * u + 4 * lg, kf + ((wave * 8 + u) * 64 + lane) * 4);
+    for (int j = 0; j < 4; ++j) RS::row8_to(sK, 16 * wave + li, 32 * j + 8 * lg, kf + ((wave * 4 + j) * 64 + lane) * 8);
   }
 
   // ---- inverse L2 norms (eps inside the sqrt, deltanet_chunk.cpp:27-39):
@@ -818,9 +837,10 @@ constexpr int kLdVT = 68;   // LDS row stride of the transposed R tile (floats)
 
 // Operands of one chunk for stage A (prefetched a chunk ahead) and for stages
 // B-D (loaded at the start of the chunk's own step, in flight during stage A).
+template <typename TIn>
 struct ScanEarly {
-  float4 k[8];  // raw K (record Kr): token 16M+li, key dims 16u+4lg..+3
-  float4 q[8];  // raw Q rows, same map
+  typename RawOf<TIn>::R8 k[4];  // raw K (record Kr): token 16M+li, key dims 32j+8lg..+7
+  typename RawOf<TIn>::R8 q[4];  // raw Q rows, same map
 };
 template <typename TIn>
 struct ScanLate {
@@ -843,7 +863,7 @@ struct ScanLate {
 //   D  S rows 32M..32M+31 <- e^{gL} S + K'^T R
 // 100-112 MFMA per wavefront per chunk (stage C: 4 (M+1)).
 // MINB workgroups per CU.  fp16 inputs, large launches: three (168 VGPRs;
-// the instance spills 3): more resident wavefronts measured faster than two
+// the instance spills 16 bytes per lane): more resident wavefronts measured faster than two
 // workgroups holding both operand sets double-buffered.  fp32 inputs hold
 // twice the Q and K operand registers: at 168 VGPRs they spilled 236 bytes
 // per lane inside the chunk loop (6.5-9 us per chunk step against 3.1 for
@@ -916,15 +936,15 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   // 16M+li from the input (padding rows read the chunk's row 0, as the intra
   // kernel's Q operand does; their output rows are dropped)
   const size_t in_off = ((size_t)h * p.N + t_begin) * kD;
-  const TIn* qin = static_cast<const TIn*>(p.q) + in_off + 4 * lg;
-  auto load_early = [&](ScanEarly& e, int c) {
-    const TIn* kf = reinterpret_cast<const TIn*>(record(c) + kWsKr) + (M * 8 * 64 + lane) * 4;
+  const TIn* qin = static_cast<const TIn*>(p.q) + in_off + 8 * lg;
+  auto load_early = [&](ScanEarly<TIn>& e, int c) {
+    const TIn* kf = reinterpret_cast<const TIn*>(record(c) + kWsKr) + (M * 4 * 64 + lane) * 8;
     const int row = 16 * M + li;
     const TIn* qrow = qin + (size_t)(c * kC + (row < L - c * kC ? row : 0)) * kD;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      e.k[u] = R::ld4(kf, u * 64 * 4);
-      e.q[u] = R::ld4(qrow, 16 * u);
+    for (int j = 0; j < 4; ++j) {
+      e.k[j] = R::ld8(kf + j * 64 * 8);
+      e.q[j] = R::ld8(qrow + 32 * j);
     }
   };
   // Stage B-D operands, in the order the stages use them (a wave's loads
@@ -951,7 +971,7 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   };
 
   // zero_s: S is zero (first chunk without an initial state)
-  auto step = [&](const ScanEarly& e, const ScanLate<TIn>& l, int c, auto zero_s) {
+  auto step = [&](const ScanEarly<TIn>& e, const ScanLate<TIn>& l, int c, auto zero_s) {
     const int tok0 = t_begin + c * kC;
     const int len = min(kC, L - c * kC);
 
@@ -962,26 +982,27 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
     f4v aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
     if constexpr (!decltype(zero_s)::value) {
       // the S piece of step u+1 is read while step u's MFMAs run
-      float4 sb_next = *reinterpret_cast<const float4*>(&sST[li * kLdST + 4 * lg]);
+      // step u contracts key dims 32(u/2) + 8lg + 4(u%2) + k over (lg, k)
+      float4 sb_next = *reinterpret_cast<const float4*>(&sST[li * kLdST + 8 * lg]);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const float4 sb = sb_next;
-        if (u + 1 < 8) sb_next = *reinterpret_cast<const float4*>(&sST[li * kLdST + 16 * (u + 1) + 4 * lg]);
-        const float4 xk = R::cvt4(e.k[u]);
-        const float4 x = R::cvt4(e.q[u]);
+        if (u + 1 < 8)
+          sb_next = *reinterpret_cast<const float4*>(&sST[li * kLdST + 32 * ((u + 1) >> 1) + 8 * lg + 4 * ((u + 1) & 1)]);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          aw = mfma4(elem(sb, k), elem(xk, k), aw);
-          aq = mfma4(elem(sb, k), elem(x, k), aq);
+          aw = mfma4(elem(sb, k), R::get8(e.k[u >> 1], 4 * (u & 1) + k), aw);
+          aq = mfma4(elem(sb, k), R::get8(e.q[u >> 1], 4 * (u & 1) + k), aq);
         }
       }
-      // The loads issued just before this stage (same scheduling region, about
-      // 36 of them) are spread over the MFMA stream rather than issued as one
+      // The loads issued just before this stage (same scheduling region, 25
+      // of them) are spread over the MFMA stream rather than issued as one
       // burst, which would queue in the CU's vector-memory pipe behind the
       // other wavefronts' bursts: 2 and 3 loads around each 4 MFMAs.  Measured
-      // on config 2 (ms per call, same box, bit-identical): 2+3 0.875-0.878,
-      // 3+2 0.875-0.878, 2+4 0.878-0.881, 1+4 0.879-0.883, 1+3 0.881-0.885,
-      // 2+2 0.895-0.898, 4+2 0.899, 4+4 0.967.
+      // on config 2 (ms per call, same box, bit-identical): 2+3 0.755, 1+2
+      // 0.760, 1+3 0.763 (with 4-element K and Q fragments, 33 loads: 2+3
+      // 0.875-0.878, 3+2 0.875-0.878, 2+4 0.878-0.881, 1+4 0.879-0.883, 1+3
+      // 0.881-0.885, 2+2 0.895-0.898, 4+2 0.899, 4+4 0.967).
       // (masks: 0x100 LDS read, 0x020 VMEM read, 0x008 MFMA) -- the S piece
       // of step u+1 goes out before step u's 8 MFMAs
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
@@ -1072,7 +1093,7 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   // first chunk to drop its stage A at compile time (a run-time flag, or the
   // peeled loop for every launch, made the fp16 instance spill more).
   using NZ = std::integral_constant<bool, false>;
-  ScanEarly ea, eb;
+  ScanEarly<TIn> ea, eb;
   ScanLate<TIn> lt;
   if constexpr (ZERO_INIT) {
     __syncthreads();
