@@ -70,29 +70,28 @@ constexpr int kD = 128;
 //   v_new = U - W S = T R,   o = Qs*(Q S) + (A T) R,
 //   S' = e^{gL} S + K^T diag(Ks) v_new = e^{gL} S + K'^T R,  K' = T^T diag(Ks) K,
 // so the scan needs A T and K' (and raw K, Q, V from the input) instead of
-// U, W and A: 42 KB of record instead of 74 KB, and the intra kernel never
+// U, W and A: 49 KB of record instead of 74 KB, and the intra kernel never
 // reads V.  The matrices are in the scan's MFMA fragment order: fragment f of
 // wavefront M is 64 lanes x 4 consecutive elements, so every load of the scan
 // reads one contiguous 1 KB block.  Loads whose 64 lanes touch 16 separate
-// rows (the row-major alternative) cost the vector-memory pipe several times
-// more per byte.  Lane l = 16*lg + li.
+// rows (the row-major alternative) cost the vector-memory pipe more per byte;
+// the raw K and Q rows of stage A are read that way, 16 rows x 64 bytes per
+// load (8 consecutive elements per lane), which measured as fast as a
+// fragment-order copy of K in the record (at 16 rows x 32 bytes per load the
+// copy had been 25% faster).  Lane l = 16*lg + li.
 //   K'  [M 4][u 4][t 2][lane][4]  K'[16u+4lg+e][32M+2li+t]          fp32
 //   AT  [M 4][J 4][lane][4]       (A T)[16M+li][16J+4lg+e], J <= M   fp32
 //   Qs  [64] Q scale (q_scale iq e^gcum)
 //   C1  [64] beta           C2 [64] beta e^gcum ik
 //   Misc[0] e^{gL}
-//   Kr  [M 4][j 4][lane][8]       K[16M+li][32j+8lg+e], raw input type
 // A T's blocks above the diagonal (zero) are neither stored nor multiplied.
-// Kr is the scan's stage-A operand: raw K rows read from the input instead
-// (16 rows of 32 bytes per load instruction) made the scan 25% slower.
 constexpr int kWsKp = 0;
 constexpr int kWsA = 8192;
 constexpr int kWsQs = 12288;
 constexpr int kWsC1 = 12352;
 constexpr int kWsC2 = 12416;
 constexpr int kWsMisc = 12480;
-constexpr int kWsKr = 12544;      // 8192 elements: 16 KB (fp16) or 32 KB (fp32)
-constexpr int kWsStride = 20736;  // 82944 bytes, a multiple of 256
+constexpr int kWsStride = 12544;  // 50176 bytes, a multiple of 256
 // Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
 // which untyped loads/stores need for the num_records range check to apply.
 constexpr int kBufDword3 = 0x00020000;
@@ -271,13 +270,6 @@ template <> struct RowStage<uint16_t> {
                        spk::h2f((uint16_t)(u.y & 0xffffu)), spk::h2f((uint16_t)(u.y >> 16)));
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return spk::h2f(s[r * kLd + c]); }
-  // row r, columns c..c+7, stored raw as 8 consecutive elements at dst
-  static __device__ __forceinline__ void row8_to(const T* s, int r, int c, T* dst) {
-    const uint2 u = *reinterpret_cast<const uint2*>(s + r * kLd + c);
-    const uint2 w = *reinterpret_cast<const uint2*>(s + r * kLd + c + 4);
-    ws_store(reinterpret_cast<float*>(dst), __uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(w.x),
-             __uint_as_float(w.y));
-  }
 };
 template <> struct RowStage<float> {
   static constexpr int kLd = 132;  // floats (528 B)
@@ -289,12 +281,6 @@ template <> struct RowStage<float> {
     return *reinterpret_cast<const float4*>(s + r * kLd + c);
   }
   static __device__ __forceinline__ float get1(const T* s, int r, int c) { return s[r * kLd + c]; }
-  static __device__ __forceinline__ void row8_to(const T* s, int r, int c, T* dst) {
-    const float4 v = *reinterpret_cast<const float4*>(s + r * kLd + c);
-    const float4 w = *reinterpret_cast<const float4*>(s + r * kLd + c + 4);
-    ws_store(dst, v.x, v.y, v.z, v.w);
-    ws_store(dst + 4, w.x, w.y, w.z, w.w);
-  }
 };
 
 // L is block lower triangular: its 10 blocks (I >= J) of 16x16 are stored
@@ -568,11 +554,11 @@ __device__ __forceinline__ void gram_dispatch(int part, int wave, const F& f) {
 // PARTS workgroups per (chunk, head) (blockIdx.z = part), for launches with
 // too few (chunk, head) pairs to fill the chip: every part loads K and the
 // value columns it needs, forms L's Gram tiles and T (the serial part), then
-// computes and stores only its share of the record: U / W column tiles 4*part..4*part+3 (PARTS 2),
-// 2*part and 2*part+1 (PARTS 4: its four wavefronts split the two tiles' row
-// blocks as {0,3} / {1,2}, 40 MFMA each instead of 160) or tile `part`
-// (PARTS 8: waves 0-1 form U, 2-3 form W, row blocks {0,3} / {1,2}, 20 MFMA
-// each), and the A blocks of the wavefronts w with w % PARTS == part.
+// computes and stores only its share of the record: K' column tiles
+// 4*part..4*part+3 (PARTS 2, one per wavefront), 2*part and 2*part+1
+// (PARTS 4: wavefronts 0-1 form row blocks {0,3} of the two tiles, 2-3
+// blocks {1,2}) or tile `part` (PARTS 8: wavefront w forms row block w),
+// and the A T blocks of the wavefronts w with w % PARTS == part.
 // Each value is computed by the same operation sequence whatever PARTS is, so
 // the record is bit-identical.
 template <typename TIn, int PARTS>
@@ -670,14 +656,6 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
     RS::put4(sK, r, c4, kx);
   }
   __syncthreads();
-
-  // ---- raw K rows of token block `wave` in the scan's stage-A fragment
-  // order (the wavefront owning the block writes them; padding rows are 0)
-  if (own_block) {
-    typename RS::T* kf = reinterpret_cast<typename RS::T*>(ws + kWsKr);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) RS::row8_to(sK, 16 * wave + li, 32 * j + 8 * lg, kf + ((wave * 4 + j) * 64 + lane) * 8);
-  }
 
   // ---- inverse L2 norms (eps inside the sqrt, deltanet_chunk.cpp:27-39):
   // K rows from LDS, 4 threads per row; Q rows from this lane's registers
@@ -839,7 +817,7 @@ constexpr int kLdVT = 68;   // LDS row stride of the transposed R tile (floats)
 // B-D (loaded at the start of the chunk's own step, in flight during stage A).
 template <typename TIn>
 struct ScanEarly {
-  typename RawOf<TIn>::R8 k[4];  // raw K (record Kr): token 16M+li, key dims 32j+8lg..+7
+  typename RawOf<TIn>::R8 k[4];  // raw K rows: token 16M+li, key dims 32j+8lg..+7
   typename RawOf<TIn>::R8 q[4];  // raw Q rows, same map
 };
 template <typename TIn>
@@ -930,21 +908,21 @@ __global__ __launch_bounds__(256, MINB) void chunk_state_kernel(ChunkParams p) {
   // Every load is unconditional (the intra kernel's padding Q rows are row 0
   // of the chunk, zeroed here through qs; the last chunk is prefetched again
   // rather than guarded), so the compiler's vmcnt bookkeeping stays exact.
-  // Each load instruction reads one contiguous fragment.
+  // Each record load instruction reads one contiguous fragment.
   auto record = [&](int c) { return p.ws + ((size_t)(co + c) * p.H + h) * kWsStride; };
-  // raw K rows of token block M from the record (fragment order), raw Q rows
-  // 16M+li from the input (padding rows read the chunk's row 0, as the intra
-  // kernel's Q operand does; their output rows are dropped)
+  // raw K and Q rows 16M+li from the input (padding rows read the chunk's
+  // row 0, as the intra kernel's Q operand does; their K S rows meet beta = 0
+  // in stage B and their output rows are dropped)
   const size_t in_off = ((size_t)h * p.N + t_begin) * kD;
   const TIn* qin = static_cast<const TIn*>(p.q) + in_off + 8 * lg;
+  const TIn* kin = static_cast<const TIn*>(p.k) + in_off + 8 * lg;
   auto load_early = [&](ScanEarly<TIn>& e, int c) {
-    const TIn* kf = reinterpret_cast<const TIn*>(record(c) + kWsKr) + (M * 4 * 64 + lane) * 8;
     const int row = 16 * M + li;
-    const TIn* qrow = qin + (size_t)(c * kC + (row < L - c * kC ? row : 0)) * kD;
+    const size_t ro = (size_t)(c * kC + (row < L - c * kC ? row : 0)) * kD;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      e.k[j] = R::ld8(kf + j * 64 * 8);
-      e.q[j] = R::ld8(qrow + 32 * j);
+      e.k[j] = R::ld8(kin + ro + 32 * j);
+      e.q[j] = R::ld8(qin + ro + 32 * j);
     }
   };
   // Stage B-D operands, in the order the stages use them (a wave's loads

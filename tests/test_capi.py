@@ -53,7 +53,7 @@ def test_argument_errors_without_device():
     d = _lib.SpkDecodeArgs()
     d.batch, d.num_heads = 1, 16
     assert lib.spk_deltanet_decode_step(C.byref(d), None) == -1         # qkv missing
-    assert lib.spk_chunk_prefill_workspace_size(16, 104, 1, 64) == (2 + 1) * 16 * 82944
+    assert lib.spk_chunk_prefill_workspace_size(16, 104, 1, 64) == (2 + 1) * 16 * 50176
     assert lib.spk_lm_head_workspace_size(248320) % 256 == 0
 
 
