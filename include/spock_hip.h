@@ -387,6 +387,14 @@ int spk_deltanet_prefill_gbeta(const uint16_t* a, const uint16_t* b, int64_t ld,
 int spk_deltanet_norm_gate(const float* core, int64_t core_head_stride, const uint16_t* z,
                            int64_t z_ld, const float* norm_weight, float eps, int32_t tokens,
                            uint16_t* out, int64_t out_ld, spk_stream_t stream);
+/* The unfused decode norm-gate, deltanet_norm_gate.comp:80-105 (dispatched
+ * after deltanet_recurrent.comp at vk_session.cpp:1743-1756 and :3245-3257,
+ * push constants {num_heads, head_dim, eps, output_offset = 0}): per head h,
+ * io[h*128 .. +127] (fp16, in place) <- fp16(fp16(w * RMSNorm(io)) *
+ * SiLU(z)), z [num_heads][128] fp16, norm_weight [128] fp32.  head_dim must
+ * be 128. */
+int spk_deltanet_norm_gate_f16(uint16_t* io, const uint16_t* z, const float* norm_weight,
+                               int32_t num_heads, int32_t head_dim, float eps, spk_stream_t stream);
 /* history[*count] = *token (when *count < capacity), *count += 1, *pos += 1:
  * the greedy loop's bookkeeping, kept on the device so one recorded decode
  * step serves every token. */

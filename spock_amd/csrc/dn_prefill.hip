@@ -92,20 +92,16 @@ __global__ void dn_prefill_gbeta_kernel(const uint16_t* __restrict__ a, const ui
   beta[h * T + t] = 1.0f / (1.0f + spk::expf_det(-bv));
 }
 
-// Gated RMSNorm of the fp32 chunk output: grid (16 heads, T); one wave.
-__global__ __launch_bounds__(64) void dn_norm_gate_kernel(const float* __restrict__ core, long long head_stride,
-                                                          const uint16_t* __restrict__ z, long long zld,
-                                                          const float* __restrict__ norm_w, float eps,
-                                                          uint16_t* __restrict__ out, long long old) {
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-  const float* o = core + ((long long)h * head_stride + t) * kDim;
-  const float oa = o[lane], ob = o[lane + 64];
+// Gated RMSNorm of one 128-wide head row held by one wave (lane l: elements
+// l and l + 64): the squares' tree (s[l] + s[l+64], then strides 32..1),
+// r = 1/sqrt(sum/128 + eps), out = fp16(fp16(w * (o*r)) * SiLU(z)).
+__device__ __forceinline__ void norm_gate_row(float oa, float ob, const uint16_t* __restrict__ zr,
+                                              const float* __restrict__ norm_w, float eps,
+                                              uint16_t* __restrict__ orow, int lane) {
   float v = oa * oa + ob * ob;
   v = spk::tree64_to_lane0(v);
   const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));  // lane 0 broadcast, no LDS
   const float r = spk::rsqrt_det(tot / 128.0f + eps);
-  const uint16_t* zr = z + (long long)t * zld + h * kDim;
-  uint16_t* orow = out + (long long)t * old + h * kDim;
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     const int j = lane + 64 * half;
@@ -113,6 +109,29 @@ __global__ __launch_bounds__(64) void dn_norm_gate_kernel(const float* __restric
     const float weighted = spk::h2f(spk::f2h(norm_w[j] * normed));
     orow[j] = spk::f2h(weighted * spk::silu_det(spk::h2f(zr[j])));
   }
+}
+
+// Gated RMSNorm of the fp32 chunk output: grid (16 heads, T); one wave.
+__global__ __launch_bounds__(64) void dn_norm_gate_kernel(const float* __restrict__ core, long long head_stride,
+                                                          const uint16_t* __restrict__ z, long long zld,
+                                                          const float* __restrict__ norm_w, float eps,
+                                                          uint16_t* __restrict__ out, long long old) {
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  const float* o = core + ((long long)h * head_stride + t) * kDim;
+  norm_gate_row(o[lane], o[lane + 64], z + (long long)t * zld + h * kDim, norm_w, eps,
+                out + (long long)t * old + h * kDim, lane);
+}
+
+// deltanet_norm_gate.comp:80-105 on fp16 rows, in place: grid (heads); one
+// wave.  The shader's 256-lane tree first adds 128 zero partials (exact), so
+// its sum is the 128-wide tree above.
+__global__ __launch_bounds__(64) void dn_norm_gate_f16_kernel(uint16_t* __restrict__ io,
+                                                              const uint16_t* __restrict__ z,
+                                                              const float* __restrict__ norm_w, float eps) {
+  const int h = blockIdx.x, lane = threadIdx.x;
+  uint16_t* row = io + (long long)h * kDim;
+  const float oa = spk::h2f(row[lane]), ob = spk::h2f(row[lane + 64]);
+  norm_gate_row(oa, ob, z + (long long)h * kDim, norm_w, eps, row, lane);
 }
 
 }  // namespace
@@ -160,4 +179,15 @@ extern "C" int spk_deltanet_norm_gate(const float* core, int64_t core_head_strid
                      (long long)core_head_stride, z, (long long)z_ld, norm_weight, eps != 0.0f ? eps : 1e-6f, out,
                      (long long)out_ld);
   return spk::check_launch("spk_deltanet_norm_gate");
+}
+
+extern "C" int spk_deltanet_norm_gate_f16(uint16_t* io, const uint16_t* z, const float* norm_weight,
+                                          int32_t num_heads, int32_t head_dim, float eps, spk_stream_t stream) {
+  if (!io || !z || !norm_weight) return spk::fail(SPK_ERR_NULL, "spk_deltanet_norm_gate_f16: NULL pointer");
+  if (num_heads <= 0 || head_dim != kDim)
+    return spk::fail(SPK_ERR_SHAPE, "spk_deltanet_norm_gate_f16: num_heads %d head_dim %d (head_dim must be %d)",
+                     num_heads, head_dim, kDim);
+  hipLaunchKernelGGL(dn_norm_gate_f16_kernel, dim3(num_heads), dim3(64), 0, spk::to_hip(stream), io, z, norm_weight,
+                     eps);
+  return spk::check_launch("spk_deltanet_norm_gate_f16");
 }

@@ -55,6 +55,9 @@ def test_argument_errors_without_device():
     assert lib.spk_deltanet_decode_step(C.byref(d), None) == -1         # qkv missing
     assert lib.spk_chunk_prefill_workspace_size(16, 104, 1, 64) == (2 + 1) * 16 * 50176
     assert lib.spk_lm_head_workspace_size(248320) % 256 == 0
+    assert lib.spk_deltanet_norm_gate_f16(None, 1, 1, 16, 128, 1e-6, None) == -1   # io missing
+    assert lib.spk_deltanet_norm_gate_f16(1, 1, 1, 16, 64, 1e-6, None) == -2      # head_dim != 128
+    assert lib.spk_deltanet_norm_gate_f16(1, 1, 1, 0, 128, 1e-6, None) == -2      # no heads
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

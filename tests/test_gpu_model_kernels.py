@@ -344,6 +344,36 @@ def test_deltanet_prefill_gbeta_and_norm_gate_bitexact(dev, oracle):
     assert np.array_equal(_u16(out), exp)
 
 
+@pytest.mark.parametrize("case", ["capture", "normal", "tiny", "large", "zero_rows"])
+def test_deltanet_norm_gate_f16_bitexact(dev, oracle, case):
+    """spk_deltanet_norm_gate_f16 (deltanet_norm_gate.comp, fp16 rows in
+    place) against orc_norm_gate_f16: the reference capture's core / z (with
+    the weight they imply; head 0 is fp16-subnormal there), random rows at
+    three magnitudes (subnormal, unit, near the fp16 range whose squares
+    stay finite in fp32), and heads that are exactly zero."""
+    from conftest import GOLDEN
+    from spock_amd import _lib
+    f32 = np.float32
+    nh = 16
+    nw = np.random.default_rng(5).uniform(0.5, 1.5, 128).astype(f32)
+    if case == "capture":
+        d = GOLDEN / "ref_data"
+        core = np.fromfile(d / "layer0_step1_dn_core_2048.fp16", np.uint16)
+        z = np.fromfile(d / "layer0_step1_dn_z_2048.fp16", np.uint16)
+    else:
+        std = {"normal": 1.0, "tiny": 2e-6, "large": 3000.0, "zero_rows": 1.0}[case]
+        core = _rand16(80, nh * 128, std)
+        z = _rand16(81, nh * 128, 4.0)
+        if case == "zero_rows":
+            core.reshape(nh, 128)[::3] = 0
+    io = _h(core, dev)
+    dz, dnw = _h(z, dev), _f(nw, dev)
+    _lib.check(_lib.lib().spk_deltanet_norm_gate_f16(io.data_ptr(), dz.data_ptr(), dnw.data_ptr(), nh, 128, 1e-6,
+                                                     _stream()), "norm gate f16")
+    torch.cuda.synchronize()
+    assert np.array_equal(_u16(io), oracle.norm_gate_f16(core, z, nw))
+
+
 @pytest.mark.parametrize("M,N,K,res", [(512, 6144, 1024, False), (37, 16, 1024, False), (100, 1000, 64, True),
                                        (70, 1024, 3584, True), (512, 1024, 2048, True), (512, 3584, 1024, False),
                                        (33, 40, 96, True), (300, 6000, 96, False), (512, 2048, 1024, True),
