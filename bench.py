@@ -406,6 +406,16 @@ def bench_model(steps, warmup, use_graph=True, cpu=False):
             mism = [i for i, (a, b) in enumerate(zip(best.tokens.tolist(), golden)) if a != b]
             r["first_token_mismatch"] = mism[0] if mism else None
         res[mode] = r
+    # the same decode with each DeltaNet layer's projections and step as two
+    # launches (the session's fused launch is the default)
+    with model.Session(art, use_graph=use_graph, fused_dn_step=False) as s:
+        s.generate(prompt[:64], 4)
+        runs = [s.generate(prompt, MODEL_NEW) for _ in range(max(1, min(3, steps)))]
+    best = min(runs, key=lambda r: r.gpu_decode_ms)
+    res["split_dn_step"] = {"decode_us_per_token": round(best.gpu_decode_ms / 1e3 / best.decode_steps * 1e6, 2),
+                            "launches": "projections, then the DeltaNet step, per layer"}
+    if golden is not None:
+        res["split_dn_step"]["tokens_equal_cpu_oracle"] = best.tokens.tolist() == golden
     # Per-region GPU time of the decode step (the reference's gpu_region_us),
     # from a separate untimed run: HIP events between the regions, so the
     # step's kernels are launched one by one instead of replayed as a graph.

@@ -264,6 +264,19 @@ typedef struct SpkGemvOutput {
 int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count,
                    spk_stream_t stream);
 
+/* A batch-1 DeltaNet layer's input in one launch: spk_gemv_fused with the
+ * RMSNorm input and the four outputs qkv (6144 rows), z (2048), a (16), b (16),
+ * then spk_deltanet_decode_step (d: batch 1, 16 heads, its qkv/z/a/b the
+ * outputs' y).  No single counterpart in the reference: it replaces the
+ * dispatch runs of vk_session.cpp:2606-2870 (projections) and :2876-2884
+ * (conv + recurrence + norm-gate) for a session that runs them back to back.
+ * The workgroups that form one head's rows count their arrival in
+ * arrive[64 * head], and the last runs that head's step; arrive is 1,024 device
+ * ints (4 KiB), zero before the first call, and every call leaves them zero.  Calls that
+ * overlap on one `arrive` race.  Same outputs, bit for bit, as the two calls. */
+int spk_deltanet_inproj_step(const SpkGemvInput* in, const SpkGemvOutput* outs, const SpkDecodeArgs* d,
+                             int32_t* arrive, spk_stream_t stream);
+
 /* Full-attention token mixer: split_q_gate.comp, rms_norm_per_head.comp (q and
  * k, weights applied as 1 + w), rope_apply.comp (pairs (i, i+32) of the first
  * 64 dims, table rope[pos][64] = (cos, sin) pairs), kv_cache_store.comp,

@@ -92,11 +92,13 @@ std::vector<float> rope_table(std::uint32_t max_seq) {
 }
 
 Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::uint32_t max_seq, bool use_graph,
-                             bool ordered_prefill, GpuTimestamps gpu_timestamps, bool lm_head_one_launch)
+                             bool ordered_prefill, GpuTimestamps gpu_timestamps, bool lm_head_one_launch,
+                             bool fused_dn_step)
     : verbose_(verbose),
       use_graph_(use_graph),
       ordered_prefill_(ordered_prefill),
       lm_one_launch_(lm_head_one_launch),
+      fused_dn_step_(fused_dn_step),
       max_seq_(max_seq ? max_seq : MAX_SEQ),
       gpu_ts_(gpu_timestamps) {
   if (max_seq_ > 65536) throw std::runtime_error("max_seq must be <= 65536");
@@ -181,6 +183,8 @@ Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::u
   argmax_key_.zero(stream_);  // spk_argmax_key_take returns it to zero after every use
   take_slots_ = DeviceBuffer(spk_lm_head_take_slots(static_cast<int32_t>(V)) * 8);
   take_slots_.zero(stream_);  // spk_lm_head_argmax_take returns them to zero after every use
+  dn_arrive_ = DeviceBuffer(4096);
+  dn_arrive_.zero(stream_);  // spk_deltanet_inproj_step returns its 16 counts to zero after every use
   tok_ = DeviceBuffer(256);
   pos_ = DeviceBuffer(256);
   history_cap_ = max_seq_;
@@ -404,7 +408,6 @@ void Qwen35Session::enqueue_decode_step() {
           {w.dn_z, z_.get<std::uint16_t>(), nullptr, static_cast<int32_t>(VAL), nullptr},
           {w.dn_a, a_.get<std::uint16_t>(), nullptr, 16, nullptr},
           {w.dn_b, b_.get<std::uint16_t>(), nullptr, 16, nullptr}};
-      spk_check(spk_gemv_fused(&in, outs, 4, S(stream_)), "deltanet projections");
       SpkDecodeArgs d{};
       d.batch = 1;
       d.num_heads = 16;
@@ -423,7 +426,13 @@ void Qwen35Session::enqueue_decode_step() {
       d.z = z_.get<std::uint16_t>();
       d.z_stride = VAL;
       d.norm_weight = w.dn_norm;
-      spk_check(spk_deltanet_decode_step(&d, S(stream_)), "deltanet decode step");
+      if (fused_dn_step_) {
+        spk_check(spk_deltanet_inproj_step(&in, outs, &d, dn_arrive_.get<std::int32_t>(), S(stream_)),
+                  "deltanet projections + decode step");
+      } else {
+        spk_check(spk_gemv_fused(&in, outs, 4, S(stream_)), "deltanet projections");
+        spk_check(spk_deltanet_decode_step(&d, S(stream_)), "deltanet decode step");
+      }
       SpkGemvInput oi{};
       oi.kind = SPK_GEMV_IN_PLAIN;
       oi.in_dim = VAL;
@@ -709,7 +718,7 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
   const int rc = guarded([&] {
     if (!repack_dir) throw std::runtime_error("spk_model_open: NULL directory");
     if (flags & ~(SPK_MODEL_NO_GRAPH | SPK_MODEL_MATRIX_PREFILL | SPK_MODEL_GPU_TIMESTAMPS | SPK_MODEL_GPU_REGIONS |
-                  SPK_MODEL_LMHEAD_ONE_LAUNCH))
+                  SPK_MODEL_LMHEAD_ONE_LAUNCH | SPK_MODEL_SPLIT_DN_STEP))
       throw std::runtime_error("spk_model_open: unknown flags");
     using spock::hip::GpuTimestamps;
     const GpuTimestamps ts = (flags & SPK_MODEL_GPU_REGIONS)      ? GpuTimestamps::per_region
@@ -719,7 +728,8 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
                                                          max_seq > 0 ? static_cast<std::uint32_t>(max_seq) : 0u,
                                                          (flags & SPK_MODEL_NO_GRAPH) == 0,
                                                          (flags & SPK_MODEL_MATRIX_PREFILL) == 0, ts,
-                                                         (flags & SPK_MODEL_LMHEAD_ONE_LAUNCH) != 0);
+                                                         (flags & SPK_MODEL_LMHEAD_ONE_LAUNCH) != 0,
+                                                         (flags & SPK_MODEL_SPLIT_DN_STEP) == 0);
     m = new SpkModel{std::move(s), {}};
   });
   return rc == 0 ? m : nullptr;

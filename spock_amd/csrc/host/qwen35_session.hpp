@@ -72,7 +72,8 @@ class Qwen35Session {
   // holds no timing events).
   explicit Qwen35Session(const std::string& repack_dir, bool verbose = false, std::uint32_t max_seq = MAX_SEQ,
                          bool use_graph = true, bool ordered_prefill = true,
-                         GpuTimestamps gpu_timestamps = GpuTimestamps::off, bool lm_head_one_launch = false);
+                         GpuTimestamps gpu_timestamps = GpuTimestamps::off, bool lm_head_one_launch = false,
+                         bool fused_dn_step = true);
   ~Qwen35Session();
   Qwen35Session(const Qwen35Session&) = delete;
   Qwen35Session& operator=(const Qwen35Session&) = delete;
@@ -131,6 +132,7 @@ class Qwen35Session {
   bool use_graph_ = true;
   bool ordered_prefill_ = true;
   bool lm_one_launch_ = false;  // spk_lm_head_argmax_take, else the key + take pair
+  bool fused_dn_step_ = true;  // spk_deltanet_inproj_step, else the projections then the step
   Qwen35Shape shape_;
   std::uint32_t max_seq_ = MAX_SEQ;
   std::uint32_t n_dn_ = 0, n_attn_ = 0;
@@ -153,7 +155,7 @@ class Qwen35Session {
   DeviceBuffer dn_state_, conv_state_, kv_cache_, a_log_bias_, rope_;
   // decode activations
   DeviceBuffer h_, qkv_, z_, a_, b_, qg_, k_, v_, attn_out_, gate_, up_, logits_;
-  DeviceBuffer attn_ws_, argmax_key_, take_slots_, tok_, pos_, history_;
+  DeviceBuffer attn_ws_, argmax_key_, take_slots_, dn_arrive_, tok_, pos_, history_;
   std::uint32_t history_cap_ = 0;   // token history capacity (= max_seq_: one token per position)
   // prefill activations (capacity prefill_cap_ tokens)
   std::uint32_t prefill_cap_ = 0;

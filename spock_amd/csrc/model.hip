@@ -15,6 +15,7 @@
 #include "argmax_key.hpp"
 #include "capi_common.hpp"
 #include "numerics.hpp"
+#include "dn_step.hpp"
 
 #include <float.h>
 
@@ -1123,6 +1124,164 @@ int grid_for(long long n) {
   return (int)(b > 4096 ? 4096 : (b < 1 ? 1 : b));
 }
 
+
+// ---------------------------------------------------------------------------
+// DeltaNet layer input of a batch-1 decode step in one launch: the input
+// RMSNorm and the q/k/v/z/a/b projections (fused_gemv_kernel's RMSNORM
+// arithmetic, bit for bit), then each head's decode step (spk_dn::dn_step on
+// the workgroup's NW wavefronts) in the last of the head's workgroups to
+// finish.  Workgroup id = 8 (2i + h/8) + h%8 forms rows 2NW i .. 2NW i+2NW-1
+// of head h's 512 q|k|v|z rows, so a head's workgroups have ids congruent
+// mod 8: workgroups are dealt to the 8 XCDs round-robin, so they share one
+// L2, which holds their rows for the head's step.  Each workgroup waits for
+// its row stores, then adds one to the head's arrival count (relaxed
+// atomic); the one that sees the count complete runs the step and resets the
+// count for the next launch.  The 16 counts sit on separate cache lines (on
+// one line the 1,024 atomics serialised: 20.3 us per launch against 11.0).
+// Every workgroup also loads the head's a and b weight rows with its own,
+// so the last one forms a and b without another round trip, and brings a
+// share of the head's state and conv rows into the L2, so the step's first
+// operands do not come from HBM (config 4: 676.4 -> 666.0 us per token).
+// Measured per token, config 4, against the two launches: 4 wavefronts
+// 666.0 vs 678.8 us, 8 wavefronts 660.5-661.6 vs 679.0-680.4, 16
+// wavefronts 668.7 vs 680.6.
+// ---------------------------------------------------------------------------
+constexpr int kDnArriveStride = 64;  // ints between two heads' counts (256 B: own cache lines)
+constexpr int kDnWaves = 8;          // wavefronts per workgroup
+
+struct InprojStep {
+  const uint16_t* x;       // hidden [1024], or the embedding table when token != NULL
+  const uint16_t* norm_w;  // input RMSNorm weight [1024]
+  const int32_t* token;
+  int token_rows;
+  uint16_t* h_out;  // the embedding row (layer 0), or NULL
+  const uint16_t* Wqkv;
+  const uint16_t* Wz;
+  const uint16_t* Wa;
+  const uint16_t* Wb;
+  uint16_t* qkv;
+  uint16_t* z;
+  uint16_t* a;
+  uint16_t* b;
+  int32_t* arrive;  // [16 * kDnArriveStride]
+  spk_dn::DecodeParams dp;
+};
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
+  constexpr int kPieces = 256 / NW;  // workgroups per head (2 rows per wavefront)
+  __shared__ float xs[kHidden];
+  __shared__ float red[257];
+  __shared__ int last;
+  __shared__ uint16_t ab[2];
+  const int id = blockIdx.x;
+  const int h = (id & 7) + 8 * ((id >> 3) & 1);
+  const int piece = id >> 4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // rows r, r+1 of the head's q|k|v|z block (region 0..3 = q, k, v, z)
+  const int r = 2 * NW * piece + 2 * wave;
+  const int region = r >> 7;
+  const uint16_t* W = region < 3 ? s.Wqkv : s.Wz;
+  uint16_t* y = region < 3 ? s.qkv : s.z;
+  const int row = (region < 3 ? region * 2048 : 0) + h * 128 + (r & 127);
+
+  // input operands first, then the weight rows (fused_gemv_kernel's order)
+  const uint16_t* hsrc = s.x;
+  if (s.token) {
+    const int tk = s.token[0];
+    hsrc += (size_t)((tk >= 0 && tk < s.token_rows) ? tk : 0) * kHidden;
+  }
+  const int t4 = 4 * (tid & 255);
+  const uint2 hv = *reinterpret_cast<const uint2*>(hsrc + t4);
+  const uint2 nwv = *reinterpret_cast<const uint2*>(s.norm_w + t4);
+  uint4 wv[2][2], wab[2][2];
+  load_rows<2, 2>(W, row, row + 2, lane, wv);
+  load_rows<2, 1>(s.Wa, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[0]));
+  load_rows<2, 1>(s.Wb, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[1]));
+  // the head's step operands into this XCD's L2 for the last workgroup: a
+  // share of the 64 KiB state and one of the six 1 KiB conv rows (state q|k|v,
+  // weights q|k|v)
+  constexpr int kStateShare = 16384 / kPieces;  // floats per workgroup
+  const float4 tst = *reinterpret_cast<const float4*>(s.dp.state + (size_t)h * 16384 + piece * kStateShare +
+                                                      (wave % (kStateShare / 256)) * 256 + 4 * lane);
+  const int creg = (piece + wave) % 6;
+  const uint16_t* cbase = creg < 3 ? s.dp.conv_state : s.dp.conv_w;
+  const float4 tcv = *reinterpret_cast<const float4*>(cbase + ((creg % 3) * 2048 + h * 128) * 4 + 8 * lane);
+  __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue
+  {
+    const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
+                        spk::h2f(hv.y >> 16)};
+    const float w[4] = {spk::h2f(nwv.x & 0xffffu), spk::h2f(nwv.x >> 16), spk::h2f(nwv.y & 0xffffu),
+                        spk::h2f(nwv.y >> 16)};
+    float pp = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pp = __builtin_fmaf(v[i], v[i], pp);
+    // rms_norm.comp's 256-partial tree (block_tree256 for 256 threads)
+    if (tid < 256) red[tid] = pp;
+    __syncthreads();
+    if (tid < 128) red[tid] = red[tid] + red[tid + 128];
+    __syncthreads();
+    if (tid < 64) red[tid] = red[tid] + red[tid + 64];
+    __syncthreads();
+    if (tid < 64) {
+      float t = red[tid];
+      t = spk::tree64_to_lane0(t);
+      if (tid == 0) red[256] = t;
+    }
+    __syncthreads();
+    const float sum = red[256];
+    const float nf = 1.0f / __builtin_sqrtf(sum / 1024.0f + 1e-6f);
+    if (tid < 256) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[t4 + i] = round16((v[i] * nf) * (1.0f + w[i]));
+    }
+  }
+  __syncthreads();
+  float xf[16];
+#pragma unroll
+  for (int k = 0; k < 16; k += 4) {
+    const float4 t = *reinterpret_cast<const float4*>(&xs[lane * 16 + k]);
+    xf[k] = t.x;
+    xf[k + 1] = t.y;
+    xf[k + 2] = t.z;
+    xf[k + 3] = t.w;
+  }
+  float acc[2] = {lane_dot<2>(wv[0], xf), lane_dot<2>(wv[1], xf)};
+  spk::tree64_rows<2>(acc);
+  if (lane == 0) {
+    y[row] = spk::f2h(acc[0]);
+    y[row + 1] = spk::f2h(acc[1]);
+  }
+  if (s.h_out && id == 0 && tid < 256) *reinterpret_cast<uint2*>(s.h_out + t4) = hv;
+
+  // arrival: this workgroup's row stores (and the L2 touches) complete, then
+  // one count per workgroup
+  asm volatile("" ::"v"(tst.x), "v"(tcv.x));
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(s.arrive + h * kDnArriveStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           kPieces - 1;
+  __syncthreads();
+  if (!last) return;
+  if (tid == 0) __hip_atomic_store(s.arrive + h * kDnArriveStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // a[h] and b[h] (wavefront 0), the projections' order
+  if (wave == 0) {
+    float t[2] = {lane_dot<2>(wab[0], xf), lane_dot<2>(wab[1], xf)};
+    spk::tree64_rows<2>(t);
+    if (lane == 0) {
+      ab[0] = spk::f2h(t[0]);
+      ab[1] = spk::f2h(t[1]);
+      s.a[h] = ab[0];
+      s.b[h] = ab[1];
+    }
+  }
+  __syncthreads();
+  spk_dn::dn_step<true, true, false, true, NW, true>(s.dp, h, 0, ab[0], ab[1]);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1235,6 +1394,56 @@ extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs,
     if (rc) return rc;
   }
   return SPK_OK;
+}
+
+extern "C" int spk_deltanet_inproj_step(const SpkGemvInput* in, const SpkGemvOutput* outs, const SpkDecodeArgs* d,
+                                        int32_t* arrive, spk_stream_t stream) {
+  if (!in || !outs || !d || !arrive) return spk::fail(SPK_ERR_NULL, "spk_deltanet_inproj_step: NULL argument");
+  if (in->kind != SPK_GEMV_IN_RMSNORM || in->in_dim != kHidden || !in->x || !in->x2)
+    return spk::fail(SPK_ERR_ARG, "spk_deltanet_inproj_step: the input must be the RMSNorm kind over %d", kHidden);
+  if (in->token && in->token_rows <= 0)
+    return spk::fail(SPK_ERR_SHAPE, "spk_deltanet_inproj_step: token_rows %d", in->token_rows);
+  if (!spk::aligned(in->x, 16) || !spk::aligned(in->x2, 16) || (in->h_out && !spk::aligned(in->h_out, 16)))
+    return spk::fail(SPK_ERR_ALIGN, "spk_deltanet_inproj_step: input vectors must be 16-byte aligned");
+  static const int dims[4] = {3 * 2048, 2048, 16, 16};
+  for (int i = 0; i < 4; ++i) {
+    if (!outs[i].W || !outs[i].y) return spk::fail(SPK_ERR_NULL, "spk_deltanet_inproj_step: output %d NULL", i);
+    if (outs[i].out_dim != dims[i] || outs[i].residual || outs[i].W_up)
+      return spk::fail(SPK_ERR_SHAPE, "spk_deltanet_inproj_step: output %d must be a plain %d-row projection", i,
+                       dims[i]);
+    if (!spk::aligned(outs[i].W, 16)) return spk::fail(SPK_ERR_ALIGN, "spk_deltanet_inproj_step: W %d alignment", i);
+    if (outs[i].y == in->x || outs[i].y == in->x2)
+      return spk::fail(SPK_ERR_ARG, "spk_deltanet_inproj_step: output %d aliases the input", i);
+  }
+  if (d->batch != 1 || d->num_heads != 16)
+    return spk::fail(SPK_ERR_SHAPE, "spk_deltanet_inproj_step: batch %d heads %d (batch 1, 16 heads)", d->batch,
+                     d->num_heads);
+  if (d->qkv != outs[0].y || d->z != outs[1].y || d->a != outs[2].y || d->b != outs[3].y)
+    return spk::fail(SPK_ERR_ARG, "spk_deltanet_inproj_step: the step's qkv/z/a/b must be the projections' outputs");
+  if (!d->conv_state || !d->conv_weight || !d->state || !d->a_log_bias || !d->norm_weight)
+    return spk::fail(SPK_ERR_NULL, "spk_deltanet_inproj_step: step buffer NULL");
+  if (!spk::aligned(d->conv_state, 8) || !spk::aligned(d->conv_weight, 8) || !spk::aligned(d->state, 16))
+    return spk::fail(SPK_ERR_ALIGN, "spk_deltanet_inproj_step: conv buffers 8-byte, state 16-byte aligned");
+  if (d->layer_idx < 0) return spk::fail(SPK_ERR_ARG, "spk_deltanet_inproj_step: layer_idx < 0");
+  InprojStep s;
+  s.x = in->x;
+  s.norm_w = in->x2;
+  s.token = in->token;
+  s.token_rows = in->token_rows;
+  s.h_out = in->h_out;
+  s.Wqkv = outs[0].W;
+  s.Wz = outs[1].W;
+  s.Wa = outs[2].W;
+  s.Wb = outs[3].W;
+  s.qkv = outs[0].y;
+  s.z = outs[1].y;
+  s.a = outs[2].y;
+  s.b = outs[3].y;
+  s.arrive = arrive;
+  s.dp = spk_dn::make_params(d);
+  hipLaunchKernelGGL(dn_inproj_step_kernel<kDnWaves>, dim3(16 * 256 / kDnWaves), dim3(64 * kDnWaves), 0,
+                     spk::to_hip(stream), s);
+  return spk::check_launch("spk_deltanet_inproj_step");
 }
 
 extern "C" size_t spk_attention_workspace_size(int32_t positions, int32_t tokens) {

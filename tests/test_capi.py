@@ -58,6 +58,7 @@ def test_argument_errors_without_device():
     assert lib.spk_deltanet_norm_gate_f16(None, 1, 1, 16, 128, 1e-6, None) == -1   # io missing
     assert lib.spk_deltanet_norm_gate_f16(1, 1, 1, 16, 64, 1e-6, None) == -2      # head_dim != 128
     assert lib.spk_deltanet_norm_gate_f16(1, 1, 1, 0, 128, 1e-6, None) == -2      # no heads
+    assert lib.spk_deltanet_inproj_step(None, None, None, None, None) == -1
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -48,10 +48,13 @@ def _prompt(golden):
     return (synth.splitmix64(4, n) % np.uint64(golden["artifact"]["vocab"])).astype(np.int32)
 
 
-def test_config4_greedy_tokens_bitexact(dev, artifact, golden):
+@pytest.mark.parametrize("fused", [False, True])
+def test_config4_greedy_tokens_bitexact(dev, artifact, golden, fused):
+    """fused: each DeltaNet layer's input projections and decode step in one
+    launch (spk_deltanet_inproj_step)."""
     from spock_amd import model
-    print("[config4] ordered prefill + 128 greedy tokens", flush=True)
-    with model.Session(artifact) as s:
+    print(f"[config4] ordered prefill + 128 greedy tokens, fused step {fused}", flush=True)
+    with model.Session(artifact, fused_dn_step=fused) as s:
         r = s.generate(_prompt(golden), golden["new_tokens"])
     got = r.tokens.tolist()
     want = golden["tokens"]

@@ -114,6 +114,82 @@ def test_gemv_plain_or_silu_with_residual_in_place(dev, in_dim, silu):
     assert np.array_equal(_u16(dr), exp)
 
 
+@pytest.mark.parametrize("with_token", [False, True])
+def test_deltanet_inproj_step_equals_the_two_calls(dev, with_token):
+    """spk_deltanet_inproj_step (projections and decode step in one launch,
+    the last of a head's workgroups running its step) against
+    spk_gemv_fused + spk_deltanet_decode_step on copies of the same buffers,
+    two steps in a row: every output, the state and the conv history bit for
+    bit, and the arrival counts back at zero after each call."""
+    from spock_amd import _lib, synth
+    print(f"[inproj+step token={with_token}]", flush=True)
+    lib = _lib.lib()
+    V = 512
+    E = _rand16(30, V * 1024).reshape(V, 1024)
+    nrm = _rand16(31, 1024, 0.1)
+    shapes = [6144, 2048, 16, 16]
+    Ws = [_h(_rand16(32 + i, n * 1024, 0.02).reshape(n, 1024), dev) for i, n in enumerate(shapes)]
+    dE, dn = _h(E, dev), _h(nrm, dev)
+    dtok = torch.tensor([211], dtype=torch.int32, device=dev)
+    inp = synth.decode_inputs(1, seed=7)
+    nw = np.random.default_rng(8).uniform(0.5, 1.5, 128).astype(np.float32)
+    shared = {"conv_w": _h(inp["conv_w"], dev), "alb": _f(inp["a_log_bias"], dev), "nw": _f(nw, dev)}
+    arrive = torch.zeros(16 * 64, dtype=torch.int32, device=dev)
+
+    def buffers():
+        b = {"state": _f(inp["state"], dev), "conv": _h(inp["conv_state"], dev), "h_out": torch.zeros(1024, dtype=torch.float16, device=dev)}
+        b["x"] = dE if with_token else _h(E[5], dev)
+        b["ys"] = [torch.zeros(n, dtype=torch.float16, device=dev) for n in shapes]
+        return b
+
+    def args(b):
+        gi = _lib.SpkGemvInput()
+        gi.kind, gi.in_dim, gi.x, gi.x2 = _lib.SPK_GEMV_IN_RMSNORM, 1024, b["x"].data_ptr(), dn.data_ptr()
+        if with_token:
+            gi.token, gi.token_rows, gi.h_out = dtok.data_ptr(), V, b["h_out"].data_ptr()
+        outs = (_lib.SpkGemvOutput * 4)()
+        for i, (W, y, n) in enumerate(zip(Ws, b["ys"], shapes)):
+            outs[i].W, outs[i].y, outs[i].out_dim = W.data_ptr(), y.data_ptr(), n
+        d = _lib.SpkDecodeArgs()
+        d.batch, d.num_heads, d.layer_idx = 1, 16, 5
+        d.qkv, d.qkv_stride = b["ys"][0].data_ptr(), 6144
+        d.conv_state, d.conv_state_stride, d.conv_weight = b["conv"].data_ptr(), 6144 * 4, shared["conv_w"].data_ptr()
+        d.a, d.b, d.ab_stride = b["ys"][2].data_ptr(), b["ys"][3].data_ptr(), 16
+        d.a_log_bias, d.state, d.state_stride = shared["alb"].data_ptr(), b["state"].data_ptr(), 16 * 128 * 128
+        d.z, d.z_stride, d.norm_weight = b["ys"][1].data_ptr(), 2048, shared["nw"].data_ptr()
+        return gi, outs, d
+
+    ref, fus = buffers(), buffers()
+    gr, orr, dr = args(ref)
+    gf, of, df = args(fus)
+    for step in range(2):
+        _lib.check(lib.spk_gemv_fused(C.byref(gr), orr, 4, _stream()), "projections")
+        _lib.check(lib.spk_deltanet_decode_step(C.byref(dr), _stream()), "decode step")
+        _lib.check(lib.spk_deltanet_inproj_step(C.byref(gf), of, C.byref(df), arrive.data_ptr(), _stream()),
+                   "inproj step")
+        torch.cuda.synchronize()
+        for i in range(4):
+            assert torch.equal(ref["ys"][i], fus["ys"][i]), (step, i)
+        assert torch.equal(ref["state"], fus["state"]), step
+        assert torch.equal(ref["conv"], fus["conv"]), step
+        assert torch.equal(ref["h_out"], fus["h_out"]), step
+        assert int(arrive.abs().sum()) == 0, step
+
+
+def test_deltanet_inproj_step_rejects_bad_args(dev):
+    from spock_amd import _lib
+    lib = _lib.lib()
+    gi = _lib.SpkGemvInput()
+    gi.kind, gi.in_dim = _lib.SPK_GEMV_IN_PLAIN, 1024
+    outs = (_lib.SpkGemvOutput * 4)()
+    d = _lib.SpkDecodeArgs()
+    arrive = torch.zeros(16 * 64, dtype=torch.int32, device=dev)
+    assert lib.spk_deltanet_inproj_step(C.byref(gi), outs, C.byref(d), None, _stream()) == -1
+    x = torch.zeros(1024, dtype=torch.float16, device=dev)
+    gi.x, gi.x2 = x.data_ptr(), x.data_ptr()
+    assert lib.spk_deltanet_inproj_step(C.byref(gi), outs, C.byref(d), arrive.data_ptr(), _stream()) == -5  # kind
+
+
 def test_gemv_rejects_aliasing_and_shapes(dev):
     from spock_amd import _lib
     x = torch.zeros(1024, dtype=torch.float16, device=dev)

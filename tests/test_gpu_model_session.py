@@ -31,13 +31,16 @@ def _prompt(n, seed=5):
     return (synth.splitmix64(seed, n) % np.uint64(VOCAB)).astype(np.int32)
 
 
-@pytest.mark.parametrize("use_graph,one_launch", [(True, False), (False, False), (True, True)])
-def test_decode_from_oracle_state_bitexact(dev, small_artifact, use_graph, one_launch):
+@pytest.mark.parametrize("use_graph,one_launch,fused", [(True, False, False), (False, False, False),
+                                                        (True, True, False), (True, False, True),
+                                                        (False, False, True)])
+def test_decode_from_oracle_state_bitexact(dev, small_artifact, use_graph, one_launch, fused):
     """one_launch: the final norm + lm_head + argmax as one launch instead of
-    the default key launch then take."""
+    the default key launch then take.  fused: each DeltaNet layer's input
+    projections and decode step in one launch."""
     import oracle_model
     from spock_amd import model
-    print(f"[session decode graph={use_graph} lm_head one_launch={one_launch}]", flush=True)
+    print(f"[session decode graph={use_graph} lm_head one_launch={one_launch} fused={fused}]", flush=True)
     om = oracle_model.OracleModel(small_artifact, max_seq=MAX_SEQ)
     prompt = _prompt(70)
     tok = om.prefill(prompt)
@@ -47,7 +50,8 @@ def test_decode_from_oracle_state_bitexact(dev, small_artifact, use_graph, one_l
     for i in range(12):
         t, logits, hidden = om.decode(t, want_logits=True)
         want.append(t)
-    with model.Session(small_artifact, max_seq=MAX_SEQ, use_graph=use_graph, lm_head_one_launch=one_launch) as s:
+    with model.Session(small_artifact, max_seq=MAX_SEQ, use_graph=use_graph, lm_head_one_launch=one_launch,
+                       fused_dn_step=fused) as s:
         s.set_state(snap["dn_state"], snap["conv"], snap["kv"], snap["pos"], tok)
         got = s.decode(12)
         glogits, ghidden = s.last_output()
