@@ -302,13 +302,16 @@ size_t spk_attention_workspace_size(int32_t positions, int32_t tokens);
 /* One token at position *pos_dev (< max_seq; read on the device, so the call
  * can be recorded once and replayed); workspace for (max_seq, 1). */
 int spk_attention_decode(const SpkAttnArgs* args, spk_stream_t stream);
-/* spk_attention_decode followed by the o_proj projection (+ residual) with
- * the second stage -- blocks combined in order, normalised, sigmoid-gated --
- * computed inside the projection's prologue: attention_decode.comp,
- * sigmoid_gate.comp, the o_proj matvec and residual_add.comp
- * (vk_session.cpp:2676-2830) in two launches instead of three.  o_proj: W
- * [out_dim][2048], y, residual as in spk_gemv_fused (W_up must be NULL);
- * args->out is not written.  Same bits as spk_attention_decode then
+/* spk_attention_decode followed by the o_proj projection (+ residual):
+ * attention_decode.comp, sigmoid_gate.comp, the o_proj matvec and
+ * residual_add.comp (vk_session.cpp:2676-2830) in two launches instead of
+ * three.  The second stage -- blocks combined in order, normalised,
+ * sigmoid-gated into args->out -- runs in the last-finishing block workgroup
+ * of each KV head, found by an arrival count in the last 512 bytes of the
+ * workspace: they must be zero before the first call, and every call leaves
+ * them zero (calls that overlap on one workspace race).  o_proj: W
+ * [out_dim][2048], y, residual as in spk_gemv_fused (W_up must be NULL; y and
+ * residual must not be args->out).  Same bits as spk_attention_decode then
  * spk_gemv_fused (PLAIN input over args->out). */
 int spk_attention_decode_oproj(const SpkAttnArgs* args, const SpkGemvOutput* o_proj, spk_stream_t stream);
 /* `tokens` consecutive tokens at positions pos0.. (rows of qg/k/v/out are

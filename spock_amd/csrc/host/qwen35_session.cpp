@@ -179,6 +179,7 @@ Qwen35Session::Qwen35Session(const std::string& repack_dir, bool verbose, std::u
   up_ = DeviceBuffer(INTER * 2);
   logits_ = DeviceBuffer(V * 2);
   attn_ws_ = DeviceBuffer(spk_attention_workspace_size(static_cast<int32_t>(max_seq_), 1));
+  attn_ws_.zero(stream_);  // spk_attention_decode_oproj's arrival counts start at zero and are left at zero
   argmax_key_ = DeviceBuffer(SPK_ARGMAX_KEY_WORDS * 8);
   argmax_key_.zero(stream_);  // spk_argmax_key_take returns it to zero after every use
   take_slots_ = DeviceBuffer(spk_lm_head_take_slots(static_cast<int32_t>(V)) * 8);

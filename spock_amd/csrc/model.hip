@@ -99,19 +99,7 @@ struct FusedGemv {
   const uint16_t* res[kLaunchOut];
   int out_dim[kLaunchOut];
   int first_block[kLaunchOut + 1];
-  // input kind kInAttn: the attention blocks' partials (m, S, O[256]) per
-  // (query head, block of 64 positions), the position read on the device and
-  // the gate halves of the q projection (x = qg)
-  const float* part;
-  int max_blocks;
-  int max_seq;
-  const int32_t* pos_dev;
 };
-
-// Input kind of the o_proj GEMV fused behind attention decode (not in the C
-// ABI's SpkGemvInput: spk_attention_decode_oproj selects it).
-constexpr int kInAttn = 3;
-constexpr int kAttnPre = 16;  // blocks whose partials are loaded with the weight rows
 
 template <int N8, int R>
 __device__ __forceinline__ void load_rows(const uint16_t* __restrict__ W, int row0, int out_dim, int lane,
@@ -175,30 +163,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   static_assert(256 * PER * 8 <= kMaxIn, "x staging overruns xs");
   uint2 hv = make_uint2(0, 0), nwv = make_uint2(0, 0);
   uint4 xv[PER], uv[PER];
-  // kInAttn: lane group (h = tid/32, j = tid%32) owns dims 8j..8j+7 of query
-  // head h; the first kAttnPre blocks' m, S and O are loaded here (their
-  // addresses do not depend on the position), clamped to the grid's blocks.
-  int apos = 0;
-  float am = 0.0f, as = 0.0f;
-  float4 aO[KIND == kInAttn ? kAttnPre : 1][2];
-  uint4 agate = make_uint4(0, 0, 0, 0);
-  if constexpr (KIND == kInAttn) {
-    const int h = tid >> 5, j = tid & 31;
-    // position and gate first: a wave's loads return in issue order, so the
-    // sigmoids start while the partials are still in flight
-    apos = a.pos_dev[0];
-    agate = *reinterpret_cast<const uint4*>(a.x + h * 512 + 256 + 8 * j);
-    const float* ph = a.part + (size_t)h * a.max_blocks * kPartFloats;
-    const int bj = min(j, a.max_blocks - 1);
-    am = ph[(size_t)bj * kPartFloats];
-    as = ph[(size_t)bj * kPartFloats + 1];
-#pragma unroll
-    for (int i = 0; i < kAttnPre; ++i) {
-      const float* po = ph + (size_t)min(i, a.max_blocks - 1) * kPartFloats + 2 + 8 * j;
-      aO[i][0] = *reinterpret_cast<const float4*>(po);
-      aO[i][1] = *reinterpret_cast<const float4*>(po + 4);
-    }
-  } else if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
+  if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
     const uint16_t* h = a.x;
     if (a.token) {  // ids outside [0, token_rows) select row 0 instead of reading out of bounds
       const int id = a.token[0];
@@ -226,76 +191,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   load_rows<N8, R>(Wd, row0, out_dim, lane, wv);
   if (PAIR) load_rows<N8, PAIR ? R : 1>(W2d, row0, out_dim, lane, wv2);
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue
-  if constexpr (KIND == kInAttn) {
-    // attn_combine_kernel's arithmetic for the 2048 gated outputs: blocks
-    // combined in order (tot += S_b c_b, O += O_b c_b, c_b = e^{m_b - M}),
-    // normalised, fp16, times sigmoid(gate), fp16.  Lane j of the head's 32
-    // computes c_b and S_b of block b = j (+32 per chunk); the others take
-    // them by shuffle, so no barrier is needed.
-    const int h = tid >> 5, j = tid & 31;
-    const int gbase = tid & 32;  // this head's first lane in the wave
-    float sig[8];
-    {
-      float g[8];
-      unpack8(agate, g);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sig[e] = 1.0f / (1.0f + spk::expf_det(-g[e]));
-    }
-    const float* ph = a.part + (size_t)h * a.max_blocks * kPartFloats;
-    const int nb = (apos >= 0 && apos < a.max_seq) ? (apos + kAttnBlock) / kAttnBlock : 0;
-    float M = j < nb ? am : -INFINITY;
-    for (int b = j + 32; b < nb; b += 32) M = fmaxf(M, ph[(size_t)b * kPartFloats]);
-    M = spk::half_wave_max(M);
-    float tot = 0.0f;
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < nb; c0 += 32) {
-      float mj = am, sj = as;
-      if (c0 > 0 && c0 + j < nb) {
-        mj = ph[(size_t)(c0 + j) * kPartFloats];
-        sj = ph[(size_t)(c0 + j) * kPartFloats + 1];
-      }
-      const float cj = (c0 + j < nb) ? spk::expf_det(mj - M) : 0.0f;
-      const int n = min(32, nb - c0);
-#pragma unroll
-      for (int i0 = 0; i0 < 32; i0 += 8) {
-        if (i0 >= n) break;
-        float4 ov[8][2];
-        if (i0 < kAttnPre && c0 == 0) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            ov[i][0] = aO[i0 < kAttnPre ? i0 + i : 0][0];
-            ov[i][1] = aO[i0 < kAttnPre ? i0 + i : 0][1];
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float* po = ph + (size_t)(c0 + min(i0 + i, n - 1)) * kPartFloats + 2 + 8 * j;
-            ov[i][0] = *reinterpret_cast<const float4*>(po);
-            ov[i][1] = *reinterpret_cast<const float4*>(po + 4);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          // lane i0+i of this head's half wave (lanes 0-31: head 2w, 32-63:
-          // 2w+1).  These reads are independent, so the LDS permutes
-          // pipeline: two readlanes and a select per value measured slower
-          // (config 4: 690.7 vs 684.2 us per token).
-          const float c = __shfl(cj, gbase + i0 + i, 64);
-          const float sb = __shfl(sj, gbase + i0 + i, 64);
-          if (i0 + i < n) {
-            tot = tot + sb * c;
-            const float vv[8] = {ov[i][0].x, ov[i][0].y, ov[i][0].z, ov[i][0].w,
-                                 ov[i][1].x, ov[i][1].y, ov[i][1].z, ov[i][1].w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = o[e] + vv[e] * c;
-          }
-        }
-      }
-    }
-    const float inv = 1.0f / (tot + 1e-30f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xs[h * kHeadDim + 8 * j + e] = round16(round16(o[e] * inv) * sig[e]);
-  } else if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {
+  if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {
     const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
                         spk::h2f(hv.y >> 16)};
     const float w[4] = {spk::h2f(nwv.x & 0xffffu), spk::h2f(nwv.x >> 16), spk::h2f(nwv.y & 0xffffu),
@@ -452,6 +348,7 @@ struct AttnArgs {
   int max_blocks;      // blocks of 64 positions the grid covers
   int store_kv;        // decode: the current position's block stores its K/V row
   int tokens;          // T
+  int32_t* arrive;     // decode with the combine: one count per KV head, 64 ints apart
 };
 
 // K rows in LDS are padded to 264 halves (528 B): lane p reading 16 B of row p
@@ -550,11 +447,22 @@ __device__ __forceinline__ void attn_block_wave(const uint16_t* qs, const uint16
 }
 
 // grid (max_blocks, kv_heads, T); block 256.
+// COMBINE (decode, T = 1): the grid is 1-D, workgroup id = 8 b + 4 kvh (the
+// others exit at once), so the blocks of one KV head run on one XCD and share
+// its L2; after writing its partials each block counts its arrival on the KV
+// head's counter, and the last of the head's live blocks combines them for
+// the head's 4 query heads (attn_combine_kernel's arithmetic, bit for bit)
+// into out, and resets the counter.
+template <bool COMBINE>
 __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
   __shared__ __align__(16) uint16_t qs[4][kHeadDim];  // fp16-rounded q, stored exactly as fp16
   __shared__ __align__(16) uint16_t Ks[kAttnBlock][kKLd];
   __shared__ __align__(16) uint16_t Vs[kAttnBlock][kHeadDim];
-  const int b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+  __shared__ int last;
+  if (COMBINE && (blockIdx.x & 3)) return;
+  const int b = COMBINE ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int kvh = COMBINE ? (int)((blockIdx.x >> 2) & 1) : (int)blockIdx.y;
+  const int t = COMBINE ? 0 : (int)blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = a.pos_dev ? a.pos_dev[0] : a.pos0 + t;
   if (pos < 0 || pos >= a.max_seq) return;
@@ -619,6 +527,82 @@ __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
   __syncthreads();
   float* part = a.part + (((size_t)t * kQHeads + qh) * a.max_blocks + b) * kPartFloats;
   attn_block_wave(qs[wave], Ks, Vs, b, npos, lane, part);
+  if constexpr (COMBINE) {
+    const int nb = (pos + kAttnBlock) / kAttnBlock;
+    __builtin_amdgcn_s_waitcnt(0);  // this block's partials and K/V row stored
+    __syncthreads();
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(a.arrive + 64 * kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nb - 1;
+    __syncthreads();
+    if (!last) return;
+    if (tid == 0) __hip_atomic_store(a.arrive + 64 * kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // query head qh (this wavefront), dims 4 lane .. 4 lane + 3; the first
+    // kPre blocks' partials are loaded in one round trip, later ones 8 at a
+    // time, every load of a group issued before any is used
+    constexpr int kPre = 16;
+    const float* ph = a.part + (size_t)qh * a.max_blocks * kPartFloats;
+    float mv[kPre], sv[kPre];
+    float4 ovp[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+      const float* pb = ph + (size_t)min(i, nb - 1) * kPartFloats;
+      mv[i] = pb[0];
+      sv[i] = pb[1];
+      ovp[i] = *reinterpret_cast<const float4*>(pb + 2 + 4 * lane);
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) M = fmaxf(M, mv[i]);  // clamped copies of block nb-1 change no maximum
+    for (int b0 = kPre; b0 < nb; b0 += 8) {
+      float mm[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mm[i] = ph[(size_t)min(b0 + i, nb - 1) * kPartFloats];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) M = fmaxf(M, mm[i]);
+    }
+    float tot = 0.0f, o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+      if (i < nb) {
+        const float c = spk::expf_det(mv[i] - M);
+        tot = tot + sv[i] * c;
+        o[0] = o[0] + ovp[i].x * c;
+        o[1] = o[1] + ovp[i].y * c;
+        o[2] = o[2] + ovp[i].z * c;
+        o[3] = o[3] + ovp[i].w * c;
+      }
+    }
+    for (int b0 = kPre; b0 < nb; b0 += 8) {
+      float mm[8], ss[8];
+      float4 oo[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float* pb = ph + (size_t)min(b0 + i, nb - 1) * kPartFloats;
+        mm[i] = pb[0];
+        ss[i] = pb[1];
+        oo[i] = *reinterpret_cast<const float4*>(pb + 2 + 4 * lane);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (b0 + i < nb) {
+          const float c = spk::expf_det(mm[i] - M);
+          tot = tot + ss[i] * c;
+          o[0] = o[0] + oo[i].x * c;
+          o[1] = o[1] + oo[i].y * c;
+          o[2] = o[2] + oo[i].z * c;
+          o[3] = o[3] + oo[i].w * c;
+        }
+      }
+    }
+    const float inv = 1.0f / (tot + 1e-30f);
+    float g[4];
+    load4h(a.qg + qh * 512 + 256 + 4 * lane, g);
+    uint16_t r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = spk::f2h(round16(o[e] * inv) * (1.0f / (1.0f + spk::expf_det(-g[e]))));
+    *reinterpret_cast<uint2*>(a.out + qh * kHeadDim + 4 * lane) =
+        make_uint2((uint32_t)r[0] | ((uint32_t)r[1] << 16), (uint32_t)r[2] | ((uint32_t)r[3] << 16));
+  }
 }
 
 // Prefill block pass: one workgroup per (64-position block b, KV head, group
@@ -1316,10 +1300,6 @@ static int launch_fused_gemv(const SpkGemvInput* in, const SpkGemvOutput* outs, 
     a.first_block[i] = blocks;
   }
   a.first_block[kLaunchOut] = blocks;
-  a.part = nullptr;
-  a.max_blocks = 0;
-  a.max_seq = 0;
-  a.pos_dev = nullptr;
   hipStream_t s = spk::to_hip(stream);
   const bool pair = outs[0].W_up != nullptr;
 #define SPK_FGK(n8, r, kind)                                                                            \
@@ -1446,10 +1426,16 @@ extern "C" int spk_deltanet_inproj_step(const SpkGemvInput* in, const SpkGemvOut
   return spk::check_launch("spk_deltanet_inproj_step");
 }
 
-extern "C" size_t spk_attention_workspace_size(int32_t positions, int32_t tokens) {
-  if (positions <= 0 || tokens <= 0) return 0;
+// the blocks' partials, then (decode with o_proj) two arrival counts on
+// lines of their own
+static size_t attn_partials_bytes(int32_t positions, int32_t tokens) {
   const size_t nb = ((size_t)positions + kAttnBlock - 1) / kAttnBlock;
   return (((size_t)tokens * kQHeads * nb * kPartFloats * sizeof(float)) + 255) / 256 * 256;
+}
+
+extern "C" size_t spk_attention_workspace_size(int32_t positions, int32_t tokens) {
+  if (positions <= 0 || tokens <= 0) return 0;
+  return attn_partials_bytes(positions, tokens) + 2 * 256;
 }
 
 static int attention_common(const SpkAttnArgs* p, int T, int positions, const char* who, AttnArgs& a,
@@ -1491,7 +1477,7 @@ extern "C" int spk_attention_decode(const SpkAttnArgs* p, spk_stream_t stream) {
   a.pos0 = 0;
   a.store_kv = 1;
   hipStream_t s = spk::to_hip(stream);
-  hipLaunchKernelGGL(attn_blocks_kernel, dim3(a.max_blocks, kKvHeads, 1), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_blocks_kernel<false>, dim3(a.max_blocks, kKvHeads, 1), dim3(256), 0, s, a);
   rc = spk::check_launch("spk_attention_decode (blocks)");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(kQHeads, 1), dim3(256), 0, s, a);
@@ -1505,33 +1491,24 @@ extern "C" int spk_attention_decode_oproj(const SpkAttnArgs* p, const SpkGemvOut
     return spk::fail(SPK_ERR_SHAPE, "%s: o_proj out_dim %d (single projection)", name, o_proj->out_dim);
   if (!spk::aligned(o_proj->W, 16)) return spk::fail(SPK_ERR_ALIGN, "%s: o_proj W must be 16-byte aligned", name);
   AttnArgs a;
-  int rc = attention_common(p, 1, p ? p->max_seq : 0, name, a, false);
+  int rc = attention_common(p, 1, p ? p->max_seq : 0, name, a);
   if (rc) return rc;
   if (!p->pos_dev) return spk::fail(SPK_ERR_NULL, "%s: NULL pos_dev", name);
+  if (o_proj->y == p->out || o_proj->residual == p->out)
+    return spk::fail(SPK_ERR_ARG, "%s: o_proj output aliases the attention output", name);
   a.pos_dev = p->pos_dev;
   a.pos0 = 0;
   a.store_kv = 1;
+  a.arrive = reinterpret_cast<int32_t*>(static_cast<char*>(p->workspace) + attn_partials_bytes(p->max_seq, 1));
   hipStream_t s = spk::to_hip(stream);
-  hipLaunchKernelGGL(attn_blocks_kernel, dim3(a.max_blocks, kKvHeads, 1), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_blocks_kernel<true>, dim3(8 * a.max_blocks), dim3(256), 0, s, a);
   rc = spk::check_launch(name);
   if (rc) return rc;
-  FusedGemv g{};
-  g.kind = kInAttn;
-  g.in_dim = kQHeads * kHeadDim;
-  g.x = p->qg;
-  g.count = 1;
-  g.W[0] = o_proj->W;
-  g.y[0] = o_proj->y;
-  g.res[0] = o_proj->residual;
-  g.out_dim[0] = o_proj->out_dim;
-  const int blocks = (o_proj->out_dim + 3) / 4;  // R = 1 row per wave
-  for (int i = 1; i <= kLaunchOut; ++i) g.first_block[i] = blocks;
-  g.part = a.part;
-  g.max_blocks = a.max_blocks;
-  g.max_seq = a.max_seq;
-  g.pos_dev = p->pos_dev;
-  hipLaunchKernelGGL((fused_gemv_kernel<4, 1, false, kInAttn>), dim3(blocks), dim3(256), 0, s, g);
-  return spk::check_launch(name);
+  SpkGemvInput gi{};
+  gi.kind = SPK_GEMV_IN_PLAIN;
+  gi.in_dim = kQHeads * kHeadDim;
+  gi.x = p->out;
+  return launch_fused_gemv(&gi, o_proj, 1, true, 4, 1, stream);
 }
 
 extern "C" int spk_attention_prefill(const SpkAttnArgs* p, int32_t pos0, int32_t tokens, spk_stream_t stream) {

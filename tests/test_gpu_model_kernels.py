@@ -251,7 +251,7 @@ def _attn_args(dev, rope, kv, qg, k, v, qn, kn, max_seq, T, positions):
     d["rope"] = _f(rope, dev)
     d["out"] = torch.empty(T * 2048, dtype=torch.float16, device=dev)
     ws = int(_lib.lib().spk_attention_workspace_size(positions, T))
-    d["ws"] = torch.empty(ws, dtype=torch.uint8, device=dev)
+    d["ws"] = torch.zeros(ws, dtype=torch.uint8, device=dev)  # the o_proj form's arrival counts start at zero
     a = _lib.SpkAttnArgs()
     a.qg, a.k, a.v = d["qg"].data_ptr(), d["k"].data_ptr(), d["v"].data_ptr()
     a.q_norm_w, a.k_norm_w, a.rope = d["qn"].data_ptr(), d["kn"].data_ptr(), d["rope"].data_ptr()
