@@ -458,6 +458,12 @@ int spk_selftest_numerics(const float* x, int32_t n, float* out, spk_stream_t st
  * strides (else each workgroup reads its own contiguous share); out holds
  * `blocks` words (almost never written). */
 int spk_selftest_mfma_peak(int32_t blocks, int32_t iters, float* out, spk_stream_t stream);
+/* out[i] = the XCD (XCC) that ran workgroup i of a `blocks`-workgroup launch.
+ * spk_deltanet_inproj_step and spk_attention_decode_oproj hand rows from one
+ * workgroup to another through the L2 they share, which holds when
+ * workgroup ids are dealt to the XCDs round-robin (id mod 8 on MI355X); the
+ * GPU tests check that with this call. */
+int spk_selftest_xcc_ids(int32_t blocks, int32_t* out, spk_stream_t stream);
 int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, int32_t mode, uint32_t* out,
                              spk_stream_t stream);
 

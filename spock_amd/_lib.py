@@ -36,6 +36,7 @@ SIGNATURES = {
     "spk_lm_head_argmax_noalloc": (C.c_int, [_p, _p, _i32, _i32, _p, _p, _p]),
     "spk_selftest_numerics": (C.c_int, [_p, _i32, _p, _p]),
     "spk_selftest_mfma_peak": (C.c_int, [_i32, _i32, _p, _p]),
+    "spk_selftest_xcc_ids": (C.c_int, [_i32, _p, _p]),
     "spk_selftest_stream_read": (C.c_int, [_p, _sz, _i32, _i32, _p, _p]),
     # Qwen3.5 model kernels
     "spk_gemv_fused": (C.c_int, [_p, _p, _i32, _p]),

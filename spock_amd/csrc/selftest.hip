@@ -93,7 +93,20 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
   if (acc == 0x9e3779b9u) out[blockIdx.x] = acc;
 }
 
+// XCC (XCD) id of each workgroup: hardware register HW_REG_XCC_ID (20),
+// bits 3:0.
+__global__ __launch_bounds__(64) void xcc_id_kernel(int32_t* __restrict__ out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = (int32_t)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15);
+}
+
 }  // namespace
+
+extern "C" int spk_selftest_xcc_ids(int32_t blocks, int32_t* out, spk_stream_t stream) {
+  if (!out) return spk::fail(SPK_ERR_NULL, "spk_selftest_xcc_ids: NULL out");
+  if (blocks <= 0) return spk::fail(SPK_ERR_SHAPE, "spk_selftest_xcc_ids: blocks %d", blocks);
+  hipLaunchKernelGGL(xcc_id_kernel, dim3(blocks), dim3(64), 0, spk::to_hip(stream), out);
+  return spk::check_launch("spk_selftest_xcc_ids");
+}
 
 extern "C" int spk_selftest_mfma_peak(int32_t blocks, int32_t iters, float* out, spk_stream_t stream) {
   if (!out) return spk::fail(SPK_ERR_NULL, "spk_selftest_mfma_peak: NULL out");

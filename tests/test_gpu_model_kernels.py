@@ -176,6 +176,19 @@ def test_deltanet_inproj_step_equals_the_two_calls(dev, with_token):
         assert int(arrive.abs().sum()) == 0, step
 
 
+def test_workgroups_are_dealt_to_xcds_round_robin(dev):
+    """The fused DeltaNet launch and the attention combine hand rows between
+    workgroups whose ids are congruent mod 8 through the L2 of their XCD:
+    the dispatch must deal workgroup ids to the 8 XCDs round-robin."""
+    from spock_amd import _lib
+    n = 4096
+    out = torch.full((n,), -1, dtype=torch.int32, device=dev)
+    _lib.check(_lib.lib().spk_selftest_xcc_ids(n, out.data_ptr(), _stream()), "xcc ids")
+    torch.cuda.synchronize()
+    ids = out.cpu().numpy()
+    assert np.array_equal(ids, np.arange(n) % 8), np.unique(ids)
+
+
 def test_deltanet_inproj_step_rejects_bad_args(dev):
     from spock_amd import _lib
     lib = _lib.lib()
