@@ -1,8 +1,10 @@
 // decode.hip -- DeltaNet recurrent decode step for B independent sequences.
 //
 // One workgroup of 4, 8 or 16 wavefronts per (head, sequence): the launch
-// picks the width from the batch (16 wavefronts when a handful of heads must
-// carry the whole launch, 4 when thousands of workgroups fill the chip).  The
+// picks the width and the state-load kind from the batch (16 wavefronts and
+// plain loads when a handful of heads must carry the whole launch, 4
+// wavefronts and non-temporal loads when thousands of workgroups fill the
+// chip).  The
 // step itself (conv, L2, g/beta, recurrence, norm-gate; its reduction orders)
 // is spk_dn::dn_step in dn_step.hpp.
 #include <stdlib.h>
@@ -16,9 +18,9 @@ namespace {
 using spk_dn::DecodeParams;
 using spk_dn::make_params;
 
-template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE, int WAVES>
+template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE, int WAVES, bool NT_STATE>
 __global__ __launch_bounds__(WAVES * 64) void dn_decode_kernel(DecodeParams p) {
-  spk_dn::dn_step<CONV, REC, GB_TAIL, NORM_GATE, WAVES>(p, blockIdx.x, blockIdx.y);
+  spk_dn::dn_step<CONV, REC, GB_TAIL, NORM_GATE, WAVES, false, NT_STATE>(p, blockIdx.x, blockIdx.y);
 }
 
 int validate(const SpkDecodeArgs* a, bool conv, bool rec, bool gb_inline, bool norm_gate) {
@@ -57,21 +59,43 @@ int validate(const SpkDecodeArgs* a, bool conv, bool rec, bool gb_inline, bool n
   return SPK_OK;
 }
 
-// Wavefronts per workgroup by the number of workgroups the launch has:
-// overridable with SPK_DECODE_WAVES=4|8|16 (measurement only).  Measured (us
-// per launch, B = 1 / 16 / 64 / 256 with 16 heads): 16 wavefronts 4.5 / 8.25
-// / 29.2 / 99, 8: 4.55 / 8.37 / 25.5 / 86.7, 4: 5.1 / 9.4 / 25.6 / 87.3.  The
-// reduction order does not depend on the count, so results are identical.
-int decode_waves(int workgroups) {
+// Launch shape by the number of workgroups (heads x sequences): 16
+// wavefronts up to 256 workgroups, 4 above; non-temporal state loads from
+// 256 workgroups on.  The wavefront count is overridable with
+// SPK_DECODE_WAVES=4|8|16 (measurement only).  Measured (us per launch,
+// graph-timed over rotated copies, one box, B = 1 / 4 / 16 / 32 / 64 / 128 /
+// 256 with 16 heads):
+//   plain loads, 16 wavefronts  4.62 / 5.17 / 8.21 / 14.37 / 28.42 / 46.88 / 87.62
+//   plain loads,  8 wavefronts  4.71 / 5.25 / 8.38 / 14.16 / 25.08 / 42.33 / 81.32
+//   plain loads,  4 wavefronts  5.32 / 5.88 / 9.43 / 14.33 / 25.10 / 42.67 / 81.87
+//   non-temporal, 16 wavefronts 4.94 / 5.75 / 8.00 / 13.56 / 25.48 / 44.19 / 84.54
+//   non-temporal,  8 wavefronts 4.95 / 5.72 / 8.18 / 14.29 / 23.60 / 42.42 / 81.07
+//   non-temporal,  4 wavefronts 5.71 / 6.59 / 9.21 / 13.51 / 23.76 / 42.91 / 81.22
+// The reduction order depends on neither, so results are identical.
+struct DecodeShape {
+  int waves;
+  bool nt_state;
+};
+
+DecodeShape decode_shape(int workgroups) {
   static const int forced = [] {
     const char* e = getenv("SPK_DECODE_WAVES");
     const int v = e ? atoi(e) : 0;
     return (v == 4 || v == 8 || v == 16) ? v : 0;
   }();
-  if (forced) return forced;
-  if (workgroups <= 256) return 16;
-  if (workgroups <= 512) return 8;
-  return 4;
+  const bool nt = workgroups >= 256;
+  if (forced) return {forced, nt};
+  return {workgroups <= 256 ? 16 : 4, nt};
+}
+
+template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE, bool NT>
+void launch_shape(int waves, dim3 grid, hipStream_t s, const DecodeParams& p) {
+  if (waves == 16)
+    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 16, NT>), grid, dim3(1024), 0, s, p);
+  else if (waves == 8)
+    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 8, NT>), grid, dim3(512), 0, s, p);
+  else
+    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 4, NT>), grid, dim3(256), 0, s, p);
 }
 
 template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE>
@@ -80,17 +104,12 @@ int launch(const SpkDecodeArgs* a, spk_stream_t stream, const char* name) {
   if (rc) return rc;
   if (a->batch == 0) return SPK_OK;
   dim3 grid(a->num_heads, a->batch);
-  const int waves = decode_waves(a->num_heads * a->batch);
+  const DecodeShape sh = decode_shape(a->num_heads * a->batch);
   hipStream_t s = spk::to_hip(stream);
-  if (waves == 16)
-    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 16>), grid, dim3(1024), 0, s,
-                       make_params(a));
-  else if (waves == 8)
-    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 8>), grid, dim3(512), 0, s,
-                       make_params(a));
+  if (sh.nt_state)
+    launch_shape<CONV, REC, GB_TAIL, NORM_GATE, true>(sh.waves, grid, s, make_params(a));
   else
-    hipLaunchKernelGGL((dn_decode_kernel<CONV, REC, GB_TAIL, NORM_GATE, 4>), grid, dim3(256), 0, s,
-                       make_params(a));
+    launch_shape<CONV, REC, GB_TAIL, NORM_GATE, false>(sh.waves, grid, s, make_params(a));
   return spk::check_launch(name);
 }
 

@@ -66,8 +66,10 @@ __device__ __forceinline__ float tree32(const float (*part)[128], int col) {
 // the state tail (deltanet_recurrent.comp) instead of a/b/A_log/dt_bias.
 // NORM_GATE: RMSNorm-gate the output (else fp16 of the raw output).
 // AB_IN: the step's a and b inputs (fp16 bits) are the arguments a_in and
-// b_in instead of p.a / p.b.
-template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE, int WAVES, bool AB_IN = false>
+// b_in instead of p.a / p.b.  NT_STATE: read the state with non-temporal
+// loads (faster once hundreds of workgroups stream states, slower for a few).
+template <bool CONV, bool REC, bool GB_TAIL, bool NORM_GATE, int WAVES, bool AB_IN = false,
+          bool NT_STATE = false>
 __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, uint16_t a_in = 0,
                                         uint16_t b_in = 0) {
   // G row groups of 4 rows per lane: 32 row groups over WAVES*2 lanes per column
@@ -141,8 +143,16 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
   if (REC) {
     st_head = p.state + (long long)seq * p.state_stride + (long long)h * 128 * 128;
 #pragma unroll
-    for (int m = 0; m < M; ++m)
-      S[m] = *reinterpret_cast<const float4*>(st_head + (rq * M + m) * 128 + c4 * 4);
+    for (int m = 0; m < M; ++m) {
+      const float* src = st_head + (rq * M + m) * 128 + c4 * 4;
+      if (NT_STATE) {
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const f4v t = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(src));
+        S[m] = make_float4(t.x, t.y, t.z, t.w);
+      } else {
+        S[m] = *reinterpret_cast<const float4*>(src);
+      }
+    }
   }
 
   if (REC && !GB_TAIL && wave == 3) {
