@@ -354,6 +354,30 @@ def bench_lm_head(steps, warmup):
     return res
 
 
+def bench_gemv_orders(steps, warmup):
+    """spk_matvec_f16_order over the lm_head matrix (248320 x 1024, 508.6
+    MB, two rotated copies) in each reference summation order; logits only."""
+    import torch
+    from spock_amd import synth
+    dev = torch.device("cuda:0")
+    W0 = torch.from_numpy(synth.gemv_weights(VOCAB, HIDDEN, seed=31).view(np.float16)).to(dev)
+    Ws = [W0, W0.clone()]
+    x = torch.from_numpy(synth.gemv_input(HIDDEN, seed=32).view(np.float16)).to(dev)
+    y = torch.empty(VOCAB, dtype=torch.float16, device=dev)
+    from spock_amd import _lib
+    lib = _lib.lib()
+    nbytes = VOCAB * HIDDEN * 2 + HIDDEN * 2 + VOCAB * 2
+    res = {"shape": [VOCAB, HIDDEN], "bytes_per_call": nbytes}
+    for name, order in (("spans", 0), ("strided", 1), ("serial", 2)):
+        fn = lambda i, order=order: lib.spk_matvec_f16_order(Ws[i].data_ptr(), x.data_ptr(), y.data_ptr(),
+                                                             VOCAB, HIDDEN, order, _stream())
+        ms = timed_graph(fn, steps, warmup, rotate=2)
+        gbs = nbytes / (ms / 1e3) / 1e9
+        res[name] = {"launch_us": round(ms * 1e3, 2), "achieved_gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return res
+
+
 MODEL_SEED, MODEL_PROMPT, MODEL_NEW = 2026, 512, 128
 
 
@@ -613,7 +637,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="model workload: launch the decode kernels one by one instead of the HIP graph")
-    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "lm_head", "copy", "model", "ceilings", "cpu"],
+    ap.add_argument("--only", choices=["prefill", "config0", "decode", "gemv", "gemv_orders", "lm_head", "copy", "model",
+                                       "ceilings", "cpu"],
                     help="run one workload and print its own JSON (for profiler runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -636,9 +661,10 @@ def main():
         prefill_as_headline = lambda s, w: bench_prefill(
             s, w, before_timing=lambda: bench_ceilings(20, 5), prewarm=PREFILL_PREWARM_CALLS)
         fns = {"prefill": prefill_as_headline, "config0": bench_config0, "gemv": bench_gemv_chain,
-               "lm_head": bench_lm_head, "copy": bench_copy, "ceilings": bench_ceilings,
+               "lm_head": bench_lm_head, "gemv_orders": bench_gemv_orders, "copy": bench_copy,
+               "ceilings": bench_ceilings,
                "model": lambda s, w: bench_model(s, w, use_graph=not args.no_graph),
-        "cpu": lambda s, w: cpu_baselines_secondary(),
+               "cpu": lambda s, w: cpu_baselines_secondary(),
                "decode": lambda s, w: [bench_decode(B, s, w) for B in (1, 16, 64, 256)]}
         r = fns[args.only](args.steps, args.warmup)
         print(json.dumps({"only": args.only, "result": r}, default=float), flush=True)
@@ -677,6 +703,8 @@ def main():
         log(f"[bench] gemv chain {secondary['gemv_chain']}")
         secondary["lm_head_argmax"] = bench_lm_head(args.steps, args.warmup)
         log(f"[bench] lm_head {secondary['lm_head_argmax']}")
+        secondary["gemv_orders"] = bench_gemv_orders(args.steps, args.warmup)
+        log(f"[bench] gemv orders {secondary['gemv_orders']}")
         secondary["config4_full_model"] = bench_model(args.steps, args.warmup, cpu=not args.no_cpu_baseline)
         log(f"[bench] full model {secondary['config4_full_model']}")
         secondary["measured_ceilings"] = ceilings

@@ -177,6 +177,21 @@ int spk_deltanet_recurrent(const SpkDecodeArgs* args, spk_stream_t stream);
 int spk_matvec_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, int32_t out_dim,
                    int32_t in_dim, spk_stream_t stream);
 
+/* The same GEMV in the summation order of a chosen reference shader (the
+ * session's pipeline selection, vk_session.cpp:2228-2256 and :3533-3545):
+ *   SPK_MATVEC_ORDER_SPANS    lm_head_tiled.comp:40-87 (= spk_matvec_f16;
+ *                             in_dim % 64 == 0)
+ *   SPK_MATVEC_ORDER_STRIDED  matvec_tiled.comp:41-84 (SPOCK_GPU_MATVEC_TILED):
+ *                             lane l of 64 sums j = l, l+64, ... sequentially,
+ *                             then the 32..1 tree; any in_dim > 0
+ *   SPK_MATVEC_ORDER_SERIAL   matvec.comp:28-41 (the session's default): one
+ *                             sequential sum over j = 0 .. in_dim-1; any in_dim > 0
+ * fp32 accumulation from 0 (fp16 x fp16 products are exact, so fma and
+ * mul+add agree), one RNE rounding to fp16.  SPK_ERR_ARG for another order. */
+enum { SPK_MATVEC_ORDER_SPANS = 0, SPK_MATVEC_ORDER_STRIDED = 1, SPK_MATVEC_ORDER_SERIAL = 2 };
+int spk_matvec_f16_order(const uint16_t* W, const uint16_t* x, uint16_t* y, int32_t out_dim,
+                         int32_t in_dim, int32_t order, spk_stream_t stream);
+
 /* Several independent GEMVs, up to 4 per launch (the decode projections). */
 typedef struct SpkMatvecDesc {
   const uint16_t* W;

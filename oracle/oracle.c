@@ -649,6 +649,47 @@ int orc_matvec_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, size_t out
   return 0;
 }
 
+/* matvec_tiled.comp:41-84: lane l of 64 sums j = l, l+64, ... < in_dim
+ * (:54-58, fp32 from 0), then s[l] += s[l+stride] for stride 32..1 (:66-73),
+ * fp16 store (:80).  Any in_dim. */
+int orc_matvec_f16_strided(const uint16_t* W, const uint16_t* x, uint16_t* y, size_t out_dim,
+                           size_t in_dim) {
+  if (in_dim == 0) return -1;
+  float* xf = (float*)malloc(in_dim * 4);
+  orc_h2f_array(x, xf, in_dim);
+  float part[64];
+  for (size_t r = 0; r < out_dim; ++r) {
+    const uint16_t* row = W + r * in_dim;
+    for (size_t l = 0; l < 64; ++l) {
+      float acc = 0.0f;
+      for (size_t j = l; j < in_dim; j += 64) acc = fmaf(orc_h2f(row[j]), xf[j], acc);
+      part[l] = acc;
+    }
+    for (size_t stride = 32; stride > 0; stride >>= 1)
+      for (size_t l = 0; l < stride; ++l) part[l] = part[l] + part[l + stride];
+    y[r] = orc_f2h_rne(part[0]);
+  }
+  free(xf);
+  return 0;
+}
+
+/* matvec.comp:28-41: one invocation per row, sum over j = 0 .. in_dim-1 in
+ * order (:35-38, fp32 from 0), fp16 store (:40).  Any in_dim. */
+int orc_matvec_f16_serial(const uint16_t* W, const uint16_t* x, uint16_t* y, size_t out_dim,
+                          size_t in_dim) {
+  if (in_dim == 0) return -1;
+  float* xf = (float*)malloc(in_dim * 4);
+  orc_h2f_array(x, xf, in_dim);
+  for (size_t r = 0; r < out_dim; ++r) {
+    const uint16_t* row = W + r * in_dim;
+    float acc = 0.0f;
+    for (size_t j = 0; j < in_dim; ++j) acc = fmaf(orc_h2f(row[j]), xf[j], acc);
+    y[r] = orc_f2h_rne(acc);
+  }
+  free(xf);
+  return 0;
+}
+
 uint32_t orc_argmax_f16(const uint16_t* vals, size_t n) {
   const size_t E = (n + 255) / 256;
   float mv[256];

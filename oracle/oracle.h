@@ -39,6 +39,11 @@
  *                               orc_recurrent) and orc_norm_gate_row, each pinned
  *                               above; beta also by the layer0 g_beta capture
  *   orc_matvec_f16 / orc_lm_head  fp64 dot products -> one RNE rounding (<=1 ulp)
+ *   orc_matvec_f16_strided / _serial  the same fp64 bound, and cancellation rows
+ *                               (+L and -L placed in one lane's chain, x = 1,
+ *                               small exact terms elsewhere) whose exact sum
+ *                               only the named order keeps: the other orders
+ *                               absorb small terms into L first
  *   orc_argmax_f16              brute-force emulation of argmax.comp's lane/tree
  *                               order on crafted tie patterns
  */
@@ -162,6 +167,13 @@ void orc_decode_step(size_t B, size_t num_heads, size_t layer_idx, float q_scale
  * 64-lane tree with strides 32..1.  Requires in % 64 == 0 (lm_head_tiled.comp:46). */
 int orc_matvec_f16(const uint16_t* W, const uint16_t* x, uint16_t* y,
                    size_t out_dim, size_t in_dim);
+/* matvec_tiled.comp:41-84 order: lane l sums j = l, l+64, ... sequentially,
+ * then the 32..1 tree; any in_dim > 0. */
+int orc_matvec_f16_strided(const uint16_t* W, const uint16_t* x, uint16_t* y,
+                           size_t out_dim, size_t in_dim);
+/* matvec.comp:28-41 order: one sequential sum over j; any in_dim > 0. */
+int orc_matvec_f16_serial(const uint16_t* W, const uint16_t* x, uint16_t* y,
+                          size_t out_dim, size_t in_dim);
 /* argmax.comp:27-63 exactly (256 lanes, contiguous blocks, strict-greater tree) */
 uint32_t orc_argmax_f16(const uint16_t* vals, size_t n);
 /* lm_head logits (matvec) + argmax; logits may be NULL */

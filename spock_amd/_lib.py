@@ -30,6 +30,7 @@ SIGNATURES = {
     "spk_deltanet_recurrent": (C.c_int, [_p, _p]),
     "spk_matvec_f16": (C.c_int, [_p, _p, _p, _i32, _i32, _p]),
     "spk_matvec_f16_batched": (C.c_int, [_p, _i32, _p]),
+    "spk_matvec_f16_order": (C.c_int, [_p, _p, _p, _i32, _i32, _i32, _p]),
     "spk_argmax_f16": (C.c_int, [_p, _i32, _p, _p]),
     "spk_lm_head_workspace_size": (_sz, [_i32]),
     "spk_lm_head_argmax": (C.c_int, [_p, _p, _i32, _i32, _p, _p, _p, _sz, _p]),

@@ -267,6 +267,121 @@ __global__ __launch_bounds__(256) void gemv_batched_kernel(GemvBatch b) {
   }
 }
 
+// matvec_tiled.comp:41-84's order: lane l sums j = l, l+64, l+128, ... < in_dim
+// sequentially (fp32, from 0), then the 64-lane tree s[l] += s[l+stride] for
+// stride 32..1; any in_dim.  One wavefront per R rows; each load instruction
+// reads 64 consecutive fp16 of a row (128 coalesced bytes), U steps of every
+// row in flight before the first is used.  Past in_dim a lane's index is
+// clamped and its product not added.
+template <int R>
+__global__ __launch_bounds__(256) void gemv_strided_kernel(const uint16_t* __restrict__ W,
+                                                           const uint16_t* __restrict__ x,
+                                                           uint16_t* __restrict__ y, int out_dim,
+                                                           int in_dim) {
+  constexpr int U = 8;
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (row0 >= out_dim) return;  // wave-uniform: the whole wavefront leaves
+  const int steps = (in_dim + 63) / 64;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  for (int i0 = 0; i0 < steps; i0 += U) {
+    uint16_t wv[R][U], xv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = min(lane + 64 * (i0 + u), in_dim - 1);
+      xv[u] = x[j];
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[r][u] = W[(size_t)min(row0 + r, out_dim - 1) * in_dim + j];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = lane + 64 * (i0 + u) < in_dim;
+      const float xf = spk::h2f(xv[u]);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float t = __builtin_fmaf(spk::h2f(wv[r][u]), xf, acc[r]);
+        acc[r] = valid ? t : acc[r];
+      }
+    }
+  }
+  spk::tree64_rows<R>(acc);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (row0 + r < out_dim) y[row0 + r] = spk::f2h(acc[r]);
+  }
+}
+
+// matvec.comp:28-41's order: one lane per row, j = 0 .. in_dim-1 sequentially
+// (fp32, from 0).  Needs in_dim % 64 == 0 and 16-byte aligned W and x: each
+// wavefront owns 64 rows and walks them in 64-column tiles, read
+// row-coalesced (8 lanes x 16 B per 128-byte row segment, next tile's loads
+// issued before this tile's products) into LDS, where each lane then reads its
+// own row (rows padded by one dword, so the 64 lanes' reads hit 64 banks).
+__global__ __launch_bounds__(256) void gemv_serial_kernel(const uint16_t* __restrict__ W,
+                                                          const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y, int out_dim,
+                                                          int in_dim) {
+  __shared__ uint32_t tile[4][64][33];
+  __shared__ float xs[4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row_base = (blockIdx.x * 4 + wave) * 64;
+  const int sub = lane & 7;   // 16-byte piece of a 128-byte row segment
+  const int rr = lane >> 3;   // rows rr, rr+8, ..., rr+56 of the tile
+  const uint16_t* src[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    src[q] = W + (size_t)min(row_base + rr + 8 * q, out_dim - 1) * in_dim + 8 * sub;
+  const int tiles = in_dim / 64;
+  uint4 v[8];
+  uint16_t xv;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] = *reinterpret_cast<const uint4*>(src[q]);
+  xv = x[lane];
+  float acc = 0.0f;
+  for (int c = 0; c < tiles; ++c) {
+    __syncthreads();  // every lane is done reading the previous tile
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      uint32_t* t = &tile[wave][rr + 8 * q][4 * sub];
+      t[0] = v[q].x;
+      t[1] = v[q].y;
+      t[2] = v[q].z;
+      t[3] = v[q].w;
+    }
+    xs[wave][lane] = spk::h2f(xv);
+    __syncthreads();
+    if (c + 1 < tiles) {  // next tile in flight while this one is summed
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = *reinterpret_cast<const uint4*>(src[q] + 64 * (c + 1));
+      xv = x[64 * (c + 1) + lane];
+    }
+#pragma unroll
+    for (int j2 = 0; j2 < 32; ++j2) {
+      const uint32_t d = tile[wave][lane][j2];
+      acc = __builtin_fmaf(spk::h2f((uint16_t)(d & 0xffffu)), xs[wave][2 * j2], acc);
+      acc = __builtin_fmaf(spk::h2f((uint16_t)(d >> 16)), xs[wave][2 * j2 + 1], acc);
+    }
+  }
+  if (row_base + lane < out_dim) y[row_base + lane] = spk::f2h(acc);
+}
+
+// The same order for any in_dim and alignment: one lane per row, fp16 loads.
+__global__ __launch_bounds__(256) void gemv_serial_generic_kernel(const uint16_t* __restrict__ W,
+                                                                  const uint16_t* __restrict__ x,
+                                                                  uint16_t* __restrict__ y,
+                                                                  int out_dim, int in_dim) {
+  const int row = blockIdx.x * 256 + threadIdx.x;
+  if (row >= out_dim) return;
+  const uint16_t* wr = W + (size_t)row * in_dim;
+  float acc = 0.0f;
+  for (int j = 0; j < in_dim; ++j) acc = __builtin_fmaf(spk::h2f(wr[j]), spk::h2f(x[j]), acc);
+  y[row] = spk::f2h(acc);
+}
+
 constexpr int kLmRows = 8;  // rows per wavefront in the lm_head stream
 
 int launch_gemv(const uint16_t* W, const uint16_t* x, uint16_t* y, int out_dim, int in_dim,
@@ -323,6 +438,36 @@ extern "C" int spk_matvec_f16(const uint16_t* W, const uint16_t* x, uint16_t* y,
   if (rc) return rc;
   if (out_dim == 0) return SPK_OK;
   return launch_gemv(W, x, y, out_dim, in_dim, spk::to_hip(stream));
+}
+
+extern "C" int spk_matvec_f16_order(const uint16_t* W, const uint16_t* x, uint16_t* y,
+                                    int32_t out_dim, int32_t in_dim, int32_t order,
+                                    spk_stream_t stream) {
+  const char* who = "spk_matvec_f16_order";
+  if (order == SPK_MATVEC_ORDER_SPANS) return spk_matvec_f16(W, x, y, out_dim, in_dim, stream);
+  if (order != SPK_MATVEC_ORDER_STRIDED && order != SPK_MATVEC_ORDER_SERIAL)
+    return spk::fail(SPK_ERR_ARG, "%s: unknown order %d", who, order);
+  if (!W || !x || !y) return spk::fail(SPK_ERR_NULL, "%s: NULL pointer", who);
+  if (out_dim < 0 || in_dim <= 0)
+    return spk::fail(SPK_ERR_SHAPE, "%s: out_dim %d in_dim %d", who, out_dim, in_dim);
+  if (out_dim == 0) return SPK_OK;
+  hipStream_t s = spk::to_hip(stream);
+  if (order == SPK_MATVEC_ORDER_STRIDED) {
+    if (out_dim >= 16384)
+      hipLaunchKernelGGL((gemv_strided_kernel<4>), dim3((out_dim + 15) / 16), dim3(256), 0, s, W, x, y,
+                         out_dim, in_dim);
+    else
+      hipLaunchKernelGGL((gemv_strided_kernel<1>), dim3((out_dim + 3) / 4), dim3(256), 0, s, W, x, y,
+                         out_dim, in_dim);
+    return spk::check_launch(who);
+  }
+  if (in_dim % 64 == 0 && spk::aligned(W, 16) && spk::aligned(x, 16))
+    hipLaunchKernelGGL(gemv_serial_kernel, dim3((out_dim + 255) / 256), dim3(256), 0, s, W, x, y, out_dim,
+                       in_dim);
+  else
+    hipLaunchKernelGGL(gemv_serial_generic_kernel, dim3((out_dim + 255) / 256), dim3(256), 0, s, W, x, y,
+                       out_dim, in_dim);
+  return spk::check_launch(who);
 }
 
 extern "C" int spk_matvec_f16_batched(const SpkMatvecDesc* d, int32_t count, spk_stream_t stream) {

@@ -228,6 +228,22 @@ def matvec_f16(W: torch.Tensor, x: torch.Tensor, y: Optional[torch.Tensor] = Non
     return y
 
 
+MATVEC_ORDERS = {"spans": 0, "strided": 1, "serial": 2}
+
+
+def matvec_f16_order(W: torch.Tensor, x: torch.Tensor, order: str,
+                     y: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """spk_matvec_f16_order: "spans" (lm_head_tiled.comp), "strided"
+    (matvec_tiled.comp) or "serial" (matvec.comp) summation order."""
+    out_dim, in_dim = W.shape
+    if y is None:
+        y = torch.empty(out_dim, dtype=torch.float16, device=W.device)
+    check(lib().spk_matvec_f16_order(_ptr(W), _ptr(x), _ptr(y), out_dim, in_dim,
+                                     MATVEC_ORDERS[order], _stream()),
+          "spk_matvec_f16_order")
+    return y
+
+
 def matvec_f16_batched(items) -> None:
     """items: sequence of (W, x, y) device tensors; one call."""
     arr = (SpkMatvecDesc * len(items))()

@@ -66,6 +66,9 @@ def _load_oracle():
                                     _p, _sz, _p, _sz, _p, _p, _p, _sz, _p, _p, _sz, _p, _sz, _p]
     lib.orc_matvec_f16.restype = _c.c_int
     lib.orc_matvec_f16.argtypes = [_p, _p, _p, _sz, _sz]
+    for name in ("orc_matvec_f16_strided", "orc_matvec_f16_serial"):
+        getattr(lib, name).restype = _c.c_int
+        getattr(lib, name).argtypes = [_p, _p, _p, _sz, _sz]
     lib.orc_argmax_f16.restype = _c.c_uint32
     lib.orc_argmax_f16.argtypes = [_p, _sz]
     lib.orc_lm_head_argmax.restype = _c.c_uint32
@@ -267,6 +270,19 @@ def matvec_f16(W, x):
     rc = lib().orc_matvec_f16(_ptr(W), _ptr(x), _ptr(y), W.shape[0], W.shape[1])
     if rc != 0:
         raise RuntimeError("in_dim must be a multiple of 64")
+    return y
+
+
+def matvec_f16_order(W, x, order):
+    """order: "spans" (orc_matvec_f16), "strided" or "serial"."""
+    if order == "spans":
+        return matvec_f16(W, x)
+    W = _u16(W)
+    x = _u16(x)
+    y = np.empty(W.shape[0], dtype=np.uint16)
+    fn = {"strided": lib().orc_matvec_f16_strided, "serial": lib().orc_matvec_f16_serial}[order]
+    if fn(_ptr(W), _ptr(x), _ptr(y), W.shape[0], W.shape[1]) != 0:
+        raise RuntimeError("in_dim must be positive")
     return y
 
 

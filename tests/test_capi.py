@@ -49,6 +49,12 @@ def test_argument_errors_without_device():
     assert lib.spk_chunk_prefill(C.byref(a), None) == -1                # out_state/workspace missing
     assert lib.spk_matvec_f16(None, None, None, 4, 64, None) == -1
     assert lib.spk_matvec_f16(1, 1, 1, 4, 63, None) == -2               # in_dim % 64
+    assert lib.spk_matvec_f16_order(1, 1, 1, 4, 63, 0, None) == -2      # spans: in_dim % 64
+    assert lib.spk_matvec_f16_order(1, 1, 1, 4, 64, 3, None) == -5      # unknown order (SPK_ERR_ARG)
+    assert b"order" in lib.spk_last_error()
+    assert lib.spk_matvec_f16_order(None, 1, 1, 4, 63, 1, None) == -1
+    assert lib.spk_matvec_f16_order(1, 1, 1, 4, 0, 2, None) == -2       # in_dim <= 0
+    assert lib.spk_matvec_f16_order(1, 1, 1, 0, 63, 1, None) == 0       # nothing to do
     assert lib.spk_argmax_f16(1, 0, 1, None) == -2
     d = _lib.SpkDecodeArgs()
     d.batch, d.num_heads = 1, 16

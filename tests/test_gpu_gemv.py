@@ -1,7 +1,8 @@
 """GPU parity of the decode GEMVs, lm_head and argmax against the oracle.
 
 Bar: bit-exact fp16 outputs and argmax indices (the oracle restates
-lm_head_tiled.comp's summation order and argmax.comp's tie rule)."""
+lm_head_tiled.comp's, matvec_tiled.comp's and matvec.comp's summation orders
+and argmax.comp's tie rule)."""
 import numpy as np
 import pytest
 import torch
@@ -23,6 +24,56 @@ def test_matvec_bitexact(dev, oracle, out_dim, in_dim):
     y = ops.matvec_f16(_t(dev, W), _t(dev, x))
     torch.cuda.synchronize()
     assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16(W, x))
+
+
+@pytest.mark.parametrize("order", ["strided", "serial", "spans"])
+@pytest.mark.parametrize("out_dim,in_dim", CHAIN[:3] + [(1024, 3584), (7, 64), (300, 192), (37, 200),
+                                                         (260, 1000), (5, 1), (40000, 512)])
+def test_matvec_order_bitexact(dev, oracle, order, out_dim, in_dim):
+    if order == "spans" and in_dim % 64:
+        pytest.skip("lm_head_tiled.comp's order needs in_dim % 64 == 0")
+    from spock_amd import ops, synth
+    W = synth.gemv_weights(out_dim, in_dim, seed=out_dim * 5 + in_dim)
+    x = synth.gemv_input(in_dim, seed=in_dim + 1)
+    y = ops.matvec_f16_order(_t(dev, W), _t(dev, x), order)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16_order(W, x, order))
+
+
+@pytest.mark.parametrize("order", ["strided", "serial"])
+def test_matvec_order_lm_head_size(dev, oracle, order):
+    from spock_amd import ops, synth
+    V, Hd = 248320, 1024
+    W = synth.gemv_weights(V, Hd, seed=41)
+    x = synth.gemv_input(Hd, seed=42)
+    y = ops.matvec_f16_order(_t(dev, W), _t(dev, x), order)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16_order(W, x, order))
+
+
+def test_matvec_order_unaligned_and_cancellation(dev, oracle):
+    """x and W 2-byte offset (the serial order's generic kernel), and rows
+    that only one summation order sums exactly."""
+    from spock_amd import ops, synth
+    from test_oracle_decode_gemv import _cancel_rows
+    W = synth.gemv_weights(70, 1024, seed=3)
+    x = synth.gemv_input(1024, seed=4)
+    Wb = torch.empty(70 * 1024 + 1, dtype=torch.float16, device=dev)
+    xb = torch.empty(1024 + 1, dtype=torch.float16, device=dev)
+    Wb[1:] = _t(dev, W.reshape(-1))
+    xb[1:] = _t(dev, x)
+    for order in ("strided", "serial"):
+        y = ops.matvec_f16_order(Wb[1:].view(70, 1024), xb[1:], order)
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16_order(W, x, order))
+    for in_dim in (256, 200, 1024):
+        rows = _cancel_rows(in_dim)
+        Wc = np.stack([w.astype(np.float16) for w in rows.values()]).view(np.uint16)
+        xc = np.full(in_dim, np.float16(1.0)).view(np.uint16)
+        for order in rows:
+            y = ops.matvec_f16_order(_t(dev, Wc), _t(dev, xc), order)
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16_order(Wc, xc, order))
 
 
 def test_matvec_batched_equals_single(dev):

@@ -2,7 +2,8 @@
   - unfused recurrence == reference GPU capture (layer 0, step 1) bit for bit;
   - beta == sigmoid(captured b) within 1 ulp of the captured fp32 bits;
   - fused step vs an fp64 restatement of the shader math;
-  - GEMV vs fp64 dot products rounded once;
+  - GEMV vs fp64 dot products rounded once, in each of the three reference
+    summation orders, and rows that only the named order sums exactly;
   - argmax vs an independent restatement of argmax.comp on crafted ties.
 """
 import numpy as np
@@ -102,6 +103,59 @@ def test_matvec_vs_fp64(oracle, out_dim, in_dim):
     y = oracle.matvec_f16(W, x)
     exact = W.view(np.float16).astype(np.float64) @ x.view(np.float16).astype(np.float64)
     assert fp16_ulp(y, exact.astype(np.float16).view(np.uint16)).max() <= 1
+
+
+@pytest.mark.parametrize("order", ["strided", "serial"])
+@pytest.mark.parametrize("out_dim,in_dim", [(64, 1024), (33, 3584), (17, 64), (9, 200), (5, 1000), (3, 1)])
+def test_matvec_orders_vs_fp64(oracle, order, out_dim, in_dim):
+    from spock_amd import synth
+    W = synth.gemv_weights(out_dim, in_dim, seed=in_dim + 3)
+    x = synth.gemv_input(in_dim, seed=out_dim + 5)
+    y = oracle.matvec_f16_order(W, x, order)
+    exact = W.view(np.float16).astype(np.float64) @ x.view(np.float16).astype(np.float64)
+    assert fp16_ulp(y, exact.astype(np.float16).view(np.uint16)).max() <= 1
+
+
+def _cancel_rows(in_dim):
+    """One row per summation order whose exact sum only that order keeps
+    (x = 1): +L and -L (L = 2048) meet first inside one of that order's
+    partial sums, so the small terms (s = 2^-14, sums exact in fp32) survive.
+    In the other orders at least one small term is added to +L or -L on its
+    own first, and s is a quarter of an fp32 ulp of 2048, so it is lost."""
+    L, s = 2048.0, 2.0 ** -14
+    sp = in_dim // 64 if in_dim % 64 == 0 else 4
+    rows = {}
+    w = np.full(in_dim, s)          # matvec_tiled: lanes 5 and 37 meet at tree stride 32
+    w[5::64] = 0.0
+    w[37::64] = 0.0
+    w[5], w[37] = L, -L
+    rows["strided"] = w
+    w = np.full(in_dim, s)          # matvec: +L, zeros, then -L opens lane 1's span
+    w[0], w[1:sp], w[sp] = L, 0.0, -L
+    rows["serial"] = w
+    if in_dim % 64 == 0 and sp >= 2:
+        w = np.full(in_dim, s)      # lm_head_tiled: both open lane 2's span; one s before them
+        w[1:2 * sp] = 0.0
+        w[2 * sp], w[2 * sp + 1] = L, -L
+        rows["spans"] = w
+    return rows
+
+
+@pytest.mark.parametrize("in_dim", [256, 200, 1024])
+def test_matvec_orders_cancellation_rows(oracle, in_dim):
+    rows = _cancel_rows(in_dim)
+    x = np.full(in_dim, np.float16(1.0)).view(np.uint16)
+    orders = [o for o in ("strided", "serial", "spans") if o != "spans" or in_dim % 64 == 0]
+    for row_order, w in rows.items():
+        exact = np.float16(w.sum())  # L - L cancels; the small terms are exact
+        assert exact != 0
+        W = w.astype(np.float16).view(np.uint16).reshape(1, in_dim)
+        for order in orders:
+            got = oracle.matvec_f16_order(W, x, order)[0]
+            if order == row_order:
+                assert got == exact.view(np.uint16), (row_order, order)
+            else:
+                assert got != exact.view(np.uint16), (row_order, order)
 
 
 def _argmax_shader(vals):
