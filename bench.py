@@ -316,9 +316,21 @@ def bench_lm_head(steps, warmup):
     lib = _lib.lib()
     wsb = ws.numel()
     nbytes = VOCAB * HIDDEN * 2
-    # the path the decode step runs: the lm_head folds every workgroup's
-    # 64-bit argmax key into 64 device words by atomic max, then a one-wave
-    # take that reduces and resets them
+    # the path the decode step runs: one launch, each workgroup posts its
+    # 64-bit argmax key to a slot and an extra last workgroup takes the argmax
+    n_slots = lib.spk_lm_head_take_slots(VOCAB)
+    slots = torch.zeros(n_slots, dtype=torch.int64, device=dev)
+    fn_one = lambda i: lib.spk_lm_head_argmax_take(Ws[i].data_ptr(), x.data_ptr(), None, VOCAB, HIDDEN, None,
+                                                   slots.data_ptr(), n_slots, out.data_ptr(), None, None, None, 0,
+                                                   _stream())
+    ms = timed_graph(fn_one, steps, warmup, rotate=2)
+    avg = ms / 1e3
+    gbs = nbytes / avg / 1e9
+    res = {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
+           "frac": round(gbs / HBM_PEAK_GBS, 4),
+           "launches": "one: per-workgroup key slots taken by an extra last workgroup"}
+    # the key + take pair (SPK_MODEL_LMHEAD_KEY_TAKE): every workgroup folds
+    # its key into 64 device words by atomic max, then a one-wave take
     key = torch.zeros(64, dtype=torch.int64, device=dev)  # SPK_ARGMAX_KEY_WORDS
 
     def fn_key(i):
@@ -328,21 +340,8 @@ def bench_lm_head(steps, warmup):
     ms = timed_graph(fn_key, steps, warmup, rotate=2)
     avg = ms / 1e3
     gbs = nbytes / avg / 1e9
-    res = {"launch_us": round(avg * 1e6, 2), "bytes_per_call": nbytes, "achieved_gbs": round(gbs, 1),
-           "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": "lm_head with atomic argmax key + take"}
-    # one launch: each workgroup posts its key to a slot, an extra last
-    # workgroup takes the argmax
-    n_slots = lib.spk_lm_head_take_slots(VOCAB)
-    slots = torch.zeros(n_slots, dtype=torch.int64, device=dev)
-    fn_one = lambda i: lib.spk_lm_head_argmax_take(Ws[i].data_ptr(), x.data_ptr(), None, VOCAB, HIDDEN, None,
-                                                   slots.data_ptr(), n_slots, out.data_ptr(), None, None, None, 0,
-                                                   _stream())
-    ms = timed_graph(fn_one, steps, warmup, rotate=2)
-    avg = ms / 1e3
-    gbs = nbytes / avg / 1e9
-    res["one_launch"] = {"launch_us": round(avg * 1e6, 2), "achieved_gbs": round(gbs, 1),
-                         "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "launches": "one: per-workgroup key slots taken by an extra last workgroup"}
+    res["key_take"] = {"launch_us": round(avg * 1e6, 2), "achieved_gbs": round(gbs, 1),
+                       "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": "lm_head with atomic argmax key + take"}
     # the two-launch form (per-workgroup partial keys, then a one-workgroup reduction)
     fn = lambda i: lib.spk_lm_head_argmax(Ws[i].data_ptr(), x.data_ptr(), VOCAB, HIDDEN, None,
                                           out.data_ptr(), ws.data_ptr(), wsb, _stream())

@@ -476,8 +476,9 @@ int spk_selftest_mfma_peak(int32_t blocks, int32_t iters, float* out, spk_stream
 /* out[i] = the XCD (XCC) that ran workgroup i of a `blocks`-workgroup launch.
  * spk_deltanet_inproj_step and spk_attention_decode_oproj hand rows from one
  * workgroup to another through the L2 they share, which holds when
- * workgroup ids are dealt to the XCDs round-robin (id mod 8 on MI355X); the
- * GPU tests check that with this call. */
+ * workgroup ids are dealt to the XCDs round-robin: (id + s) mod 8 on
+ * MI355X, where the start s continues the rotation of earlier dispatches, so
+ * ids congruent mod 8 share an XCD; the GPU tests check that with this call. */
 int spk_selftest_xcc_ids(int32_t blocks, int32_t* out, spk_stream_t stream);
 int spk_selftest_stream_read(const void* p, size_t bytes, int32_t blocks, int32_t mode, uint32_t* out,
                              spk_stream_t stream);

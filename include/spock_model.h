@@ -55,16 +55,19 @@ enum {
                                     2204-2218): events after each layer, lm_head and
                                     argmax; the step's kernels are then launched one
                                     by one, since a recorded graph holds no events */
-  SPK_MODEL_LMHEAD_ONE_LAUNCH = 16, /* final norm + lm_head + argmax in one launch
-                                    (spk_lm_head_argmax_take) instead of the key
-                                    launch then the take (spk_lm_head_argmax_key,
-                                    spk_argmax_key_take); same tokens, within
-                                    about 1 us per token of the pair */
-  SPK_MODEL_SPLIT_DN_STEP = 32      /* each DeltaNet layer's input projections and
+  SPK_MODEL_LMHEAD_ONE_LAUNCH = 16, /* accepted, no effect: the final norm +
+                                    lm_head + argmax run as one launch
+                                    (spk_lm_head_argmax_take) by default */
+  SPK_MODEL_SPLIT_DN_STEP = 32,     /* each DeltaNet layer's input projections and
                                     decode step as two launches (spk_gemv_fused,
                                     spk_deltanet_decode_step) instead of one
                                     (spk_deltanet_inproj_step); same tokens,
                                     about 19 us per token slower */
+  SPK_MODEL_LMHEAD_KEY_TAKE = 64    /* the final norm + lm_head with the atomic
+                                    argmax key, then the take, as two launches
+                                    (spk_lm_head_argmax_key, spk_argmax_key_take)
+                                    instead of one; same tokens, about 10 us per
+                                    token slower */
 };
 
 /* Opens <repack_dir>, uploads every tensor, allocates the per-layer state for

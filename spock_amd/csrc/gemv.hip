@@ -12,6 +12,7 @@
 // the 64-bit keys of argmax_key.hpp.
 #include "argmax_key.hpp"
 #include "capi_common.hpp"
+#include "dense_rows.hpp"
 #include "numerics.hpp"
 
 #include <float.h>
@@ -134,8 +135,25 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const uint16_t* __restrict
   float xf[8 * N8];
   load_x<N8>(x, lane, xf);
   const int row0 = (blockIdx.x * 4 + wave) * R;
+  // rows loaded densely and regrouped into the span order (dense_rows.hpp)
+  __shared__ uint4 rows_lds[4][64 * N8];
+  uint4 wv[R][N8];
+  spk::dense_rows_issue<N8, R, true>(W, row0, vocab, lane, wv);
+  __builtin_amdgcn_sched_barrier(0);  // every row in flight before the regroup
+  spk::dense_rows_regroup<N8, R>(wv, rows_lds[wave], lane);
   float sums[R];
-  rows_dot<N8, R, true>(W, 512 * N8, row0, vocab, xf, lane, sums);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    sums[r] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N8; ++k) {
+      float wf[8];
+      unpack8(wv[r][k], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sums[r] = __builtin_fmaf(wf[e], xf[8 * k + e], sums[r]);
+    }
+  }
+  spk::tree64_rows<R>(sums);
   unsigned long long key = 0ull;
   if (lane == 0) {
 #pragma unroll
@@ -382,7 +400,7 @@ __global__ __launch_bounds__(256) void gemv_serial_generic_kernel(const uint16_t
   y[row] = spk::f2h(acc);
 }
 
-constexpr int kLmRows = 8;  // rows per wavefront in the lm_head stream
+constexpr int kLmRows = 4;  // rows per wavefront in the lm_head stream
 
 int launch_gemv(const uint16_t* W, const uint16_t* x, uint16_t* y, int out_dim, int in_dim,
                 hipStream_t s) {

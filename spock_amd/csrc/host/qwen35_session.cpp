@@ -719,7 +719,7 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
   const int rc = guarded([&] {
     if (!repack_dir) throw std::runtime_error("spk_model_open: NULL directory");
     if (flags & ~(SPK_MODEL_NO_GRAPH | SPK_MODEL_MATRIX_PREFILL | SPK_MODEL_GPU_TIMESTAMPS | SPK_MODEL_GPU_REGIONS |
-                  SPK_MODEL_LMHEAD_ONE_LAUNCH | SPK_MODEL_SPLIT_DN_STEP))
+                  SPK_MODEL_LMHEAD_ONE_LAUNCH | SPK_MODEL_SPLIT_DN_STEP | SPK_MODEL_LMHEAD_KEY_TAKE))
       throw std::runtime_error("spk_model_open: unknown flags");
     using spock::hip::GpuTimestamps;
     const GpuTimestamps ts = (flags & SPK_MODEL_GPU_REGIONS)      ? GpuTimestamps::per_region
@@ -729,7 +729,7 @@ extern "C" SpkModel* spk_model_open(const char* repack_dir, int32_t max_seq, int
                                                          max_seq > 0 ? static_cast<std::uint32_t>(max_seq) : 0u,
                                                          (flags & SPK_MODEL_NO_GRAPH) == 0,
                                                          (flags & SPK_MODEL_MATRIX_PREFILL) == 0, ts,
-                                                         (flags & SPK_MODEL_LMHEAD_ONE_LAUNCH) != 0,
+                                                         (flags & SPK_MODEL_LMHEAD_KEY_TAKE) == 0,
                                                          (flags & SPK_MODEL_SPLIT_DN_STEP) == 0);
     m = new SpkModel{std::move(s), {}};
   });

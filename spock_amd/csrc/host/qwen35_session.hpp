@@ -72,7 +72,7 @@ class Qwen35Session {
   // holds no timing events).
   explicit Qwen35Session(const std::string& repack_dir, bool verbose = false, std::uint32_t max_seq = MAX_SEQ,
                          bool use_graph = true, bool ordered_prefill = true,
-                         GpuTimestamps gpu_timestamps = GpuTimestamps::off, bool lm_head_one_launch = false,
+                         GpuTimestamps gpu_timestamps = GpuTimestamps::off, bool lm_head_one_launch = true,
                          bool fused_dn_step = true);
   ~Qwen35Session();
   Qwen35Session(const Qwen35Session&) = delete;

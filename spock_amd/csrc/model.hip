@@ -15,6 +15,7 @@
 #include "argmax_key.hpp"
 #include "capi_common.hpp"
 #include "numerics.hpp"
+#include "dense_rows.hpp"
 #include "dn_step.hpp"
 
 #include <float.h>
@@ -22,7 +23,7 @@
 namespace {
 
 constexpr int kHidden = 1024;
-constexpr int kLmKeyRows = 8;  // vocabulary rows per wavefront of the lm_head key kernels
+constexpr int kLmKeyRows = 4;  // vocabulary rows per wavefront of the lm_head key kernels
 constexpr int kHeadDim = 256;
 constexpr int kQHeads = 8;
 constexpr int kKvHeads = 2;
@@ -1004,14 +1005,11 @@ __global__ __launch_bounds__(256) void lm_head_key_kernel(const uint16_t* __rest
 #pragma unroll
     for (int c = 0; c < PER; ++c) xv[c] = *reinterpret_cast<const uint4*>(x + 8 * min(tid + 256 * c, NV - 1));
   }
+  // rows loaded densely, regrouped into the span order after the prologue
+  // (dense_rows.hpp)
+  __shared__ uint4 rows_lds[4][64 * N8];
   uint4 wv[R][N8];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, vocab - 1);
-    const uint4* src = reinterpret_cast<const uint4*>(W + (size_t)row * in_dim + lane * (8 * N8));
-#pragma unroll
-    for (int k = 0; k < N8; ++k) wv[r][k] = ld_stream(src + k);
-  }
+  spk::dense_rows_issue<N8, R, true>(W, row0, vocab, lane, wv);
   __builtin_amdgcn_sched_barrier(0);  // every weight row in flight before the prologue
   if constexpr (NORM) {
     const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
@@ -1045,6 +1043,7 @@ __global__ __launch_bounds__(256) void lm_head_key_kernel(const uint16_t* __rest
     xf[k + 2] = t.z;
     xf[k + 3] = t.w;
   }
+  spk::dense_rows_regroup<N8, R>(wv, rows_lds[wave], lane);
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = lane_dot<N8>(wv[r], xf);

@@ -25,6 +25,7 @@ SPK_MODEL_MATRIX_PREFILL = 2
 SPK_MODEL_GPU_TIMESTAMPS = 4
 SPK_MODEL_GPU_REGIONS = 8
 SPK_MODEL_LMHEAD_ONE_LAUNCH = 16
+SPK_MODEL_LMHEAD_KEY_TAKE = 64
 SPK_MODEL_SPLIT_DN_STEP = 32
 
 
@@ -108,17 +109,17 @@ class Session:
     it in the CPU restatement's order (bit-identical).  gpu_timestamps: 0 off,
     1 GPU time per decode step, 2 also per region of the step (layer_i,
     lm_head, argmax; the step's kernels are then launched one by one).
-    lm_head_one_launch=True runs the final norm + lm_head + argmax as one
-    launch instead of the key launch then the take (same tokens).
+    lm_head_one_launch=False runs the final norm + lm_head + argmax as the key
+    launch then the take instead of one launch (same tokens).
     fused_dn_step=False runs each DeltaNet layer's input projections and
     decode step as two launches instead of one (same tokens)."""
 
     def __init__(self, repack_dir, max_seq: int = 2048, use_graph: bool = True, matrix_prefill: bool = False,
-                 gpu_timestamps: int = 0, lm_head_one_launch: bool = False, fused_dn_step: bool = True):
+                 gpu_timestamps: int = 0, lm_head_one_launch: bool = True, fused_dn_step: bool = True):
         if gpu_timestamps not in (0, 1, 2):
             raise ModelError(f"gpu_timestamps must be 0, 1 or 2, got {gpu_timestamps}")
         flags = (0 if use_graph else SPK_MODEL_NO_GRAPH) | (SPK_MODEL_MATRIX_PREFILL if matrix_prefill else 0)
-        flags |= SPK_MODEL_LMHEAD_ONE_LAUNCH if lm_head_one_launch else 0
+        flags |= 0 if lm_head_one_launch else SPK_MODEL_LMHEAD_KEY_TAKE
         flags |= 0 if fused_dn_step else SPK_MODEL_SPLIT_DN_STEP
         flags |= (0, SPK_MODEL_GPU_TIMESTAMPS, SPK_MODEL_GPU_REGIONS)[gpu_timestamps]
         self._h = lib().spk_model_open(str(repack_dir).encode(), max_seq, flags)

@@ -179,14 +179,18 @@ def test_deltanet_inproj_step_equals_the_two_calls(dev, with_token):
 def test_workgroups_are_dealt_to_xcds_round_robin(dev):
     """The fused DeltaNet launch and the attention combine hand rows between
     workgroups whose ids are congruent mod 8 through the L2 of their XCD:
-    the dispatch must deal workgroup ids to the 8 XCDs round-robin."""
+    the dispatch must deal workgroup ids to the 8 XCDs round-robin.  The
+    first workgroup's XCD continues the rotation of earlier dispatches (seen
+    at 0 and at 6), so the check is (id + start) mod 8, over several
+    launches of different sizes."""
     from spock_amd import _lib
-    n = 4096
-    out = torch.full((n,), -1, dtype=torch.int32, device=dev)
-    _lib.check(_lib.lib().spk_selftest_xcc_ids(n, out.data_ptr(), _stream()), "xcc ids")
-    torch.cuda.synchronize()
-    ids = out.cpu().numpy()
-    assert np.array_equal(ids, np.arange(n) % 8), np.unique(ids)
+    for n in (4096, 4093, 37, 4096):
+        out = torch.full((n,), -1, dtype=torch.int32, device=dev)
+        _lib.check(_lib.lib().spk_selftest_xcc_ids(n, out.data_ptr(), _stream()), "xcc ids")
+        torch.cuda.synchronize()
+        ids = out.cpu().numpy()
+        assert 0 <= ids[0] < 8, ids[0]
+        assert np.array_equal(ids, (np.arange(n) + ids[0]) % 8), (n, np.unique(ids))
 
 
 def test_deltanet_inproj_step_rejects_bad_args(dev):

@@ -31,13 +31,13 @@ def _prompt(n, seed=5):
     return (synth.splitmix64(seed, n) % np.uint64(VOCAB)).astype(np.int32)
 
 
-@pytest.mark.parametrize("use_graph,one_launch,fused", [(True, False, False), (False, False, False),
-                                                        (True, True, False), (True, False, True),
-                                                        (False, False, True)])
+@pytest.mark.parametrize("use_graph,one_launch,fused", [(True, True, True), (False, True, True),
+                                                        (True, False, True), (True, True, False),
+                                                        (False, False, False)])
 def test_decode_from_oracle_state_bitexact(dev, small_artifact, use_graph, one_launch, fused):
-    """one_launch: the final norm + lm_head + argmax as one launch instead of
-    the default key launch then take.  fused: each DeltaNet layer's input
-    projections and decode step in one launch."""
+    """one_launch=False: the final norm + lm_head with the atomic key, then
+    the take, instead of the default single launch.  fused=False: each
+    DeltaNet layer's input projections and decode step as two launches."""
     import oracle_model
     from spock_amd import model
     print(f"[session decode graph={use_graph} lm_head one_launch={one_launch} fused={fused}]", flush=True)
