@@ -484,11 +484,12 @@ void Qwen35Session::enqueue_decode_step() {
 }
 
 // Final norm, lm_head and argmax of hidden row h; the token goes to *tok and
-// is recorded in the history (count, position).  The key launch then the take
-// by default, else one launch (spk_lm_head_argmax_take; measured on one box,
-// config 4: 679.7-680.5 vs 678.4-678.9 us per token for the pair, lm_head
-// alone 83.8 vs 83.1 us); with region marks, "lm_head" ends after the first
-// launch and "argmax" after the take (empty in the one-launch form).
+// is recorded in the history (count, position).  One launch by default
+// (spk_lm_head_argmax_take: per-workgroup key slots, taken by an extra last
+// workgroup; config 4 measured 651 vs 660 us per token for the key launch then
+// the take, same build and box), else the pair; with region marks, "lm_head"
+// ends after the first launch and "argmax" after the take (in the one-launch
+// form the two marks are back to back, so "argmax" is the marks' own gap).
 void Qwen35Session::lm_head_token(const std::uint16_t* h, std::uint32_t* tok, bool marks) {
   const int32_t vocab = static_cast<int32_t>(shape_.vocab);
   std::int32_t* hist = history_.get<std::int32_t>();
