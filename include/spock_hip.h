@@ -220,7 +220,7 @@ int spk_lm_head_argmax(const uint16_t* W, const uint16_t* x, int32_t vocab, int3
  * reference: for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * per-workgroup partial keys live in a static device array of
- * SPK_LM_HEAD_NOALLOC_MAX_VOCAB / 32 keys (64 KiB), one copy per device held
+ * SPK_LM_HEAD_NOALLOC_MAX_VOCAB / 16 keys (128 KiB), one copy per device held
  * until the process ends; the call allocates nothing.  vocab above
  * SPK_LM_HEAD_NOALLOC_MAX_VOCAB is rejected with SPK_ERR_SHAPE.  Calls that
  * overlap on one device (concurrent streams or threads) race on that array:
