@@ -107,6 +107,45 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   }
 }
 
+// Matrices of hundreds of MB (the lm_head class): 4 rows per wavefront read
+// with dense non-temporal loads and regrouped into the span order
+// (dense_rows.hpp); the same sums as gemv_kernel.
+constexpr size_t kStreamBytes = size_t(128) << 20;
+template <int N8>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(const uint16_t* __restrict__ W,
+                                                          const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y, int out_dim) {
+  constexpr int R = 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float xf[8 * N8];
+  load_x<N8>(x, lane, xf);
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  __shared__ uint4 rows_lds[4][64 * N8];
+  uint4 wv[R][N8];
+  spk::dense_rows_issue<N8, R, true>(W, row0, out_dim, lane, wv);
+  __builtin_amdgcn_sched_barrier(0);  // every row in flight before the regroup
+  spk::dense_rows_regroup<N8, R>(wv, rows_lds[wave], lane);
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc[r] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N8; ++k) {
+      float wf[8];
+      unpack8(wv[r][k], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[r] = __builtin_fmaf(wf[e], xf[8 * k + e], acc[r]);
+    }
+  }
+  spk::tree64_rows<R>(acc);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (row0 + r < out_dim) y[row0 + r] = spk::f2h(acc[r]);
+  }
+}
+
 // Any in_dim % 64 == 0: scalar loads, same order.
 __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint16_t* __restrict__ W,
                                                            const uint16_t* __restrict__ x,
@@ -291,7 +330,7 @@ __global__ __launch_bounds__(256) void gemv_batched_kernel(GemvBatch b) {
 // reads 64 consecutive fp16 of a row (128 coalesced bytes), U steps of every
 // row in flight before the first is used.  Past in_dim a lane's index is
 // clamped and its product not added.
-template <int R>
+template <int R, bool NT>
 __global__ __launch_bounds__(256) void gemv_strided_kernel(const uint16_t* __restrict__ W,
                                                            const uint16_t* __restrict__ x,
                                                            uint16_t* __restrict__ y, int out_dim,
@@ -311,7 +350,10 @@ __global__ __launch_bounds__(256) void gemv_strided_kernel(const uint16_t* __res
       const int j = min(lane + 64 * (i0 + u), in_dim - 1);
       xv[u] = x[j];
 #pragma unroll
-      for (int r = 0; r < R; ++r) wv[r][u] = W[(size_t)min(row0 + r, out_dim - 1) * in_dim + j];
+      for (int r = 0; r < R; ++r) {
+        const uint16_t* p = W + (size_t)min(row0 + r, out_dim - 1) * in_dim + j;
+        wv[r][u] = NT ? __builtin_nontemporal_load(p) : *p;
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -338,6 +380,7 @@ __global__ __launch_bounds__(256) void gemv_strided_kernel(const uint16_t* __res
 // row-coalesced (8 lanes x 16 B per 128-byte row segment, next tile's loads
 // issued before this tile's products) into LDS, where each lane then reads its
 // own row (rows padded by one dword, so the 64 lanes' reads hit 64 banks).
+template <bool NT>
 __global__ __launch_bounds__(256) void gemv_serial_kernel(const uint16_t* __restrict__ W,
                                                           const uint16_t* __restrict__ x,
                                                           uint16_t* __restrict__ y, int out_dim,
@@ -357,7 +400,7 @@ __global__ __launch_bounds__(256) void gemv_serial_kernel(const uint16_t* __rest
   uint4 v[8];
   uint16_t xv;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) v[q] = *reinterpret_cast<const uint4*>(src[q]);
+  for (int q = 0; q < 8; ++q) v[q] = spk::dense_ld<NT>(reinterpret_cast<const uint4*>(src[q]));
   xv = x[lane];
   float acc = 0.0f;
   for (int c = 0; c < tiles; ++c) {
@@ -374,7 +417,7 @@ __global__ __launch_bounds__(256) void gemv_serial_kernel(const uint16_t* __rest
     __syncthreads();
     if (c + 1 < tiles) {  // next tile in flight while this one is summed
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = *reinterpret_cast<const uint4*>(src[q] + 64 * (c + 1));
+      for (int q = 0; q < 8; ++q) v[q] = spk::dense_ld<NT>(reinterpret_cast<const uint4*>(src[q] + 64 * (c + 1)));
       xv = x[64 * (c + 1) + lane];
     }
 #pragma unroll
@@ -410,6 +453,23 @@ int launch_gemv(const uint16_t* W, const uint16_t* x, uint16_t* y, int out_dim, 
     hipLaunchKernelGGL(gemv_generic_kernel, dim3((out_dim + 3) / 4), dim3(256), 0, s, W, x, y,
                        out_dim, in_dim);
     return spk::check_launch("spk_matvec_f16 (generic)");
+  }
+  if ((size_t)out_dim * (size_t)in_dim * 2 >= kStreamBytes) {
+    const dim3 g((out_dim + 15) / 16);
+    switch (in_dim / 512) {
+#define SPK_GEMV_STREAM_CASE(n8) \
+  case n8: hipLaunchKernelGGL((gemv_stream_kernel<n8>), g, dim3(256), 0, s, W, x, y, out_dim); break;
+      SPK_GEMV_STREAM_CASE(1)
+      SPK_GEMV_STREAM_CASE(2)
+      SPK_GEMV_STREAM_CASE(3)
+      SPK_GEMV_STREAM_CASE(4)
+      SPK_GEMV_STREAM_CASE(5)
+      SPK_GEMV_STREAM_CASE(6)
+      SPK_GEMV_STREAM_CASE(7)
+      default: hipLaunchKernelGGL((gemv_stream_kernel<8>), g, dim3(256), 0, s, W, x, y, out_dim); break;
+#undef SPK_GEMV_STREAM_CASE
+    }
+    return spk::check_launch("spk_matvec_f16 (stream)");
   }
   // Rows per wave: enough workgroups to cover the chip for small outputs,
   // more bytes in flight per lane for large ones.
@@ -471,17 +531,24 @@ extern "C" int spk_matvec_f16_order(const uint16_t* W, const uint16_t* x, uint16
   if (out_dim == 0) return SPK_OK;
   hipStream_t s = spk::to_hip(stream);
   if (order == SPK_MATVEC_ORDER_STRIDED) {
-    if (out_dim >= 16384)
-      hipLaunchKernelGGL((gemv_strided_kernel<4>), dim3((out_dim + 15) / 16), dim3(256), 0, s, W, x, y,
+    if ((size_t)out_dim * (size_t)in_dim * 2 >= kStreamBytes)
+      hipLaunchKernelGGL((gemv_strided_kernel<4, true>), dim3((out_dim + 15) / 16), dim3(256), 0, s, W, x, y,
+                         out_dim, in_dim);
+    else if (out_dim >= 16384)
+      hipLaunchKernelGGL((gemv_strided_kernel<4, false>), dim3((out_dim + 15) / 16), dim3(256), 0, s, W, x, y,
                          out_dim, in_dim);
     else
-      hipLaunchKernelGGL((gemv_strided_kernel<1>), dim3((out_dim + 3) / 4), dim3(256), 0, s, W, x, y,
+      hipLaunchKernelGGL((gemv_strided_kernel<1, false>), dim3((out_dim + 3) / 4), dim3(256), 0, s, W, x, y,
                          out_dim, in_dim);
     return spk::check_launch(who);
   }
-  if (in_dim % 64 == 0 && spk::aligned(W, 16) && spk::aligned(x, 16))
-    hipLaunchKernelGGL(gemv_serial_kernel, dim3((out_dim + 255) / 256), dim3(256), 0, s, W, x, y, out_dim,
-                       in_dim);
+  if (in_dim % 64 == 0 && spk::aligned(W, 16) && spk::aligned(x, 16) &&
+      (size_t)out_dim * (size_t)in_dim * 2 >= kStreamBytes)
+    hipLaunchKernelGGL(gemv_serial_kernel<true>, dim3((out_dim + 255) / 256), dim3(256), 0, s, W, x, y,
+                       out_dim, in_dim);
+  else if (in_dim % 64 == 0 && spk::aligned(W, 16) && spk::aligned(x, 16))
+    hipLaunchKernelGGL(gemv_serial_kernel<false>, dim3((out_dim + 255) / 256), dim3(256), 0, s, W, x, y,
+                       out_dim, in_dim);
   else
     hipLaunchKernelGGL(gemv_serial_generic_kernel, dim3((out_dim + 255) / 256), dim3(256), 0, s, W, x, y,
                        out_dim, in_dim);

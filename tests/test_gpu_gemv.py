@@ -40,8 +40,10 @@ def test_matvec_order_bitexact(dev, oracle, order, out_dim, in_dim):
     assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16_order(W, x, order))
 
 
-@pytest.mark.parametrize("order", ["strided", "serial"])
+@pytest.mark.parametrize("order", ["strided", "serial", "spans"])
 def test_matvec_order_lm_head_size(dev, oracle, order):
+    """508.6 MB: above 128 MB the spans and strided orders stream their rows
+    with non-temporal loads (spans: dense loads regrouped through LDS)."""
     from spock_amd import ops, synth
     V, Hd = 248320, 1024
     W = synth.gemv_weights(V, Hd, seed=41)
