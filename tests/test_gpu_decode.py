@@ -28,9 +28,11 @@ def _u16(t):
     return t.cpu().numpy().view(np.uint16)
 
 
-# workgroup shape (decode_waves, 16 heads): 16 wavefronts up to 256
-# workgroups (B <= 16), 8 up to 512 (B <= 32), then 4; the batches on both
-# sides of each switch are included
+# launch shape (decode_shape, 16 heads): 16 wavefronts up to 256 workgroups
+# (B <= 16), then 4; non-temporal state loads from 256 workgroups (B >= 16);
+# the batches on both sides of each switch are included (SPK_DECODE_WAVES
+# forces 4, 8 or 16 wavefronts for measurement; the GPU runs of this file
+# under each passed bit-exact)
 @pytest.mark.parametrize("B", [1, 3, 4, 5, 16, 17, 32, 33, 64, 100, 256])
 def test_fused_decode_step_bitexact(dev, oracle, B):
     from spock_amd import ops, synth
