@@ -477,10 +477,14 @@ __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
   // RoPE pairs, the new K/V row when this block holds the current position,
   // then K/V of position 64b + tid/4 (quarter tid%4: 64 dims of K and of V;
   // rows past the current position read row 0 and stage zeros).
-  float qv[4], qw[4], c8[8];
+  float qv[4], qw[4], c8[8], gv[4];
   load4h(a.qg + (size_t)t * 4096 + qh * 512 + 4 * lane, qv);
   load4h(a.q_norm_w + 4 * lane, qw);
   load_rope(cs, lane, c8);
+  // the output gate of this wave's query head, for the combine (read here
+  // with the first operands, so the last workgroup's combine waits on no
+  // load of its own after the partials)
+  if constexpr (COMBINE) load4h(a.qg + qh * 512 + 256 + 4 * lane, gv);
   // the new K/V row is read by every wave (a few hundred bytes) so that no
   // load sits under a branch; only the block holding the position uses it
   const bool newrow = cur >= 0 && wave == 0;
@@ -596,11 +600,9 @@ __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
       }
     }
     const float inv = 1.0f / (tot + 1e-30f);
-    float g[4];
-    load4h(a.qg + qh * 512 + 256 + 4 * lane, g);
     uint16_t r[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = spk::f2h(round16(o[e] * inv) * (1.0f / (1.0f + spk::expf_det(-g[e]))));
+    for (int e = 0; e < 4; ++e) r[e] = spk::f2h(round16(o[e] * inv) * (1.0f / (1.0f + spk::expf_det(-gv[e]))));
     *reinterpret_cast<uint2*>(a.out + qh * kHeadDim + 4 * lane) =
         make_uint2((uint32_t)r[0] | ((uint32_t)r[1] << 16), (uint32_t)r[2] | ((uint32_t)r[3] << 16));
   }
