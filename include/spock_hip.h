@@ -314,6 +314,16 @@ typedef struct SpkAttnArgs {
 
 /* Workspace bytes for `tokens` queries over positions [0, positions). */
 size_t spk_attention_workspace_size(int32_t positions, int32_t tokens);
+/* The attention layer's projections (spk_gemv_fused with the RMSNorm input
+ * and outs = {q|gate [4096], k [512], v [512]}, vk_session.cpp:2606-2675)
+ * for a session that runs spk_attention_decode(_oproj) right after: the
+ * launch also reads the layer's cached K/V rows 0 .. *attn->pos_dev (at most
+ * attn->max_seq; up to 2.5 MiB) and drops them, so that the attention launch
+ * finds them in the caches instead of at HBM latency.  attn->qg/k/v must be
+ * the three outputs; attn->kv_cache and pos_dev are read, nothing of attn is
+ * written.  Same outputs, bit for bit, as spk_gemv_fused. */
+int spk_attention_inproj(const SpkGemvInput* in, const SpkGemvOutput* outs, const SpkAttnArgs* attn,
+                         spk_stream_t stream);
 /* One token at position *pos_dev (< max_seq; read on the device, so the call
  * can be recorded once and replayed); workspace for (max_seq, 1). */
 int spk_attention_decode(const SpkAttnArgs* args, spk_stream_t stream);

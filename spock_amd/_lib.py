@@ -61,6 +61,7 @@ SIGNATURES = {
     "spk_deltanet_norm_gate": (C.c_int, [_p, _i64, _p, _i64, _p, _f32, _i32, _p, _i64, _p]),
     "spk_deltanet_norm_gate_f16": (C.c_int, [_p, _p, _p, _i32, _i32, _f32, _p]),
     "spk_deltanet_inproj_step": (C.c_int, [_p, _p, _p, _p, _p]),
+    "spk_attention_inproj": (C.c_int, [_p, _p, _p, _p]),
     "spk_matvec_f16_rows": (C.c_int, [_p, _p, _i64, _p, _i64, _p, _i32, _i32, _i32, _p]),
     "spk_chunk_prefill_ordered_workspace_size": (_sz, [_i32, _i32]),
     "spk_chunk_prefill_ordered": (C.c_int, [_p, _p]),

@@ -444,7 +444,6 @@ void Qwen35Session::enqueue_decode_step() {
       const SpkGemvOutput outs[3] = {{w.attn_q, qg_.get<std::uint16_t>(), nullptr, 4096, nullptr},
                                      {w.attn_k, k_.get<std::uint16_t>(), nullptr, 512, nullptr},
                                      {w.attn_v, v_.get<std::uint16_t>(), nullptr, 512, nullptr}};
-      spk_check(spk_gemv_fused(&in, outs, 3, S(stream_)), "attention projections");
       SpkAttnArgs aa{};
       aa.qg = qg_.get<std::uint16_t>();
       aa.k = k_.get<std::uint16_t>();
@@ -458,8 +457,11 @@ void Qwen35Session::enqueue_decode_step() {
       aa.out = attn_out_.get<std::uint16_t>();
       aa.workspace = attn_ws_.get();
       aa.workspace_bytes = attn_ws_.bytes();
-      // attention blocks, then o_proj + residual with the blocks' combine and
-      // sigmoid gate in its prologue
+      // the projections, reading the layer's cached K/V rows into the caches
+      // for the attention launch (about 0.5 us off its K/V staging)
+      spk_check(spk_attention_inproj(&in, outs, &aa, S(stream_)), "attention projections");
+      // attention blocks (the last block workgroup of each KV head combines
+      // the blocks and applies the sigmoid gate), then o_proj + residual
       const SpkGemvOutput oo{w.attn_o, h, h, static_cast<int32_t>(H), nullptr};
       spk_check(spk_attention_decode_oproj(&aa, &oo, S(stream_)), "attention decode + o_proj");
     }

@@ -100,6 +100,12 @@ struct FusedGemv {
   const uint16_t* res[kLaunchOut];
   int out_dim[kLaunchOut];
   int first_block[kLaunchOut + 1];
+  // the TOUCH form only (spk_attention_inproj): K/V cache rows 0 .. *touch_pos
+  // (at most touch_rows) read and dropped, so that the attention launch that
+  // follows finds them in the caches (spk_attention_inproj)
+  const uint16_t* touch;
+  const int32_t* touch_pos;
+  int touch_rows;
 };
 
 template <int N8, int R>
@@ -131,7 +137,7 @@ __device__ __forceinline__ float lane_dot(const uint4 (&wr)[N8], const float* xf
 // KIND is the input kind (compile time, so the input and weight loads sit in
 // one straight-line block: the input operands are issued first and the
 // prologue waits for them alone while the weight rows are in flight).
-template <int N8, int R, bool PAIR, int KIND>
+template <int N8, int R, bool PAIR, int KIND, bool TOUCH = false>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   __shared__ float xs[kMaxIn];
   __shared__ float red[257];
@@ -162,6 +168,15 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   constexpr int NV = in_dim / 8;  // 16-byte pieces of x
   constexpr int PER = (NV + 255) / 256;
   static_assert(256 * PER * 8 <= kMaxIn, "x staging overruns xs");
+  // K/V rows for the next launch: 16 bytes per thread over the grid, issued
+  // first (the position's load, then the rows) and waited for only at the end
+  uint4 tv = make_uint4(0, 0, 0, 0);
+  if (TOUCH) {
+    const int rows = min(a.touch_pos[0] + 1, a.touch_rows);
+    const size_t toff = ((size_t)blockIdx.x * 256 + tid) * 16;
+    if (toff < (size_t)max(rows, 0) * (kKvRow * 2))
+      tv = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(a.touch) + toff);
+  }
   uint2 hv = make_uint2(0, 0), nwv = make_uint2(0, 0);
   uint4 xv[PER], uv[PER];
   if constexpr (KIND == SPK_GEMV_IN_RMSNORM) {  // in_dim == 1024: 4 elements per thread
@@ -254,6 +269,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv a) {
   // the first layer's input row (token embedding) becomes the residual stream
   if constexpr (KIND == SPK_GEMV_IN_RMSNORM)
     if (a.h_out && blockIdx.x == 0) *reinterpret_cast<uint2*>(a.h_out + 4 * tid) = hv;
+  if constexpr (TOUCH) asm volatile("" ::"v"(tv.x));  // keeps the touch loads
 }
 
 // ---------------------------------------------------------------------------
@@ -1276,8 +1292,12 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
 // One launch of up to kLaunchOut outputs of spk_gemv_fused (validated by the
 // caller); only the first launch of a call writes h_out.
 static int launch_fused_gemv(const SpkGemvInput* in, const SpkGemvOutput* outs, int count, bool first, int n8, int R,
-                             spk_stream_t stream) {
+                             spk_stream_t stream, const uint16_t* touch = nullptr, const int32_t* touch_pos = nullptr,
+                             int touch_rows = 0) {
   FusedGemv a;
+  a.touch = touch;
+  a.touch_pos = touch_pos;
+  a.touch_rows = touch_rows;
   a.kind = in->kind;
   a.in_dim = in->in_dim;
   a.x = in->x;
@@ -1317,7 +1337,11 @@ static int launch_fused_gemv(const SpkGemvInput* in, const SpkGemvOutput* outs, 
     }                                                                                                   \
     break;
   if (in->kind == SPK_GEMV_IN_RMSNORM) {  // in_dim == kHidden (checked above)
-    SPK_FGK(2, 2, SPK_GEMV_IN_RMSNORM)
+    if (touch)
+      hipLaunchKernelGGL((fused_gemv_kernel<2, 2, false, SPK_GEMV_IN_RMSNORM, true>), dim3(blocks), dim3(256), 0, s, a);
+    else {
+      SPK_FGK(2, 2, SPK_GEMV_IN_RMSNORM)
+    }
     return spk::check_launch("spk_gemv_fused");
   }
   switch (n8) {
@@ -1336,8 +1360,8 @@ static int launch_fused_gemv(const SpkGemvInput* in, const SpkGemvOutput* outs, 
   return spk::check_launch("spk_gemv_fused");
 }
 
-extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count,
-                              spk_stream_t stream) {
+// spk_gemv_fused's argument contract (its messages name it).
+static int gemv_fused_check(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count) {
   if (!in || (count > 0 && !outs)) return spk::fail(SPK_ERR_NULL, "spk_gemv_fused: NULL argument");
   if (count < 1 || count > kMaxOut) return spk::fail(SPK_ERR_ARG, "spk_gemv_fused: count %d (1..%d)", count, kMaxOut);
   const int in_dim = in->in_dim;
@@ -1368,6 +1392,13 @@ extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs,
     if (o.W_up && !spk::aligned(o.W_up, 16))
       return spk::fail(SPK_ERR_ALIGN, "spk_gemv_fused: W_up %d must be 16-byte aligned", i);
   }
+  return SPK_OK;
+}
+
+extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs, int32_t count,
+                              spk_stream_t stream) {
+  if (int rc = gemv_fused_check(in, outs, count)) return rc;
+  const int in_dim = in->in_dim;
   const int n8 = in_dim / 512;
   const int R = n8 <= 2 ? 2 : 1;
   for (int c0 = 0; c0 < count; c0 += kLaunchOut) {
@@ -1375,6 +1406,28 @@ extern "C" int spk_gemv_fused(const SpkGemvInput* in, const SpkGemvOutput* outs,
     if (rc) return rc;
   }
   return SPK_OK;
+}
+
+extern "C" int spk_attention_inproj(const SpkGemvInput* in, const SpkGemvOutput* outs, const SpkAttnArgs* attn,
+                                    spk_stream_t stream) {
+  const char* name = "spk_attention_inproj";
+  if (!in || !outs || !attn) return spk::fail(SPK_ERR_NULL, "%s: NULL argument", name);
+  if (in->kind != SPK_GEMV_IN_RMSNORM)
+    return spk::fail(SPK_ERR_ARG, "%s: the input must be the RMSNorm kind", name);
+  if (!attn->kv_cache || !attn->pos_dev) return spk::fail(SPK_ERR_NULL, "%s: kv_cache/pos_dev NULL", name);
+  if (attn->max_seq <= 0) return spk::fail(SPK_ERR_SHAPE, "%s: max_seq %d", name, attn->max_seq);
+  if (!spk::aligned(attn->kv_cache, 16)) return spk::fail(SPK_ERR_ALIGN, "%s: kv_cache must be 16-byte aligned", name);
+  static const int dims[3] = {4096, 512, 512};
+  for (int i = 0; i < 3; ++i) {
+    if (!outs[i].W || !outs[i].y) return spk::fail(SPK_ERR_NULL, "%s: output %d NULL", name, i);
+    if (outs[i].out_dim != dims[i] || outs[i].residual || outs[i].W_up)
+      return spk::fail(SPK_ERR_SHAPE, "%s: output %d must be a plain %d-row projection", name, i, dims[i]);
+  }
+  if (attn->qg != outs[0].y || attn->k != outs[1].y || attn->v != outs[2].y)
+    return spk::fail(SPK_ERR_ARG, "%s: the attention's qg/k/v must be the projections' outputs", name);
+  // the rest of the projections' contract is spk_gemv_fused's
+  if (int rc = gemv_fused_check(in, outs, 3)) return rc;
+  return launch_fused_gemv(in, outs, 3, true, 2, 2, stream, attn->kv_cache, attn->pos_dev, attn->max_seq);
 }
 
 extern "C" int spk_deltanet_inproj_step(const SpkGemvInput* in, const SpkGemvOutput* outs, const SpkDecodeArgs* d,

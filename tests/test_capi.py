@@ -65,6 +65,21 @@ def test_argument_errors_without_device():
     assert lib.spk_deltanet_norm_gate_f16(1, 1, 1, 16, 64, 1e-6, None) == -2      # head_dim != 128
     assert lib.spk_deltanet_norm_gate_f16(1, 1, 1, 0, 128, 1e-6, None) == -2      # no heads
     assert lib.spk_deltanet_inproj_step(None, None, None, None, None) == -1
+    gi = _lib.SpkGemvInput()
+    gi.kind, gi.in_dim, gi.x, gi.x2 = _lib.SPK_GEMV_IN_PLAIN, 1024, 16, 16
+    outs = (_lib.SpkGemvOutput * 3)()
+    for o, n, y in zip(outs, (4096, 512, 512), (4096, 8192, 12288)):
+        o.W, o.y, o.out_dim = 16, y, n
+    aa = _lib.SpkAttnArgs()
+    assert lib.spk_attention_inproj(None, outs, C.byref(aa), None) == -1
+    assert lib.spk_attention_inproj(C.byref(gi), outs, C.byref(aa), None) == -5   # not the RMSNorm kind
+    gi.kind = _lib.SPK_GEMV_IN_RMSNORM
+    assert lib.spk_attention_inproj(C.byref(gi), outs, C.byref(aa), None) == -1   # kv_cache/pos_dev missing
+    aa.kv_cache, aa.pos_dev, aa.max_seq = 256, 256, 2048
+    assert lib.spk_attention_inproj(C.byref(gi), outs, C.byref(aa), None) == -5   # qg/k/v are not the outputs
+    aa.qg, aa.k, aa.v = 4096, 8192, 12288
+    outs[1].out_dim = 256
+    assert lib.spk_attention_inproj(C.byref(gi), outs, C.byref(aa), None) == -2   # k rows != 512
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -277,6 +277,39 @@ def _attn_args(dev, rope, kv, qg, k, v, qn, kn, max_seq, T, positions):
     return a, d
 
 
+@pytest.mark.parametrize("pos", [0, 70, 511, 700])
+def test_attention_inproj_equals_gemv_fused(dev, pos):
+    """spk_attention_inproj: the same q|gate, k, v as spk_gemv_fused; the K/V
+    rows it reads ahead (0..pos, clamped to max_seq) are left unchanged."""
+    from spock_amd import _lib
+    print(f"[attention inproj pos={pos}]", flush=True)
+    max_seq = 512
+    h = _rand16(40, 1024)
+    w = _rand16(41, 1024, 0.02)
+    Ws = [_rand16(42 + i, n * 1024, 0.02).reshape(n, 1024) for i, n in enumerate((4096, 512, 512))]
+    kv = _rand16(45, max_seq * 1024)
+    dh, dw, dkv = _h(h, dev), _h(w, dev), _h(kv, dev)
+    dWs = [_h(W, dev) for W in Ws]
+    ref = [torch.empty(n, dtype=torch.float16, device=dev) for n in (4096, 512, 512)]
+    got = [torch.full((n,), float("nan"), dtype=torch.float16, device=dev) for n in (4096, 512, 512)]
+    gi = _lib.SpkGemvInput()
+    gi.kind, gi.in_dim, gi.x, gi.x2 = _lib.SPK_GEMV_IN_RMSNORM, 1024, dh.data_ptr(), dw.data_ptr()
+    _gemv(gi, [(W.data_ptr(), y.data_ptr(), None, n) for W, y, n in zip(dWs, ref, (4096, 512, 512))])
+    outs = (_lib.SpkGemvOutput * 3)()
+    for o, W, y, n in zip(outs, dWs, got, (4096, 512, 512)):
+        o.W, o.y, o.out_dim = W.data_ptr(), y.data_ptr(), n
+    aa = _lib.SpkAttnArgs()
+    aa.qg, aa.k, aa.v = got[0].data_ptr(), got[1].data_ptr(), got[2].data_ptr()
+    dpos = torch.tensor([pos], dtype=torch.int32, device=dev)
+    aa.kv_cache, aa.max_seq, aa.pos_dev = dkv.data_ptr(), max_seq, dpos.data_ptr()
+    for _ in range(2):
+        _lib.check(_lib.lib().spk_attention_inproj(C.byref(gi), outs, C.byref(aa), _stream()), "spk_attention_inproj")
+    torch.cuda.synchronize()
+    for r, g in zip(ref, got):
+        assert torch.equal(r, g)
+    assert np.array_equal(_u16(dkv), kv)
+
+
 @pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 511])
 def test_attention_decode_bitexact(dev, pos):
     from spock_amd import _lib
