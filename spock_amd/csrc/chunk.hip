@@ -285,11 +285,19 @@ template <> struct RowStage<float> {
 
 // L is block lower triangular: its 10 blocks (I >= J) of 16x16 are stored
 // packed, block (I,J) at (I(I+1)/2 + J) * 256, row-major with stride 16.  T =
-// (I + L)^{-1} has the same shape; its diagonal blocks overwrite L's once those
-// are solved (nothing reads them afterwards) and its 6 off-diagonal blocks
-// (I > J) have a buffer of their own.
+// (I + L)^{-1} has the same shape.  Its diagonal blocks and its column-0
+// blocks overwrite L's: L_II once solved, and L_I0 when T_I0 is formed, by the
+// wavefront that is the last to read L_I0 (T_I0 is the last block of row I
+// to be formed, by distance).  T_21, T_31 and T_32 go to a 3-block buffer of
+// their own, since L_21, L_31 and L_32 are read again for T_20 and T_30.
+// (With all six off-diagonal blocks in a buffer, the intra kernel held 34.3
+// KB of LDS: 4 workgroups per CU instead of 5.)
 __device__ __forceinline__ int blk(int I, int J) { return (I * (I + 1) / 2 + J) * 256; }
-__device__ __forceinline__ int offblk(int I, int J) { return ((I - 1) * I / 2 + J) * 256; }
+__device__ __forceinline__ int tslot(int I, int J) { return (I == 2 ? 0 : J) * 256; }  // (2,1), (3,1), (3,2)
+// T's block (I, J), I >= J, once formed
+__device__ __forceinline__ const float* tblk(const float* sL, const float* sT, int I, int J) {
+  return (I == J || J == 0) ? sL + blk(I, J) : sT + tslot(I, J);
+}
 
 constexpr float kLog2e = 1.44269504f;
 
@@ -445,7 +453,7 @@ __device__ __forceinline__ void at_store(const f4v (&acc)[5], const float* sL, c
       f4v x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int J = K; J <= QB; ++J) {
-        const float* tb = (J == K) ? sL + blk(K, K) : sT + offblk(J, K);
+        const float* tb = tblk(sL, sT, J, K);
 #pragma unroll
         for (int e = 0; e < 4; ++e) x = mfma4(tb[(4 * lg + e) * 16 + li], acc[nK + J][e], x);
       }
@@ -562,12 +570,12 @@ __device__ __forceinline__ void gram_dispatch(int part, int wave, const F& f) {
 // Each value is computed by the same operation sequence whatever PARTS is, so
 // the record is bit-identical.
 template <typename TIn, int PARTS>
-__global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) void chunk_intra_kernel(ChunkParams p) {
+__global__ __launch_bounds__(256, sizeof(TIn) == 2 ? 5 : 1) void chunk_intra_kernel(ChunkParams p) {
   typedef RawOf<TIn> R;
   typedef RowStage<TIn> RS;
   __shared__ __align__(16) typename RS::T sK[64 * RS::kLd];  // K rows, raw
   __shared__ __align__(16) float sL[10 * 256];  // L blocks; diagonal blocks become T's
-  __shared__ __align__(16) float sT[6 * 256];   // off-diagonal T blocks
+  __shared__ __align__(16) float sT[3 * 256];   // T_21, T_31, T_32
   __shared__ __align__(16) float sG[64];   // gcum
   __shared__ __align__(16) float sB[64];   // beta
   __shared__ __align__(16) float sKS[64];  // Ks = e^{gL - gcum} ik
@@ -732,7 +740,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
       f4v x = {0.f, 0.f, 0.f, 0.f};
       for (int M = J; M < I; ++M) {
         const float4 a4 = *reinterpret_cast<const float4*>(&sL[blk(I, M) + li * 16 + 4 * lg]);
-        const float* tmj = (M == J) ? sL + blk(J, J) : sT + offblk(M, J);
+        const float* tmj = tblk(sL, sT, M, J);
 #pragma unroll
         for (int s = 0; s < 4; ++s) x = mfma4(elem(a4, s), tmj[(4 * lg + s) * 16 + li], x);
       }
@@ -740,8 +748,10 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
       f4v y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) y = mfma4(elem(a4, s), x[s], y);
+      // over L_I0 (J == 0: this wavefront read it last, above) or into sT
+      float* tij = (J == 0) ? sL + blk(I, 0) : sT + tslot(I, J);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sT[offblk(I, J) + (4 * lg + r) * 16 + li] = -y[r];
+      for (int r = 0; r < 4; ++r) tij[(4 * lg + r) * 16 + li] = -y[r];
     }
     __syncthreads();
   }
@@ -779,7 +789,7 @@ __global__ __launch_bounds__(256, sizeof(TIn) == 2 ? (PARTS == 1 ? 4 : 3) : 1) v
 #pragma unroll
       for (int u = 0; u <= J; ++u) {
         if (!((umask >> u) & 1u)) continue;
-        const float* tb = (u == J) ? sL + blk(J, J) : sT + offblk(J, u);
+        const float* tb = tblk(sL, sT, J, u);
 #pragma unroll
         for (int e = 0; e < 4; ++e) ak[u] = mfma4(tb[(4 * lg + e) * 16 + li], kb[e], ak[u]);
       }
