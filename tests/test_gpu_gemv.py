@@ -53,6 +53,19 @@ def test_matvec_order_lm_head_size(dev, oracle, order):
     assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16_order(W, x, order))
 
 
+@pytest.mark.parametrize("order", ["spans", "strided", "serial"])
+@pytest.mark.parametrize("out_dim,in_dim", [(131072, 512), (16384, 4096)])
+def test_matvec_order_128mb_edges(dev, oracle, order, out_dim, in_dim):
+    """128 MB, the smallest size on the streaming paths, at one and eight
+    16-byte pieces per lane of the span order (in_dim 512 and 4096)."""
+    from spock_amd import ops, synth
+    W = synth.gemv_weights(out_dim, in_dim, seed=in_dim + 7)
+    x = synth.gemv_input(in_dim, seed=in_dim + 8)
+    y = ops.matvec_f16_order(_t(dev, W), _t(dev, x), order)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), oracle.matvec_f16_order(W, x, order))
+
+
 def test_matvec_order_unaligned_and_cancellation(dev, oracle):
     """x and W 2-byte offset (the serial order's generic kernel), and rows
     that only one summation order sums exactly."""
