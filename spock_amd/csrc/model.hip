@@ -930,9 +930,9 @@ __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
 
 // One-launch form: the workgroups' keys go to one slot each (agent-scope
 // store, posted: no compute workgroup waits on a memory round trip), and one
-// extra workgroup -- the last id, so the last dispatched on its XCD -- polls
-// the slots until every one is filled, reduces them, clears them and records
-// the token.  A slot holds key + 1 (keys are below 2^64 - 1: the largest,
+// extra workgroup -- the last id, so the last dispatched -- polls the slots
+// until every one is filled (the early ones first, then the last few
+// thousand, take_slots), reduces them, clears them and records the token.  A slot holds key + 1 (keys are below 2^64 - 1: the largest,
 // +inf's, has 0xff800000 above), so 0 means "not written yet".  The poll is
 // bounded: after kTakePolls rounds (seconds) it gives up and records index
 // 0xffffffff, so the kernel always ends.
@@ -952,33 +952,58 @@ struct TakeArgs {
 // used: a poll is one memory round trip per 256 x kTakePer slots (read one
 // after the other, each waited for, a poll of 7,760 slots took ~30 loads'
 // latency).
-constexpr int kTakePer = 32;
+constexpr int kTakePer = 8;
+// The taker is dispatched last, when the first of the last few thousand
+// workgroups has finished: it reads (and, once all are seen written, clears)
+// the slots of every workgroup but the last 256 x kTakeTail while those still
+// run, then polls only those, kTakeTail per thread, one round trip a poll.
+// Every slot is cleared only after a poll has seen it written.
+constexpr int kTakeTail = 8;
 
-__device__ __forceinline__ void take_slots(const TakeArgs& t, uint32_t E) {
+// Polls slots [j_begin, j_end) until all are written (bounded); *best takes
+// their maximum.  Returns whether one was still missing when it gave up.
+template <int PER>
+__device__ __forceinline__ int take_range(const TakeArgs& t, int j_begin, int j_end, unsigned long long* best) {
   const int tid = threadIdx.x;
-  unsigned long long best = 0ull;
-  int missing = 1;
+  int missing = j_end > j_begin;
   for (int it = 0; it < kTakePolls && missing; ++it) {
-    best = 0ull;
+    unsigned long long b = 0ull;
     int miss = 0;
-    for (int j0 = 0; j0 < t.nblocks; j0 += 256 * kTakePer) {
-      unsigned long long v[kTakePer];
+    for (int j0 = j_begin; j0 < j_end; j0 += 256 * PER) {
+      unsigned long long v[PER];
 #pragma unroll
-      for (int i = 0; i < kTakePer; ++i)  // past the end: the last slot again
-        v[i] = __hip_atomic_load(t.slots + min(j0 + tid + 256 * i, t.nblocks - 1), __ATOMIC_RELAXED,
+      for (int i = 0; i < PER; ++i)  // past the end: the last slot of the range again
+        v[i] = __hip_atomic_load(t.slots + min(j0 + tid + 256 * i, j_end - 1), __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-      for (int i = 0; i < kTakePer; ++i) {
-        best = spk::umax64(best, v[i]);
+      for (int i = 0; i < PER; ++i) {
+        b = spk::umax64(b, v[i]);
         miss |= (v[i] == 0ull);
       }
     }
     missing = __syncthreads_or(miss);
-    if (missing) __builtin_amdgcn_s_sleep(2);
+    if (missing) {
+      __builtin_amdgcn_s_sleep(2);
+    } else {
+      *best = spk::umax64(*best, b);
+    }
   }
-  best = spk::block_max_u64<256>(best);
-  for (int j = tid; j < t.nblocks; j += 256)
+  return missing;
+}
+
+__device__ __forceinline__ void take_slots(const TakeArgs& t, uint32_t E) {
+  const int tid = threadIdx.x;
+  const int tail0 = max(t.nblocks - 256 * kTakeTail, 0);
+  unsigned long long best = 0ull;
+  // the early slots: read, then cleared while the last workgroups still run
+  int missing = take_range<kTakePer>(t, 0, tail0, &best);
+  for (int j = tid; j < tail0; j += 256)
     __hip_atomic_store(t.slots + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the last workgroups' slots
+  missing |= take_range<kTakeTail>(t, tail0, t.nblocks, &best);
+  for (int j = tail0 + tid; j < t.nblocks; j += 256)
+    __hip_atomic_store(t.slots + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  best = spk::block_max_u64<256>(best);
   if (tid == 0) {
     const uint32_t idx = missing ? 0xffffffffu : spk::key_to_index(best - 1ull, E);
     *t.out = idx;
