@@ -4,9 +4,8 @@
 // picks the width and the state-load kind from the batch (16 wavefronts and
 // plain loads when a handful of heads must carry the whole launch, 4
 // wavefronts and non-temporal loads when thousands of workgroups fill the
-// chip).  The
-// step itself (conv, L2, g/beta, recurrence, norm-gate; its reduction orders)
-// is spk_dn::dn_step in dn_step.hpp.
+// chip).  The step itself (conv, L2, g/beta, recurrence, norm-gate; its
+// reduction orders) is spk_dn::dn_step in dn_step.hpp.
 #include <stdlib.h>
 
 #include "capi_common.hpp"

@@ -2,11 +2,15 @@
 // standalone argmax.  All are HBM streams (weights read once); no MFMA.
 //
 // One wavefront per output row at a time, R rows in flight per wavefront.
-// Lane l reads the contiguous span [l*in/64, (l+1)*in/64) of the row with
-// 16-byte loads (in=1024: 2 x dwordx4 per lane, the wave covers the 2 KiB row),
-// accumulates fp16*fp16 products (exact in fp32) in span order, then the
-// 64-lane tree s[l] += s[l+stride] for stride 32..1 -- lm_head_tiled.comp:
-// 59-73's order -- and rounds once to fp16 (RNE).
+// Lane l sums the contiguous span [l*in/64, (l+1)*in/64) of the row
+// (fp16*fp16 products, exact in fp32, in span order), then the 64-lane tree
+// s[l] += s[l+stride] for stride 32..1 -- lm_head_tiled.comp:59-73's order --
+// and rounds once to fp16 (RNE).  Decode-sized matrices load each lane's span
+// directly with 16-byte loads (in=1024: 2 x dwordx4 per lane); the lm_head
+// and other matrices of hundreds of MB load rows densely (1 KiB of a row per
+// instruction) and regroup the pieces through LDS (dense_rows.hpp).
+// spk_matvec_f16_order adds the reference's two other orders, matvec.comp's
+// serial sum and matvec_tiled.comp's lane-strided one.
 //
 // Argmax keeps argmax.comp:27-63's exact result, including its tie rule, as
 // the 64-bit keys of argmax_key.hpp.
