@@ -51,6 +51,26 @@ def test_fused_decode_step_bitexact(dev, oracle, B):
     assert np.array_equal(gst.view(np.uint32), est.view(np.uint32))
 
 
+@pytest.mark.parametrize("nh,B", [(1, 1), (1, 300), (8, 1), (8, 40), (32, 8), (32, 9), (64, 4), (64, 5)])
+def test_fused_decode_step_other_head_counts(dev, oracle, nh, B):
+    """Head counts other than config 1's 16 (the C ABI takes 1..64), with the
+    launch-shape switches (16 -> 4 wavefronts above 256 workgroups,
+    non-temporal state loads from 256) reached through heads x batch."""
+    from spock_amd import ops, synth
+    print(f"[decode nh={nh} B={B}]", flush=True)
+    inp = synth.decode_inputs(B, seed=200 + nh + B, num_heads=nh)
+    inp["norm_w"] = np.random.default_rng(nh * 1000 + B).uniform(0.5, 1.5, 128).astype(np.float32)
+    layer = 3
+    eq, ecs, est = oracle.decode_step(inp, layer_idx=layer)
+    t = _dev_inputs(dev, inp)
+    ops.decode_step(t["qkv"], t["state"], t["conv_state"], t["conv_w"], t["a"], t["b"],
+                    t["a_log_bias"], t["z"], t["norm_w"], layer_idx=layer, num_heads=nh)
+    torch.cuda.synchronize()
+    assert np.array_equal(_u16(t["qkv"]), eq)
+    assert np.array_equal(_u16(t["conv_state"]), ecs)
+    assert np.array_equal(t["state"].cpu().numpy().view(np.uint32), est.view(np.uint32))
+
+
 def test_decode_two_steps_and_norm_weight(dev, oracle):
     """Two consecutive steps (state and conv history carried on the device), a
     non-trivial norm weight and a reference-style state stride with the 32-float
