@@ -65,6 +65,8 @@ def _check_cu_dev(cu_dev: torch.Tensor, cu_host: np.ndarray, dev) -> None:
     if len(_CU_CHECKED) > 64:
         _CU_CHECKED.clear()
     _CU_CHECKED[key] = True
+
+
 def chunk_workspace_bytes(num_heads: int, total_tokens: int, num_seqs: int = 1) -> int:
     return int(lib().spk_chunk_prefill_workspace_size(num_heads, total_tokens, num_seqs, CHUNK))
 
