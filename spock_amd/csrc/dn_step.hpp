@@ -265,7 +265,7 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
   }
   __syncthreads();
 
-  // rank-1 update, state write-back, output partials per 4-row group
+  // rank-1 update, output partials per 4-row group
   const float4 d4 = *reinterpret_cast<const float4*>(&s_delta[c4 * 4]);
 #pragma unroll
   for (int gq = 0; gq < G; ++gq) {
@@ -278,7 +278,6 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
       S[m].y = __builtin_fmaf(ki, d4.y, S[m].y);
       S[m].z = __builtin_fmaf(ki, d4.z, S[m].z);
       S[m].w = __builtin_fmaf(ki, d4.w, S[m].w);
-      *reinterpret_cast<float4*>(st_head + (rq * M + m) * 128 + c4 * 4) = S[m];
       op0 = __builtin_fmaf(S[m].x, qi, op0);
       op1 = __builtin_fmaf(S[m].y, qi, op1);
       op2 = __builtin_fmaf(S[m].z, qi, op2);
@@ -288,6 +287,12 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
   }
   __syncthreads();
 
+  // state write-back after the last barrier: issued before it, the 64 KiB of
+  // stores of a head held that barrier (and so the norm-gate) until the CU
+  // had taken them all; here they drain while wavefront 0 (the oldest, so
+  // its own stores issue first) runs the norm-gate
+#pragma unroll
+  for (int m = 0; m < M; ++m) *reinterpret_cast<float4*>(st_head + (rq * M + m) * 128 + c4 * 4) = S[m];
   if (wave == 0) {
     const float oa = tree32(s_part, lane);
     const float ob = tree32(s_part, lane + 64);
