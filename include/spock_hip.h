@@ -384,9 +384,11 @@ int spk_argmax_key_take(uint64_t* key, int32_t vocab, uint32_t* out_index, int32
  * writes *out_index (and the bookkeeping of spk_argmax_key_take when pos !=
  * NULL).  slots: slot_words >= spk_lm_head_take_slots(vocab) 64-bit words of
  * device memory that hold 0 before the call (the call leaves them at 0);
- * calls that overlap on one slot array race.  The poll is bounded: if the
- * slots are not all written within seconds (which only a corrupted slot
- * array can cause), *out_index is 0xffffffff. */
+ * calls that overlap on one slot array race.  The poll is bounded, so the
+ * kernel always ends: if the slots are not all written within seconds (the
+ * lm_head workgroups held off the GPU that long), *out_index is 0xffffffff,
+ * and slots written after the give-up stay set: zero the array again before
+ * the next call. */
 size_t spk_lm_head_take_slots(int32_t vocab);
 int spk_lm_head_argmax_take(const uint16_t* W, const uint16_t* x, const uint16_t* norm_w, int32_t vocab,
                             int32_t hidden, uint16_t* logits, uint64_t* slots, size_t slot_words,

@@ -957,7 +957,8 @@ constexpr int kTakePer = 8;
 // workgroups has finished: it reads (and, once all are seen written, clears)
 // the slots of every workgroup but the last 256 x kTakeTail while those still
 // run, then polls only those, kTakeTail per thread, one round trip a poll.
-// Every slot is cleared only after a poll has seen it written.
+// Every slot is cleared only after a poll has seen it written, except after
+// a give-up (index 0xffffffff), when slots still being written can stay set.
 constexpr int kTakeTail = 8;
 
 // Polls slots [j_begin, j_end) until all are written (bounded); *best takes
