@@ -62,6 +62,14 @@ __device__ __forceinline__ float tree32(const float (*part)[128], int col) {
   return v[0];
 }
 
+// A value the compiler cannot see through (an empty asm that defines a
+// VGPR): the starting value of an operand that only some waves load.
+__device__ __forceinline__ uint32_t opaque_u32() {
+  uint32_t v;
+  asm volatile("" : "=v"(v));
+  return v;
+}
+
 // CONV: run the conv/L2 phase.  REC: run the recurrence.  GB_TAIL: g/beta from
 // the state tail (deltanet_recurrent.comp) instead of a/b/A_log/dt_bias.
 // NORM_GATE: RMSNorm-gate the output (else fp16 of the raw output).
@@ -90,18 +98,29 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
   const int c4 = tid & 31;  // owns columns 4*c4 .. 4*c4+3
   const int rq = tid >> 5;  // owns row groups G*rq .. G*rq+G-1, i.e. rows M*rq .. M*rq+M-1
   // Load order: the conv operands, then the small g/beta and norm-gate
-  // operands, then the state, all without a branch (a branch around a load
-  // makes the compiler wait for the loads before it).  A wave's loads return
-  // in issue order, so the conv waves start on their operands while the
-  // state stream is still in flight, and no later phase waits on a memory
-  // round trip of its own.  Waves 3.. load a copy of the V block's conv
-  // operands (cache hits, unused) so that the loads need no branch.
-  uint2 olds[2] = {}, wvs[2] = {};
-  uint16_t xs[2] = {0, 0};
+  // operands, then the state.  A wave's loads return in issue order, so the
+  // conv waves start on their operands while the state stream is still in
+  // flight, and no later phase waits on a memory round trip of its own.  Each
+  // small operand is loaded only by the wave that uses it (wave-uniform
+  // branches; nothing loaded is merged with another value at a join, which
+  // would make the compiler wait for the load there): all of a CU's loads go
+  // through one memory pipe, and a head's batch-1 step is bound by how fast
+  // that pipe takes them.
+  // values a wave does not load are left unspecified (opaque_u32), not 0: a
+  // constant on the other side of the branch lets the compiler fold the
+  // conversions into the loading block, where they would wait for the loads
+  uint2 olds[2], wvs[2];
+  uint32_t xs[2];  // fp16 bits, one per register (a packed pair would be merged at the join)
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    olds[half] = make_uint2(opaque_u32(), opaque_u32());
+    wvs[half] = make_uint2(opaque_u32(), opaque_u32());
+    xs[half] = opaque_u32();
+  }
   const int conv_blk = wave < 3 ? wave : 2;  // wave 0: Q block, 1: K block, 2: V block
   const int ch0 = conv_blk * nh * 128 + h * 128;
   uint16_t* cs_seq = CONV ? p.conv_state + (long long)seq * p.conv_stride : nullptr;
-  if (CONV) {
+  if (CONV && wave < 3) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int ch = ch0 + lane + 64 * half;
@@ -110,16 +129,18 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
       xs[half] = qkv[ch];
     }
   }
-  uint16_t a16 = 0, b16 = 0;
-  float a_log = 0.0f, dt_bias = 0.0f, g_tail = 0.0f, beta_tail = 0.0f;
-  uint16_t z16[2] = {0, 0};
-  float nw[2] = {0.0f, 0.0f};
+  constexpr int kSiluWave = WAVES > 4 ? 4 : 3;  // forms SiLU(z) during the conv phase
+  uint16_t a16 = (uint16_t)opaque_u32(), b16 = (uint16_t)opaque_u32();
+  float a_log = __uint_as_float(opaque_u32()), dt_bias = __uint_as_float(opaque_u32());
+  float g_tail = 0.0f, beta_tail = 0.0f;
+  uint16_t z16[2] = {(uint16_t)opaque_u32(), (uint16_t)opaque_u32()};
+  float nw[2] = {__uint_as_float(opaque_u32()), __uint_as_float(opaque_u32())};
   if (REC) {
     if (GB_TAIL) {
       const float* tail = p.state + (long long)seq * p.state_stride + (long long)nh * 128 * 128;
       g_tail = tail[h];
       beta_tail = tail[nh + h];
-    } else {
+    } else if (wave == 3) {
       if constexpr (AB_IN) {
         a16 = a_in;
         b16 = b_in;
@@ -130,10 +151,12 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
       a_log = p.alb[(p.layer * nh + h) * 2];
       dt_bias = p.alb[(p.layer * nh + h) * 2 + 1];
     }
-    if (NORM_GATE) {  // z: the SiLU wave (into s_zs); norm weights: wave 0
+    if (NORM_GATE && wave == kSiluWave) {
       const uint16_t* zr = p.z + (long long)seq * p.z_stride + h * 128;
       z16[0] = zr[lane];
       z16[1] = zr[lane + 64];
+    }
+    if (NORM_GATE && wave == 0) {
       nw[0] = p.norm_w[lane];
       nw[1] = p.norm_w[lane + 64];
     }
@@ -165,7 +188,7 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
       s_gb[1] = 1.0f / (1.0f + spk::expf_det(-bv));
     }
   }
-  if (REC && NORM_GATE && wave == (WAVES > 4 ? 4 : 3)) {
+  if (REC && NORM_GATE && wave == kSiluWave) {
     // the gate's SiLU(z) depends on nothing the step computes: an idle wave
     // (wave 4; wave 3 beside g/beta when there are only four) forms it while
     // waves 0-2 run the conv, so the output phase only reads it
@@ -181,7 +204,7 @@ __device__ __forceinline__ void dn_step(const DecodeParams& p, int h, int seq, u
         uint2* csp = reinterpret_cast<uint2*>(cs_seq + ch * 4);
         const uint2 old = olds[half];
         const uint2 wv = wvs[half];
-        const uint16_t x = xs[half];
+        const uint16_t x = (uint16_t)xs[half];
         // shifted window (conv_l2_qk.comp:48-58): [old1, old2, old3, x]
         const uint16_t s0 = (uint16_t)(old.x >> 16);
         const uint16_t s1 = (uint16_t)(old.y & 0xffffu);
