@@ -1220,13 +1220,30 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
     const int tk = s.token[0];
     hsrc += (size_t)((tk >= 0 && tk < s.token_rows) ? tk : 0) * kHidden;
   }
+  // Each operand is loaded only by the wavefronts that use it (the CU's
+  // memory pipe takes one wavefront load instruction at a time, whatever its
+  // width): the norm input by the 256 threads of the norm prologue, the a/b
+  // rows by wavefront 0 (the last workgroup's uses them).  Values a wavefront
+  // skips start opaque (spk_dn::opaque_u32), so no load meets a constant at
+  // a branch join, where the compiler would wait for it.
   const int t4 = 4 * (tid & 255);
-  const uint2 hv = *reinterpret_cast<const uint2*>(hsrc + t4);
-  const uint2 nwv = *reinterpret_cast<const uint2*>(s.norm_w + t4);
+  uint2 hv = make_uint2(spk_dn::opaque_u32(), spk_dn::opaque_u32());
+  uint2 nwv = make_uint2(spk_dn::opaque_u32(), spk_dn::opaque_u32());
+  if (tid < 256) {
+    hv = *reinterpret_cast<const uint2*>(hsrc + t4);
+    nwv = *reinterpret_cast<const uint2*>(s.norm_w + t4);
+  }
   uint4 wv[2][2], wab[2][2];
   load_rows<2, 2>(W, row, row + 2, lane, wv);
-  load_rows<2, 1>(s.Wa, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[0]));
-  load_rows<2, 1>(s.Wb, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[1]));
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      wab[i][k] = make_uint4(spk_dn::opaque_u32(), spk_dn::opaque_u32(), spk_dn::opaque_u32(), spk_dn::opaque_u32());
+  if (wave == 0) {
+    load_rows<2, 1>(s.Wa, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[0]));
+    load_rows<2, 1>(s.Wb, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[1]));
+  }
   // the head's step operands into this XCD's L2 for the last workgroup: a
   // share of the 64 KiB state and one of the six 1 KiB conv rows (state q|k|v,
   // weights q|k|v)
