@@ -501,12 +501,19 @@ __global__ __launch_bounds__(256) void attn_blocks_kernel(AttnArgs a) {
   // with the first operands, so the last workgroup's combine waits on no
   // load of its own after the partials)
   if constexpr (COMBINE) load4h(a.qg + qh * 512 + 256 + 4 * lane, gv);
-  // the new K/V row is read by every wave (a few hundred bytes) so that no
-  // load sits under a branch; only the block holding the position uses it
+  // the new K/V row, by the one wavefront that stores it (wavefront 0 of the
+  // block holding the position); elsewhere the values start opaque, so no
+  // load meets a constant at the branch join (the compiler would wait for it
+  // there)
   const bool newrow = cur >= 0 && wave == 0;
-  const uint2 nk16 = *reinterpret_cast<const uint2*>(a.k + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
-  const uint2 kw16 = *reinterpret_cast<const uint2*>(a.k_norm_w + 4 * lane);
-  const uint2 vb = *reinterpret_cast<const uint2*>(a.v + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
+  uint2 nk16 = make_uint2(spk_dn::opaque_u32(), spk_dn::opaque_u32());
+  uint2 kw16 = make_uint2(spk_dn::opaque_u32(), spk_dn::opaque_u32());
+  uint2 vb = make_uint2(spk_dn::opaque_u32(), spk_dn::opaque_u32());
+  if (newrow) {
+    nk16 = *reinterpret_cast<const uint2*>(a.k + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
+    kw16 = *reinterpret_cast<const uint2*>(a.k_norm_w + 4 * lane);
+    vb = *reinterpret_cast<const uint2*>(a.v + (size_t)t * 512 + kvh * kHeadDim + 4 * lane);
+  }
   const int p = tid >> 2, q4 = tid & 3;
   const int gp = kAttnBlock * b + p;
   const bool live = gp < npos && p != cur;
