@@ -1251,15 +1251,27 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
     load_rows<2, 1>(s.Wa, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[0]));
     load_rows<2, 1>(s.Wb, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[1]));
   }
-  // the head's step operands into this XCD's L2 for the last workgroup: a
-  // share of the 64 KiB state and one of the six 1 KiB conv rows (state q|k|v,
-  // weights q|k|v)
-  constexpr int kStateShare = 16384 / kPieces;  // floats per workgroup
-  const float4 tst = *reinterpret_cast<const float4*>(s.dp.state + (size_t)h * 16384 + piece * kStateShare +
-                                                      (wave % (kStateShare / 256)) * 256 + 4 * lane);
-  const int creg = (piece + wave) % 6;
-  const uint16_t* cbase = creg < 3 ? s.dp.conv_state : s.dp.conv_w;
-  const float4 tcv = *reinterpret_cast<const float4*>(cbase + ((creg % 3) * 2048 + h * 128) * 4 + 8 * lane);
+  // the head's step operands into this XCD's L2 for the last workgroup, one
+  // 128-byte line per lane of wavefront 0: lanes 0-15 the workgroup's 16
+  // lines (2 KiB) of the head's 64 KiB state, lanes 16-17 two of the 48 lines
+  // of its six 1 KiB conv rows (state q|k|v, weights q|k|v), spread over the
+  // head's first 24 workgroups
+  static_assert(kPieces * 16 * 128 == 16384 * 4, "16 state lines per workgroup");
+  uint32_t touch = spk_dn::opaque_u32();
+  {
+    const int cl = 2 * piece + (lane - 16);  // conv line of lanes 16, 17
+    if (wave == 0 && (lane < 16 || (lane < 18 && cl < 48))) {
+      const char* tp;
+      if (lane < 16) {
+        tp = reinterpret_cast<const char*>(s.dp.state + (size_t)h * 16384) + (size_t)(16 * piece + lane) * 128;
+      } else {
+        const int row = cl >> 3;
+        const uint16_t* cbase = row < 3 ? s.dp.conv_state : s.dp.conv_w;
+        tp = reinterpret_cast<const char*>(cbase + ((row % 3) * 2048 + h * 128) * 4) + (cl & 7) * 128;
+      }
+      touch = *reinterpret_cast<const uint32_t*>(tp);
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue
   {
     const float v[4] = {spk::h2f(hv.x & 0xffffu), spk::h2f(hv.x >> 16), spk::h2f(hv.y & 0xffffu),
@@ -1309,7 +1321,7 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
 
   // arrival: this workgroup's row stores (and the L2 touches) complete, then
   // one count per workgroup
-  asm volatile("" ::"v"(tst.x), "v"(tcv.x));
+  asm volatile("" ::"v"(touch));
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0)
