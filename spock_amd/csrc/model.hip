@@ -50,25 +50,21 @@ __device__ __forceinline__ void unpack8(const uint4& u, float* f) {
 
 __device__ __forceinline__ float round16(float v) { return spk::h2f(spk::f2h(v)); }
 
-// Sum of 256 per-thread partials in the rms_norm.comp tree order; every thread
-// of the 256-thread block gets the result.  `red` is 256 floats of LDS.
+// Sum of the partials of threads 0..255 in the rms_norm.comp tree order
+// (s[t] += s[t+128], += s[t+64], then strides 32..1); every thread of the
+// block (256 or more threads) gets the result.  `red` is 256 floats of LDS.
 __device__ __forceinline__ float block_tree256(float p, float* red) {
   const int t = threadIdx.x;
-  red[t] = p;
+  if (t < 256) red[t] = p;
   __syncthreads();
-  if (t < 128) red[t] = red[t] + red[t + 128];
-  __syncthreads();
-  if (t < 64) red[t] = red[t] + red[t + 64];
-  __syncthreads();
-  if (t < 64) {
-    float v = red[t];
-    v = spk::tree64_to_lane0(v);
-    if (t == 0) red[256] = v;
-  }
-  __syncthreads();
-  const float r = red[256];
-  __syncthreads();
-  return r;
+  // every wavefront takes the first two levels (strides 128 and 64) for its
+  // lane l from four LDS reads -- (p[l] + p[l+128]) + (p[l+64] + p[l+192]),
+  // the tree's own pairs -- and the last six in registers: one barrier
+  // instead of one per level.  red must not be written again in the kernel.
+  const int l = t & 63;
+  const float v = (red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]);
+  const float s = spk::tree64_to_lane0(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
 }
 
 // ---------------------------------------------------------------------------
@@ -1281,20 +1277,8 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
     float pp = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) pp = __builtin_fmaf(v[i], v[i], pp);
-    // rms_norm.comp's 256-partial tree (block_tree256 for 256 threads)
-    if (tid < 256) red[tid] = pp;
-    __syncthreads();
-    if (tid < 128) red[tid] = red[tid] + red[tid + 128];
-    __syncthreads();
-    if (tid < 64) red[tid] = red[tid] + red[tid + 64];
-    __syncthreads();
-    if (tid < 64) {
-      float t = red[tid];
-      t = spk::tree64_to_lane0(t);
-      if (tid == 0) red[256] = t;
-    }
-    __syncthreads();
-    const float sum = red[256];
+    // rms_norm.comp's 256-partial tree over the first 256 threads' partials
+    const float sum = block_tree256(pp, red);
     const float nf = 1.0f / __builtin_sqrtf(sum / 1024.0f + 1e-6f);
     if (tid < 256) {
 #pragma unroll
