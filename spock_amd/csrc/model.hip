@@ -1203,7 +1203,6 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
   __shared__ float xs[kHidden];
   __shared__ float red[257];
   __shared__ int last;
-  __shared__ uint16_t ab[2];
   const int id = blockIdx.x;
   const int h = (id & 7) + 8 * ((id >> 3) & 1);
   const int piece = id >> 4;
@@ -1226,7 +1225,8 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
   // Each operand is loaded only by the wavefronts that use it (the CU's
   // memory pipe takes one wavefront load instruction at a time, whatever its
   // width): the norm input by the 256 threads of the norm prologue, the a/b
-  // rows by wavefront 0 (the last workgroup's uses them).  Values a wavefront
+  // rows by wavefront 3 (the last workgroup's forms a and b and, as the
+  // step's g/beta wavefront, uses them).  Values a wavefront
   // skips start opaque (spk_dn::opaque_u32), so no load meets a constant at
   // a branch join, where the compiler would wait for it.
   const int t4 = 4 * (tid & 255);
@@ -1243,7 +1243,7 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
       wab[i][k] = make_uint4(spk_dn::opaque_u32(), spk_dn::opaque_u32(), spk_dn::opaque_u32(), spk_dn::opaque_u32());
-  if (wave == 0) {
+  if (wave == 3) {
     load_rows<2, 1>(s.Wa, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[0]));
     load_rows<2, 1>(s.Wb, h, h + 1, lane, *reinterpret_cast<uint4(*)[1][2]>(&wab[1]));
   }
@@ -1314,19 +1314,20 @@ __global__ __launch_bounds__(NW * 64) void dn_inproj_step_kernel(InprojStep s) {
   __syncthreads();
   if (!last) return;
   if (tid == 0) __hip_atomic_store(s.arrive + h * kDnArriveStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // a[h] and b[h] (wavefront 0), the projections' order
-  if (wave == 0) {
+  // a[h] and b[h] (the projections' order) by wavefront 3, the step's g/beta
+  // wavefront, which alone reads them (in lane 0): no barrier before the step
+  uint16_t a_h = 0, b_h = 0;
+  if (wave == 3) {
     float t[2] = {lane_dot<2>(wab[0], xf), lane_dot<2>(wab[1], xf)};
     spk::tree64_rows<2>(t);
+    a_h = spk::f2h(t[0]);
+    b_h = spk::f2h(t[1]);
     if (lane == 0) {
-      ab[0] = spk::f2h(t[0]);
-      ab[1] = spk::f2h(t[1]);
-      s.a[h] = ab[0];
-      s.b[h] = ab[1];
+      s.a[h] = a_h;
+      s.b[h] = b_h;
     }
   }
-  __syncthreads();
-  spk_dn::dn_step<true, true, false, true, NW, true>(s.dp, h, 0, ab[0], ab[1]);
+  spk_dn::dn_step<true, true, false, true, NW, true>(s.dp, h, 0, a_h, b_h);
 }
 
 }  // namespace
